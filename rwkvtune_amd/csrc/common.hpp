@@ -1,0 +1,126 @@
+// Shared device helpers for the gfx950 WKV7 kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define RWKV7_HEAD 64  // head size N; the reference hard-codes it too (model.py:507-508)
+
+typedef uint16_t bf16_t;  // raw bfloat16 bits
+typedef _Float16 f16_t;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Scalar conversions (round-to-nearest-even, like at::BFloat16 / at::Half).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(bf16_t x) {
+    return __uint_as_float(((uint32_t)x) << 16);
+}
+
+__device__ __forceinline__ bf16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)0x7fc0;  // NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (bf16_t)(u >> 16);
+}
+
+template <typename IO> struct io_traits;
+
+template <> struct io_traits<float> {
+    static __device__ __forceinline__ float to_f32(float x) { return x; }
+    static __device__ __forceinline__ float from_f32(float x) { return x; }
+    // 4 consecutive elements starting at p (16-byte aligned)
+    static __device__ __forceinline__ f32x4 load4(const float* p) {
+        return *reinterpret_cast<const f32x4*>(p);
+    }
+};
+
+template <> struct io_traits<bf16_t> {
+    static __device__ __forceinline__ float to_f32(bf16_t x) { return bf16_to_f32(x); }
+    static __device__ __forceinline__ bf16_t from_f32(float x) { return f32_to_bf16(x); }
+    static __device__ __forceinline__ f32x4 load4(const bf16_t* p) {
+        uint2 u = *reinterpret_cast<const uint2*>(p);
+        f32x4 o;
+        o.x = __uint_as_float(u.x << 16);
+        o.y = __uint_as_float(u.x & 0xffff0000u);
+        o.z = __uint_as_float(u.y << 16);
+        o.w = __uint_as_float(u.y & 0xffff0000u);
+        return o;
+    }
+};
+
+template <> struct io_traits<f16_t> {
+    static __device__ __forceinline__ float to_f32(f16_t x) { return (float)x; }
+    static __device__ __forceinline__ f16_t from_f32(float x) { return (f16_t)x; }
+    static __device__ __forceinline__ f32x4 load4(const f16_t* p) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        h4 h = *reinterpret_cast<const h4*>(p);
+        f32x4 o;
+        o.x = (float)h.x; o.y = (float)h.y; o.z = (float)h.z; o.w = (float)h.w;
+        return o;
+    }
+};
+
+// ---------------------------------------------------------------------------
+// DPP lane exchanges inside a 16-lane row.  All of these read from a lane of
+// the same row, so every source lane is valid.
+//   row_mirror       lane c <- lane 15-c   (= c ^ 15)
+//   row_half_mirror  lane c <- lane 7-c within each 8  (= c ^ 7)
+//   quad_perm 2301   lane c <- c ^ 2
+//   quad_perm 1032   lane c <- c ^ 1
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float dpp_xor15(float x) {
+    return __builtin_amdgcn_update_dpp(0.0f, x, 0x140, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float dpp_xor7(float x) {
+    return __builtin_amdgcn_update_dpp(0.0f, x, 0x141, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float dpp_xor2(float x) {
+    return __builtin_amdgcn_update_dpp(0.0f, x, 0x4e, 0xf, 0xf, false);
+}
+__device__ __forceinline__ float dpp_xor1(float x) {
+    return __builtin_amdgcn_update_dpp(0.0f, x, 0xb1, 0xf, 0xf, false);
+}
+
+// Reduce-scatter over the 16 lanes of a DPP row.  Every lane of the row holds
+// 16 partial sums p[0..15]; on return, lane c of the row holds
+// sum over the row's 16 lanes of p[c].  The four butterfly partners
+// (c^15, c^7, c^2, c^1) flip bits 3, 2, 1, 0 of c in turn and together span all
+// 16 lanes; at each stage a lane keeps the half of its remaining values whose
+// index bit equals its own lane bit and sends the other half.
+__device__ __forceinline__ float row16_reduce_scatter(const float (&p)[16], int c) {
+    float q8[8];
+    const bool b3 = (c >> 3) & 1;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        float keep = b3 ? p[8 + k] : p[k];
+        float send = b3 ? p[k] : p[8 + k];
+        q8[k] = keep + dpp_xor15(send);
+    }
+    float q4[4];
+    const bool b2 = (c >> 2) & 1;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        float keep = b2 ? q8[4 + k] : q8[k];
+        float send = b2 ? q8[k] : q8[4 + k];
+        q4[k] = keep + dpp_xor7(send);
+    }
+    float q2[2];
+    const bool b1 = (c >> 1) & 1;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        float keep = b1 ? q4[2 + k] : q4[k];
+        float send = b1 ? q4[k] : q4[2 + k];
+        q2[k] = keep + dpp_xor2(send);
+    }
+    const bool b0 = c & 1;
+    float keep = b0 ? q2[1] : q2[0];
+    float send = b0 ? q2[0] : q2[1];
+    return keep + dpp_xor1(send);
+}
+
+__device__ __forceinline__ float fast_dot4(f32x4 a, f32x4 b) {
+    return fmaf(a.x, b.x, fmaf(a.y, b.y, fmaf(a.z, b.z, a.w * b.w)));
+}

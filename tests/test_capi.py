@@ -1,0 +1,79 @@
+"""CPU checks of the C ABI: the library loads, exports exactly what the header
+declares, and rejects bad arguments on the host (no kernel is launched)."""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from rwkvtune_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "rwkv7_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rwkv7\w*)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        pytest.fail("librwkv7_hip.so is not built (run python -m rwkvtune_amd.build)")
+    return _lib.load()
+
+
+def test_header_matches_exports(lib):
+    decl = declared_functions()
+    assert decl, "no functions parsed from the header"
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = sorted(set(re.findall(r"\sT\s(rwkv7\w*)$", out, flags=re.M)))
+    assert exported == decl
+    assert sorted(_lib.SIGNATURES) == decl
+    for name in decl:
+        assert getattr(lib, name) is not None
+
+
+def test_abi_version(lib):
+    assert lib.rwkv7_abi_version() == 1
+
+
+def _null6():
+    return [None] * 6
+
+
+def test_host_side_errors(lib):
+    P = ctypes.c_void_p
+    fake = P(16)  # never dereferenced: every call below fails before any launch
+    # bad dtype
+    rc = lib.rwkv7s_forward(7, 1, 1, 64, 1, fake, *[fake] * 6, fake, None)
+    assert rc == 1 and b"dtype" in lib.rwkv7_last_error()
+    # C != H*64 (a host assert in the reference kernel launcher)
+    rc = lib.rwkv7s_forward(2, 1, 1, 96, 1, fake, *[fake] * 6, fake, None)
+    assert rc == 1 and b"H*64" in lib.rwkv7_last_error()
+    # null pointer
+    rc = lib.rwkv7s_forward(2, 1, 1, 64, 1, None, *[fake] * 6, fake, None)
+    assert rc == 1 and b"null" in lib.rwkv7_last_error()
+    # empty problems succeed without touching the GPU
+    assert lib.rwkv7s_forward(2, 0, 5, 64, 1, None, *_null6(), None, None) == 0
+    assert lib.rwkv7_last_error() == b""
+    assert lib.rwkv7_wkv_decode(2, 0, 1, None, 0, None, *_null6(), None, None) == 0
+    # identity slots need a pool at least as large as the batch
+    rc = lib.rwkv7_wkv_decode(2, 4, 1, fake, 2, None, *[fake] * 6, fake, None)
+    assert rc == 1 and b"pool_slots" in lib.rwkv7_last_error()
+    # prefill: chunk length outside {0,16,32,64}; missing cu_seqlens
+    rc = lib.rwkv7_wkv_prefill(2, 1, 1, 4, fake, None, fake, 1, *[fake] * 6, fake, 48, None)
+    assert rc == 1 and b"chunk_len" in lib.rwkv7_last_error()
+    rc = lib.rwkv7_wkv_prefill(2, 1, 1, 4, None, None, fake, 1, *[fake] * 6, fake, 0, None)
+    assert rc == 1 and b"cu_seqlens" in lib.rwkv7_last_error()
+
+
+def test_python_wrapper_raises_library_message(lib):
+    with pytest.raises(ValueError, match="bad dtype"):
+        _lib.call("rwkv7s_forward", 9, 1, 1, 64, 1, ctypes.c_void_p(16),
+                  *[ctypes.c_void_p(16)] * 7, None)

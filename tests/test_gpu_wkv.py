@@ -1,0 +1,193 @@
+"""GPU parity of the WKV7 decode / token-serial kernels against the fp64 oracle.
+
+Tolerances (stated once, used everywhere below):
+  y      bf16/fp16 I/O: ||y - round(y_ref)|| / ||round(y_ref)|| <= 1e-3 over the whole
+         output, where round() is the I/O type's rounding of the fp64 oracle (the
+         reference kernel also returns y in the I/O type, wkv7s.cu:49); and every
+         element is a faithful rounding up to fp32 accumulation error:
+         |y - y_ref| <= 1 ulp of the I/O type at y_ref + 1e-5 * rms(y_ref).
+         (A per-(slot, head) norm is not used for bf16: one legitimate
+         rounding flip of a head's largest element already costs ~1e-3 of that head.)
+         fp32 I/O: per (slot, head) ||y - y_ref|| / ||y_ref|| <= 1e-5.
+  state  fp32: per (slot, head) ||S - S_ref|| / ||S_ref|| <= 1e-4.
+"""
+
+import pytest
+import torch
+
+from oracle.wkv7 import wkv7_ragged, wkv7_rowwise
+from rwkvtune_amd import operators as ops
+from rwkvtune_amd.workloads import cu_seqlens_of, ragged_lengths, wkv_inputs, wkv_state
+
+pytestmark = pytest.mark.gpu
+
+N = 64
+Y_TOL = {torch.bfloat16: 1e-3, torch.float16: 1e-3, torch.float32: 1e-5}
+S_TOL = 1e-4
+
+
+def per_head_rel(x, ref, H):
+    """max over (row, head) of ||x - ref|| / ||ref|| on [..., H*N] tensors."""
+    x = x.double().reshape(-1, H, N)
+    ref = ref.double().reshape(-1, H, N)
+    num = (x - ref).norm(dim=-1)
+    den = ref.norm(dim=-1).clamp_min(1e-30)
+    return float((num / den).max())
+
+
+def state_rel(S, ref):
+    S = S.double().reshape(-1, N * N)
+    ref = ref.double().reshape(-1, N * N)
+    return float(((S - ref).norm(dim=-1) / ref.norm(dim=-1).clamp_min(1e-30)).max())
+
+
+MANT_BITS = {torch.bfloat16: 7, torch.float16: 10}
+
+
+def ulp(x, dtype):
+    e = torch.floor(torch.log2(x.abs().clamp_min(1e-30)))
+    if dtype == torch.float16:
+        e = e.clamp_min(-14)
+    return torch.pow(2.0, e - MANT_BITS[dtype])
+
+
+def check_y(y_gpu, y_ref64, H, dtype):
+    y = y_gpu.cpu().double()
+    if dtype == torch.float32:
+        rel = per_head_rel(y, y_ref64, H)
+        assert rel <= Y_TOL[dtype], f"y per-head rel err {rel:.3e}"
+        return rel
+    ref = y_ref64.to(dtype).double()
+    rel = float((y - ref).norm() / ref.norm())
+    assert rel <= Y_TOL[dtype], f"y rel err {rel:.3e}"
+    atol = 1e-5 * float(y_ref64.pow(2).mean().sqrt())
+    bad = (y - y_ref64).abs() > ulp(y_ref64, dtype) * 1.0001 + atol
+    assert not bool(bad.any()), f"{int(bad.sum())} elements not faithfully rounded"
+    return rel
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_decode_cfg2_shape(gpu_device, dtype):
+    """Isolated decode step at the benchmark shape: B=256 slots, H=32."""
+    B, H = 256, 32
+    print(f"[case] decode B={B} H={H} dtype={dtype}", flush=True)
+    inp = wkv_inputs((B,), H, N, seed=100, dtype=dtype)
+    S0 = wkv_state(B, H, N, seed=101)
+    y_ref, S_ref = wkv7_rowwise(*(t.unsqueeze(1) for t in inp.as_tuple()), N, S0)
+    pool = S0.to(gpu_device)
+    g = inp.to(gpu_device)
+    y = ops.wkv7_decode(pool, None, *g.as_tuple())
+    torch.cuda.synchronize()
+    check_y(y, y_ref[:, 0], H, dtype)
+    assert state_rel(pool.cpu(), S_ref) <= S_TOL
+
+
+def test_decode_slot_table_and_skip(gpu_device):
+    """Rows address pool slots through slot_idx; negative slots are skipped."""
+    B, H, S = 6, 4, 9
+    print("[case] decode slot table", flush=True)
+    inp = wkv_inputs((B,), H, N, seed=102)
+    pool0 = wkv_state(S, H, N, seed=103)
+    slots = [7, 0, -1, 3, 8, 2]
+    pool = pool0.to(gpu_device)
+    sidx = torch.tensor(slots, dtype=torch.int32, device=gpu_device)
+    y = torch.full((B, H * N), 7.0, dtype=torch.bfloat16, device=gpu_device)
+    ops.wkv7_decode(pool, sidx, *inp.to(gpu_device).as_tuple(), y=y)
+    torch.cuda.synchronize()
+    pool = pool.cpu()
+    y = y.cpu()
+    for i, s in enumerate(slots):
+        if s < 0:
+            assert torch.all(y[i] == 7.0)
+            continue
+        yr, Sr = wkv7_rowwise(*(t[i:i + 1, None] for t in inp.as_tuple()), N, pool0[s:s + 1])
+        check_y(y[i:i + 1], yr[:, 0], H, torch.bfloat16)
+        assert state_rel(pool[s:s + 1], Sr) <= S_TOL
+    used = {s for s in slots if s >= 0}
+    for s in range(S):
+        if s not in used:
+            assert torch.equal(pool[s], pool0[s])
+
+
+def test_repeated_decode_steps_long(gpu_device):
+    """1000 consecutive decode steps on a small batch track the fp64 oracle."""
+    B, H, T = 2, 2, 1000
+    print("[case] 1000 decode steps", flush=True)
+    inp = wkv_inputs((B, T), H, N, seed=104)
+    S0 = wkv_state(B, H, N, seed=105)
+    y_ref, S_ref = wkv7_rowwise(*inp.as_tuple(), N, S0)
+    pool = S0.to(gpu_device)
+    g = inp.to(gpu_device)
+    ys = []
+    for t in range(T):
+        ys.append(ops.wkv7_decode(pool, None, *(x[:, t] for x in g.as_tuple())))
+    y = torch.stack(ys, 1)
+    torch.cuda.synchronize()
+    check_y(y, y_ref, H, torch.bfloat16)
+    assert state_rel(pool.cpu(), S_ref) <= S_TOL
+
+
+def test_cfg2_1000_steps_linearity(gpu_device):
+    """At the full cfg2 shape, 1000 steps: the map (S0, v) -> (S_T, y) is linear
+    for fixed r, w, k, a, b, so scaling S0 and v by 2^-3 scales every output by
+    exactly 2^-3 (bit-exact in fp32 arithmetic; y compared before bf16 rounding
+    via fp32 I/O)."""
+    B, H, T = 256, 32, 1000
+    print("[case] cfg2 1000 steps linearity", flush=True)
+    g = wkv_inputs((B,), H, N, seed=106, dtype=torch.float32).to(gpu_device)
+    S0 = wkv_state(B, H, N, seed=107).to(gpu_device)
+    pa = S0.clone()
+    pb = (S0 * 0.125).contiguous()
+    vb = g.v * 0.125
+    for _ in range(T):
+        ya = ops.wkv7_decode(pa, None, g.r, g.w, g.k, g.v, g.a, g.b)
+        yb = ops.wkv7_decode(pb, None, g.r, g.w, g.k, vb, g.a, g.b)
+    torch.cuda.synchronize()
+    assert torch.isfinite(pa).all()
+    assert torch.equal(pa * 0.125, pb)
+    assert torch.equal(ya * 0.125, yb)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_ragged_prefill_token_serial(gpu_device, dtype):
+    H = 4
+    lens = [1, 0, 37, 5, 64, 130]
+    print(f"[case] ragged prefill {lens} dtype={dtype}", flush=True)
+    cu = cu_seqlens_of(lens)
+    inp = wkv_inputs((cu[-1],), H, N, seed=108, dtype=dtype)
+    pool0 = wkv_state(8, H, N, seed=109)
+    slots = [5, 1, 0, 7, 2, 6]
+    y_ref, fin = wkv7_ragged(*inp.as_tuple(), cu, states=pool0[slots])
+    pool = pool0.to(gpu_device)
+    y = ops.wkv7_prefill(pool, torch.tensor(slots, dtype=torch.int32, device=gpu_device),
+                         torch.tensor(cu, dtype=torch.int32, device=gpu_device),
+                         *inp.to(gpu_device).as_tuple())
+    torch.cuda.synchronize()
+    check_y(y, y_ref, H, dtype)
+    assert state_rel(pool.cpu()[slots], fin) <= S_TOL
+    assert torch.equal(pool.cpu()[[3, 4]], pool0[[3, 4]])
+
+
+def test_reference_operator_contract(gpu_device):
+    """load_wkv_operator('cuda', for_inference=True) behaves like RUN_CUDA_RWKV7S."""
+    op = ops.load_wkv_operator(device="cuda", for_inference=True, head_size=64)
+    assert op is ops.load_wkv7_operator("cuda", True, 64)
+    H, T = 2, 9
+    inp = wkv_inputs((T,), H, N, seed=110).to(gpu_device)
+    with pytest.raises(ValueError):
+        op(*inp.as_tuple())
+    with pytest.raises(RuntimeError):
+        op(*(t[None, None] for t in inp.as_tuple()), state=torch.zeros(1, H, N, N, device=gpu_device))
+    with pytest.raises(RuntimeError):
+        op(*(t.to(torch.float64) for t in inp.as_tuple()), state=torch.zeros(1, H, N, N, device=gpu_device))
+    S0 = wkv_state(1, H, N, seed=111)
+    state = S0[0].to(gpu_device).contiguous()
+    y, st = op(*inp.as_tuple(), state=state, return_state=True)
+    assert st is state and y.shape == (T, H * N) and y.dtype == torch.bfloat16
+    y_ref, S_ref = wkv7_rowwise(*(t.cpu() for t in inp.as_tuple()), N, S0[0])
+    check_y(y, y_ref, H, torch.bfloat16)
+    assert state_rel(state.cpu(), S_ref) <= S_TOL
+    # batched form through rwkv7_wkv
+    st2 = S0.to(gpu_device)
+    y2 = ops.rwkv7_wkv(*(t[None] for t in inp.as_tuple()), head_size=64, state=st2)
+    check_y(y2[0], y_ref, H, torch.bfloat16)
