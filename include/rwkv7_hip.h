@@ -90,6 +90,80 @@ int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t total_tokens,
                       const void *a, const void *b, void *y, int chunk_len,
                       void *stream);
 
+/* ------------------------------------------------------------------------
+ * Layer kernels of the stateful model forward.  They replace the eager torch
+ * op chains of RWKV7Block / RWKV7TimeMix / RWKV7ChannelMix.forward_with_state
+ * (rwkvtune/models/rwkv7/model.py:174-418); the dense projections between
+ * them are plain library GEMMs.  Rows are token positions of a packed batch;
+ * the rows of one sequence are contiguous.  row_slot[m] = pool slot of row m's
+ * sequence (negative: no state, x_prev = 0, nothing written).  row_last[m] >= 0
+ * marks the first row of a sequence in this call and holds the index of the
+ * sequence's last row; -1 on every other row.  Small per-channel parameters
+ * are float32; activations use `dtype`.  C <= 8000; H a multiple of 4.
+ * ------------------------------------------------------------------------ */
+
+/*
+ * Residual source + LayerNorm + token shift + lerps.  The residual of row m is
+ * emb[tokens[m]] (tokens non-null) or x_in[m] (+ add[m] when add is non-null),
+ * then ln0 when ln0_w is non-null; it is written to x_out (nullable, float32
+ * [M, C]).  h = LayerNorm(residual; ln_w, ln_b, eps 1e-5); h_prev is the previous
+ * row's h, or prev_pool[slot] on a sequence's first row; out[j][m] =
+ * h + (h_prev - h) * mix[j] for j < n_mix (out: [n_mix, M, C]).  The sequence's
+ * last h is stored to prev_pool[slot] (float32 [pool_slots, C]).
+ * Replaces model.py:393-398 (ln0, ln1), 196-208 (shift + six lerps) and 412
+ * (att_x_prev), and with n_mix = 1 model.py:406-407, 315-321 (ln2, FFN shift).
+ */
+int rwkv7_shift_mix(int dtype, int64_t M, int64_t C, const float *x_in, const void *add,
+                    const int64_t *tokens, const void *emb, int64_t vocab,
+                    const float *ln0_w, const float *ln0_b, float *x_out,
+                    const float *ln_w, const float *ln_b, float *prev_pool,
+                    int64_t pool_slots, const int32_t *row_slot, const int32_t *row_last,
+                    int n_mix, const float *mix, void *out, void *stream);
+
+/* out[n] = LayerNorm(x_in[rows[n]] + add[rows[n]]) (rows NULL: row n; add nullable).
+ * Replaces ln_out (model.py:494) restricted to the rows whose logits are used. */
+int rwkv7_final_norm(int dtype, int64_t n, int64_t C, const float *x_in, const void *add,
+                     const int32_t *rows, const float *ln_w, const float *ln_b, void *out,
+                     void *stream);
+
+/* In-place element-wise activation of n elements: kind 0 = tanh (decay LoRA,
+ * model.py:211), 1 = sigmoid (gate LoRA, model.py:221), 2 = relu(x)^2 (FFN,
+ * model.py:337). */
+int rwkv7_activation(int dtype, int kind, int64_t n, void *x, void *stream);
+
+/*
+ * params: 8 float32 [C] vectors w0, a0, v0 (NULL on layer 0), k_k, k_a, r_k
+ * (the [H, N] tensor flattened), ln_x weight, ln_x bias.
+ *
+ * rwkv7_tmix_prep: from the projection outputs r, k, v and the LoRA outputs
+ * (w_lora = tanh(xw@w1)@w2, a_lora = (xa@a1)@a2, v_lora = (xv@v1)@v2), write the
+ * six float32 WKV operands wkv_ops = {r, w_raw, k', v', -kk, kk*a} ([M, C] each)
+ * and, on layer 0, v_first = v (float32 [M, C]; read on later layers).
+ * Replaces model.py:215-227 and the operand construction of model.py:233-247.
+ */
+int rwkv7_tmix_prep(int dtype, int64_t M, int64_t H, int layer0, const void *r, const void *k,
+                    const void *v, const void *w_lora, const void *a_lora, const void *v_lora,
+                    float *v_first, const float *const *params, float *const *wkv_ops,
+                    void *stream);
+
+/* out = (GroupNorm_H(y; ln_x, eps 64e-5) + sum_head(r*k'*r_k) * v') * g, from the
+ * float32 WKV output y and the operands written by rwkv7_tmix_prep.
+ * Replaces model.py:258-269 (before the output projection). */
+int rwkv7_tmix_post(int dtype, int64_t M, int64_t H, const float *y, const float *r_op,
+                    const float *k_op, const float *v_op, const void *g,
+                    const float *const *params, void *out, void *stream);
+
+/* Single-token fused path: rwkv7_tmix_prep + one WKV step on
+ * state_pool[row_slot[m]] (float32 [pool_slots, H, 64, 64], in place) +
+ * rwkv7_tmix_post, one wave per (row, head).  Rows with a negative slot get
+ * out = 0 and touch no state.  Replaces model.py:215-269 for T = 1 together
+ * with the decode call of the WKV operator (model.py:229-250 -> wkv7s.cu:5-54). */
+int rwkv7_tmix_decode(int dtype, int64_t M, int64_t H, int layer0, const void *r, const void *k,
+                      const void *v, const void *w_lora, const void *a_lora, const void *v_lora,
+                      const void *g, float *v_first, const float *const *params,
+                      float *state_pool, int64_t pool_slots, const int32_t *row_slot,
+                      void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,6 +32,13 @@ SIGNATURES = {
     "rwkv7s_forward": (_I32, [_I32, _I64, _I64, _I64, _I64] + [_P] * 8 + [_P]),
     "rwkv7_wkv_decode": (_I32, [_I32, _I64, _I64, _P, _I64, _P] + [_P] * 7 + [_P]),
     "rwkv7_wkv_prefill": (_I32, [_I32, _I64, _I64, _I64, _P, _P, _P, _I64] + [_P] * 7 + [_I32, _P]),
+    "rwkv7_shift_mix": (_I32, [_I32, _I64, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64,
+                               _P, _P, _I32, _P, _P, _P]),
+    "rwkv7_final_norm": (_I32, [_I32, _I64, _I64, _P, _P, _P, _P, _P, _P, _P]),
+    "rwkv7_activation": (_I32, [_I32, _I32, _I64, _P, _P]),
+    "rwkv7_tmix_prep": (_I32, [_I32, _I64, _I64, _I32] + [_P] * 6 + [_P, _P, _P, _P]),
+    "rwkv7_tmix_post": (_I32, [_I32, _I64, _I64] + [_P] * 5 + [_P, _P, _P]),
+    "rwkv7_tmix_decode": (_I32, [_I32, _I64, _I64, _I32] + [_P] * 7 + [_P, _P, _P, _I64, _P, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -127,3 +127,154 @@ extern "C" int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t tot
     return seq_dispatch(dtype, (int)nseq, (int)H, 0, cu_seqlens, slot_idx, (int)pool_slots, (int)total_tokens,
                         state_pool, r, w, k, v, a, b, y, (hipStream_t)stream);
 }
+
+// ---------------------------------------------------------------------------
+// Layer kernels (rwkv7_layer.hip)
+// ---------------------------------------------------------------------------
+
+template <typename IO>
+hipError_t launch_shift_mix(int M, int C, const float* x_in, const void* add, const int64_t* tokens,
+                            const void* emb, int64_t vocab, const float* ln0_w, const float* ln0_b,
+                            float* x_out, const float* ln_w, const float* ln_b, float* prev_pool,
+                            int pool_slots, const int32_t* row_slot, const int32_t* row_last,
+                            int n_mix, const float* mix, void* out, hipStream_t st);
+template <typename IO>
+hipError_t launch_final_norm(int n, int C, const float* x_in, const void* add, const int32_t* rows,
+                             const float* ln_w, const float* ln_b, void* out, hipStream_t st);
+template <typename IO>
+hipError_t launch_activation(int kind, int64_t n, void* x, hipStream_t st);
+template <typename IO>
+hipError_t launch_tmix_prep(int M, int H, int layer0, const void* r, const void* k, const void* v,
+                            const void* wl, const void* al, const void* vl, float* vfirst,
+                            const float* const* params, float* const* ops, hipStream_t st);
+template <typename IO>
+hipError_t launch_tmix_post(int M, int H, const float* y, const float* r_op, const float* k_op,
+                            const float* v_op, const void* g, const float* const* params, void* out,
+                            hipStream_t st);
+template <typename IO>
+hipError_t launch_tmix_decode(int M, int H, int layer0, const void* r, const void* k, const void* v,
+                              const void* wl, const void* al, const void* vl, const void* g,
+                              float* vfirst, const float* const* params, float* state, int pool_slots,
+                              const int32_t* row_slot, void* out, hipStream_t st);
+
+#define RWKV7_DISPATCH(dtype, call)                         \
+    switch (dtype) {                                        \
+        case RWKV7_DTYPE_F32: { typedef float IO; e = call; break; }  \
+        case RWKV7_DTYPE_F16: { typedef f16_t IO; e = call; break; }  \
+        default: { typedef bf16_t IO; e = call; break; }    \
+    }
+
+namespace {
+constexpr int64_t kMaxC = 8000;  // two fp32 rows of LDS per block
+bool bad_c(int64_t C) { return C <= 0 || C > kMaxC; }
+bool bad_h(int64_t H) { return H <= 0 || (H % 4) != 0 || H * RWKV7_HEAD > kMaxC; }
+}  // namespace
+
+extern "C" int rwkv7_shift_mix(int dtype, int64_t M, int64_t C, const float* x_in, const void* add,
+                               const int64_t* tokens, const void* emb, int64_t vocab,
+                               const float* ln0_w, const float* ln0_b, float* x_out,
+                               const float* ln_w, const float* ln_b, float* prev_pool,
+                               int64_t pool_slots, const int32_t* row_slot, const int32_t* row_last,
+                               int n_mix, const float* mix, void* out, void* stream) {
+    if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: bad dtype code %d", dtype);
+    if (M < 0 || bad_c(C) || n_mix < 1 || n_mix > 8 || pool_slots < 0 || M > kMaxInt)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: bad sizes M=%lld C=%lld n_mix=%d", (long long)M,
+                    (long long)C, n_mix);
+    if (M == 0) return ok();
+    if (tokens == nullptr && x_in == nullptr)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: need x_in or tokens+emb");
+    if (tokens != nullptr && (emb == nullptr || vocab <= 0))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: tokens need emb and vocab > 0");
+    if ((ln0_w == nullptr) != (ln0_b == nullptr))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: ln0 weight and bias go together");
+    if (!ln_w || !ln_b || !prev_pool || !row_slot || !row_last || !mix || !out)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: null pointer");
+    hipError_t e;
+    RWKV7_DISPATCH(dtype, (launch_shift_mix<IO>((int)M, (int)C, x_in, add, tokens, emb, vocab, ln0_w, ln0_b,
+                                                x_out, ln_w, ln_b, prev_pool, (int)pool_slots, row_slot,
+                                                row_last, n_mix, mix, out, (hipStream_t)stream)));
+    return launch_status(e, "shift_mix_kernel");
+}
+
+extern "C" int rwkv7_final_norm(int dtype, int64_t n, int64_t C, const float* x_in, const void* add,
+                                const int32_t* rows, const float* ln_w, const float* ln_b, void* out,
+                                void* stream) {
+    if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_final_norm: bad dtype code %d", dtype);
+    if (n < 0 || bad_c(C) || n > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_final_norm: bad sizes");
+    if (n == 0) return ok();
+    if (!x_in || !ln_w || !ln_b || !out) return fail(RWKV7_ERR_INVALID, "rwkv7_final_norm: null pointer");
+    hipError_t e;
+    RWKV7_DISPATCH(dtype, (launch_final_norm<IO>((int)n, (int)C, x_in, add, rows, ln_w, ln_b, out,
+                                                 (hipStream_t)stream)));
+    return launch_status(e, "final_norm_kernel");
+}
+
+extern "C" int rwkv7_activation(int dtype, int kind, int64_t n, void* x, void* stream) {
+    if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_activation: bad dtype code %d", dtype);
+    if (kind < 0 || kind > 2) return fail(RWKV7_ERR_INVALID, "rwkv7_activation: kind must be 0, 1 or 2");
+    if (n < 0 || n > ((int64_t)1 << 40)) return fail(RWKV7_ERR_INVALID, "rwkv7_activation: bad size");
+    if (n == 0) return ok();
+    if (!x) return fail(RWKV7_ERR_INVALID, "rwkv7_activation: null pointer");
+    hipError_t e;
+    RWKV7_DISPATCH(dtype, (launch_activation<IO>(kind, n, x, (hipStream_t)stream)));
+    return launch_status(e, "activation_kernel");
+}
+
+static bool params_ok(const float* const* p) {
+    for (int i = 0; i < 8; ++i)
+        if (p[i] == nullptr && i != 2) return false;  // v0 may be null on layer 0
+    return true;
+}
+
+extern "C" int rwkv7_tmix_prep(int dtype, int64_t M, int64_t H, int layer0, const void* r, const void* k,
+                               const void* v, const void* w_lora, const void* a_lora, const void* v_lora,
+                               float* v_first, const float* const* params, float* const* wkv_ops,
+                               void* stream) {
+    if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_prep: bad dtype code %d", dtype);
+    if (M < 0 || bad_h(H) || M > kMaxInt)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_prep: bad sizes (H must be a positive multiple of 4)");
+    if (M == 0) return ok();
+    if (!params || !wkv_ops || !params_ok(params) || !r || !k || !v || !w_lora || !a_lora || !v_first)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_prep: null pointer");
+    if (!layer0 && (!v_lora || !params[2])) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_prep: layer > 0 needs v_lora and v0");
+    for (int i = 0; i < 6; ++i)
+        if (!wkv_ops[i]) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_prep: null output");
+    hipError_t e;
+    RWKV7_DISPATCH(dtype, (launch_tmix_prep<IO>((int)M, (int)H, layer0, r, k, v, w_lora, a_lora, v_lora,
+                                                v_first, params, wkv_ops, (hipStream_t)stream)));
+    return launch_status(e, "tmix_prep_kernel");
+}
+
+extern "C" int rwkv7_tmix_post(int dtype, int64_t M, int64_t H, const float* y, const float* r_op,
+                               const float* k_op, const float* v_op, const void* g,
+                               const float* const* params, void* out, void* stream) {
+    if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_post: bad dtype code %d", dtype);
+    if (M < 0 || bad_h(H) || M > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_post: bad sizes");
+    if (M == 0) return ok();
+    if (!params || !params_ok(params) || !y || !r_op || !k_op || !v_op || !g || !out)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_post: null pointer");
+    hipError_t e;
+    RWKV7_DISPATCH(dtype, (launch_tmix_post<IO>((int)M, (int)H, y, r_op, k_op, v_op, g, params, out,
+                                                (hipStream_t)stream)));
+    return launch_status(e, "tmix_post_kernel");
+}
+
+extern "C" int rwkv7_tmix_decode(int dtype, int64_t M, int64_t H, int layer0, const void* r, const void* k,
+                                 const void* v, const void* w_lora, const void* a_lora, const void* v_lora,
+                                 const void* g, float* v_first, const float* const* params, float* state_pool,
+                                 int64_t pool_slots, const int32_t* row_slot, void* out, void* stream) {
+    if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_decode: bad dtype code %d", dtype);
+    if (M < 0 || bad_h(H) || pool_slots < 0 || M > kMaxInt || pool_slots > kMaxInt)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_decode: bad sizes (H must be a positive multiple of 4)");
+    if (M == 0) return ok();
+    if (!params || !params_ok(params) || !r || !k || !v || !w_lora || !a_lora || !g || !v_first ||
+        !state_pool || !row_slot || !out)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_decode: null pointer");
+    if (!layer0 && (!v_lora || !params[2]))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_decode: layer > 0 needs v_lora and v0");
+    hipError_t e;
+    RWKV7_DISPATCH(dtype, (launch_tmix_decode<IO>((int)M, (int)H, layer0, r, k, v, w_lora, a_lora, v_lora, g,
+                                                  v_first, params, state_pool, (int)pool_slots, row_slot,
+                                                  out, (hipStream_t)stream)));
+    return launch_status(e, "tmix_decode_kernel");
+}

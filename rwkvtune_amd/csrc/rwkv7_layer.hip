@@ -1,0 +1,478 @@
+// RWKV-7 layer kernels around the WKV recurrence, for the model's stateful
+// forward (rwkvtune/models/rwkv7/model.py:174-418) on gfx950.
+//
+// The reference runs each layer as ~45 eager torch ops.  Here the per-token
+// element-wise work is fused into a handful of kernels; the dense projections
+// stay library GEMMs (hipBLASLt through torch) between them:
+//
+//   shift_mix     residual add + (ln0) + LayerNorm + token shift + n lerps,
+//                 and the x_prev state update            (model.py:196-208, 310-321, 393-409)
+//   activation    tanh / sigmoid between LoRA GEMMs, relu^2 of the FFN key  (model.py:211,221,337)
+//   tmix_prep     decay / a / value-residual / kk-normalise / k update: the
+//                 six WKV operands of a prefill chunk     (model.py:215-227, 246-247)
+//   tmix_post     GroupNorm(H) + (r*k*r_k).sum*v bonus + gate   (model.py:258-269)
+//   tmix_decode   single-token fused path: prep + WKV step + post in one wave per
+//                 (row, head), state streamed from the slot pool
+//   final_norm    residual add + ln_out on selected rows  (model.py:494)
+//
+// All element-wise arithmetic is fp32 (the reference rounds every op to the
+// model dtype on GPU; on CPU it runs fp32, rwkvtune/inference/pipeline.py:166-175).
+// Rows are token positions of a packed batch; rows of one sequence are
+// contiguous.  row_slot[m] is the pool slot of row m's sequence (negative = no
+// state: zero x_prev, nothing written); row_last[m] >= 0 marks the first row of a
+// sequence in this call and holds the index of its last row.
+#include "common.hpp"
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// Sum over the 256-thread block; `red` is kWaves floats of LDS.  Safe to call
+// back to back (the leading barrier protects the previous call's reads).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) s += red[i];
+    return s;
+}
+
+// In-place LayerNorm of row[0..C) (LDS), two-pass mean / biased variance.
+__device__ void layer_norm_row(float* row, int C, const float* __restrict__ w,
+                               const float* __restrict__ b, float eps, float* red) {
+    float s = 0.f;
+    for (int i = threadIdx.x; i < C; i += kThreads) s += row[i];
+    const float mean = block_sum(s, red) / (float)C;
+    float q = 0.f;
+    for (int i = threadIdx.x; i < C; i += kThreads) {
+        const float d = row[i] - mean;
+        q += d * d;
+    }
+    const float var = block_sum(q, red) / (float)C;
+    const float inv = 1.0f / sqrtf(var + eps);
+    for (int i = threadIdx.x; i < C; i += kThreads) row[i] = (row[i] - mean) * inv * w[i] + b[i];
+    __syncthreads();
+}
+
+template <typename IO>
+struct ResidualSrc {
+    const float* x_in;      // [M, C] fp32 residual, or null when tokens/emb are used
+    const IO* add;          // [M, C] branch output to add, nullable
+    const int64_t* tokens;  // [M] token ids (layer 0), nullable
+    const IO* emb;          // [V, C]
+    int64_t vocab;
+    const float* ln0_w;     // nullable: apply ln0 after the lookup / add
+    const float* ln0_b;
+};
+
+// row[0..C) <- residual stream of row m (emb lookup or x_in + add, then ln0)
+template <typename IO>
+__device__ void load_residual(const ResidualSrc<IO>& src, int m, int C, float* row, float* red) {
+    typedef io_traits<IO> tr;
+    if (src.tokens != nullptr) {
+        const int64_t t = src.tokens[m];
+        const bool ok = t >= 0 && t < src.vocab;
+        const IO* e = src.emb + (ok ? t : 0) * (int64_t)C;
+        for (int i = threadIdx.x; i < C; i += kThreads) row[i] = ok ? tr::to_f32(e[i]) : 0.f;
+    } else {
+        const float* x = src.x_in + (size_t)m * C;
+        if (src.add != nullptr) {
+            const IO* ad = src.add + (size_t)m * C;
+            for (int i = threadIdx.x; i < C; i += kThreads) row[i] = x[i] + tr::to_f32(ad[i]);
+        } else {
+            for (int i = threadIdx.x; i < C; i += kThreads) row[i] = x[i];
+        }
+    }
+    __syncthreads();
+    if (src.ln0_w != nullptr) layer_norm_row(row, C, src.ln0_w, src.ln0_b, 1e-5f, red);
+}
+
+template <typename IO>
+__global__ __launch_bounds__(kThreads) void shift_mix_kernel(
+    int M, int C, ResidualSrc<IO> src, float* __restrict__ x_out,
+    const float* __restrict__ ln_w, const float* __restrict__ ln_b,
+    float* __restrict__ prev_pool, int pool_slots, const int32_t* __restrict__ row_slot,
+    const int32_t* __restrict__ row_last, int n_mix, const float* __restrict__ mix,
+    IO* __restrict__ out)
+{
+    typedef io_traits<IO> tr;
+    extern __shared__ float sm[];
+    float* cur = sm;
+    float* prv = sm + C;
+    float* red = sm + 2 * C;
+    const int m = blockIdx.x;
+
+    load_residual(src, m, C, cur, red);
+    if (x_out != nullptr)
+        for (int i = threadIdx.x; i < C; i += kThreads) x_out[(size_t)m * C + i] = cur[i];
+    layer_norm_row(cur, C, ln_w, ln_b, 1e-5f, red);
+
+    int slot = row_slot[m];
+    if (slot >= pool_slots) slot = -1;
+    const int last = row_last[m];
+    if (last >= 0 || m == 0) {  // first row of its sequence: x_prev comes from the state
+        const float* p = prev_pool + (size_t)(slot < 0 ? 0 : slot) * C;
+        for (int i = threadIdx.x; i < C; i += kThreads) prv[i] = slot < 0 ? 0.f : p[i];
+        __syncthreads();
+    } else {
+        load_residual(src, m - 1, C, prv, red);
+        layer_norm_row(prv, C, ln_w, ln_b, 1e-5f, red);
+    }
+    for (int i = threadIdx.x; i < C; i += kThreads) {
+        const float x = cur[i];
+        const float xx = prv[i] - x;
+        for (int j = 0; j < n_mix; ++j)
+            out[((size_t)j * M + m) * C + i] = tr::from_f32(fmaf(xx, mix[(size_t)j * C + i], x));
+    }
+    // the new x_prev is the normalised last row of the sequence; the first
+    // row's block writes it, after it has read the old value
+    if (last >= 0 && slot >= 0 && last < M) {
+        __syncthreads();
+        float* dst = prev_pool + (size_t)slot * C;
+        if (last == m) {
+            for (int i = threadIdx.x; i < C; i += kThreads) dst[i] = cur[i];
+        } else {
+            load_residual(src, last, C, prv, red);
+            layer_norm_row(prv, C, ln_w, ln_b, 1e-5f, red);
+            for (int i = threadIdx.x; i < C; i += kThreads) dst[i] = prv[i];
+        }
+    }
+}
+
+// y = LN_out(x_in[row] + add[row]) for the n listed rows (rows = null: 0..n-1)
+template <typename IO>
+__global__ __launch_bounds__(kThreads) void final_norm_kernel(
+    int C, ResidualSrc<IO> src, const int32_t* __restrict__ rows, const float* __restrict__ ln_w,
+    const float* __restrict__ ln_b, IO* __restrict__ out)
+{
+    typedef io_traits<IO> tr;
+    extern __shared__ float sm[];
+    float* cur = sm;
+    float* red = sm + C;
+    const int n = blockIdx.x;
+    const int m = rows != nullptr ? rows[n] : n;
+    load_residual(src, m, C, cur, red);
+    layer_norm_row(cur, C, ln_w, ln_b, 1e-5f, red);
+    for (int i = threadIdx.x; i < C; i += kThreads) out[(size_t)n * C + i] = tr::from_f32(cur[i]);
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// softplus as torch computes it (threshold 20: identity above)
+__device__ __forceinline__ float softplusf_(float x) { return x > 20.f ? x : log1pf(expf(x)); }
+
+template <typename IO>
+__global__ void activation_kernel(int kind, int64_t n, IO* __restrict__ x) {
+    typedef io_traits<IO> tr;
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = tr::to_f32(x[i]);
+    float o;
+    if (kind == 0) o = tanhf(v);
+    else if (kind == 1) o = sigmoidf_(v);
+    else { const float r = v > 0.f ? v : 0.f; o = r * r; }
+    x[i] = tr::from_f32(o);
+}
+
+struct TmixParams {
+    const float* w0; const float* a0; const float* v0;
+    const float* k_k; const float* k_a; const float* r_k;
+    const float* lnx_w; const float* lnx_b;
+};
+
+// Per-element pre-WKV math of one head element (lane j of the wave):
+// returns the six WKV operands and the updated k / v used by the bonus term.
+struct PrepOut { float w_raw, k, v, a_op, b_op; float rkr; };
+
+template <typename IO>
+__device__ __forceinline__ PrepOut tmix_prep_elem(
+    int layer0, size_t off, int ch, const IO* r, const IO* k, const IO* v, const IO* wl,
+    const IO* al, const IO* vl, float* vfirst, const TmixParams& P)
+{
+    typedef io_traits<IO> tr;
+    PrepOut o;
+    const float rj = tr::to_f32(r[off]);
+    const float kj = tr::to_f32(k[off]);
+    float vj = tr::to_f32(v[off]);
+    // w = -softplus(-(w0 + w_lin)) - 0.5        (model.py:227)
+    o.w_raw = -softplusf_(-(P.w0[ch] + tr::to_f32(wl[off]))) - 0.5f;
+    // value residual: layer 0 records v_first, later layers mix towards it (model.py:215-218)
+    if (layer0) {
+        vfirst[off] = vj;
+    } else {
+        const float mixv = sigmoidf_(P.v0[ch] + tr::to_f32(vl[off]));
+        vj = vj + (vfirst[off] - vj) * mixv;
+    }
+    const float aj = sigmoidf_(P.a0[ch] + tr::to_f32(al[off]));  // model.py:220
+    const float kkr = kj * P.k_k[ch];                              // model.py:223
+    const float nrm = sqrtf(wave_sum(kkr * kkr));
+    const float kk = kkr / fmaxf(nrm, 1e-12f);                     // F.normalize, eps 1e-12
+    const float kn = kj * (1.0f + (aj - 1.0f) * P.k_a[ch]);        // model.py:225
+    o.k = kn;
+    o.v = vj;
+    o.a_op = -kk;                                                  // model.py:246
+    o.b_op = kk * aj;
+    o.rkr = rj * kn * P.r_k[ch];                                   // bonus term (model.py:267)
+    return o;
+}
+
+// Prefill: write the six fp32 WKV operands (r, w_raw, k, v, -kk, kk*a) of every
+// (row, head).  One wave per (row, head); grid (M, H/4), 256 threads.
+template <typename IO>
+__global__ __launch_bounds__(kThreads) void tmix_prep_kernel(
+    int M, int H, int layer0, const IO* __restrict__ r, const IO* __restrict__ k,
+    const IO* __restrict__ v, const IO* __restrict__ wl, const IO* __restrict__ al,
+    const IO* __restrict__ vl, float* __restrict__ vfirst, TmixParams P,
+    float* __restrict__ r_op, float* __restrict__ w_op, float* __restrict__ k_op,
+    float* __restrict__ v_op, float* __restrict__ a_op, float* __restrict__ b_op)
+{
+    typedef io_traits<IO> tr;
+    const int m = blockIdx.x;
+    const int h = blockIdx.y * kWaves + (threadIdx.x >> 6);
+    if (h >= H) return;  // whole wave exits together
+    const int j = threadIdx.x & 63;
+    const int C = H * RWKV7_HEAD;
+    const int ch = h * RWKV7_HEAD + j;
+    const size_t off = (size_t)m * C + ch;
+    const PrepOut o = tmix_prep_elem(layer0, off, ch, r, k, v, wl, al, vl, vfirst, P);
+    r_op[off] = tr::to_f32(r[off]);
+    w_op[off] = o.w_raw;
+    k_op[off] = o.k;
+    v_op[off] = o.v;
+    a_op[off] = o.a_op;
+    b_op[off] = o.b_op;
+}
+
+// Prefill: out = (GroupNorm_H(y) + (sum_j r_j k_j r_k_j) v) * g   (model.py:258-269)
+template <typename IO>
+__global__ __launch_bounds__(kThreads) void tmix_post_kernel(
+    int M, int H, const float* __restrict__ y, const float* __restrict__ r_op,
+    const float* __restrict__ k_op, const float* __restrict__ v_op, const IO* __restrict__ g,
+    TmixParams P, IO* __restrict__ out)
+{
+    typedef io_traits<IO> tr;
+    const int m = blockIdx.x;
+    const int h = blockIdx.y * kWaves + (threadIdx.x >> 6);
+    if (h >= H) return;
+    const int j = threadIdx.x & 63;
+    const int C = H * RWKV7_HEAD;
+    const int ch = h * RWKV7_HEAD + j;
+    const size_t off = (size_t)m * C + ch;
+    const float yj = y[off];
+    const float mean = wave_sum(yj) * (1.0f / 64.0f);
+    const float d = yj - mean;
+    const float var = wave_sum(d * d) * (1.0f / 64.0f);
+    const float yn = d / sqrtf(var + 64e-5f) * P.lnx_w[ch] + P.lnx_b[ch];
+    const float bonus = wave_sum(r_op[off] * k_op[off] * P.r_k[ch]);
+    out[off] = tr::from_f32((yn + bonus * v_op[off]) * tr::to_f32(g[off]));
+}
+
+// Decode: one token per row, fused prep + WKV step + post.  One 64-lane wave
+// per (row, head), four per block; the state of (slot, head) is streamed with
+// the same coalesced layout as the stand-alone decode kernel: lane l = 16g + c
+// holds S[4m+g][4c..4c+3] for m = 0..15.
+template <typename IO>
+__global__ __launch_bounds__(kThreads) void tmix_decode_kernel(
+    int M, int H, int layer0, const IO* __restrict__ r, const IO* __restrict__ k,
+    const IO* __restrict__ v, const IO* __restrict__ wl, const IO* __restrict__ al,
+    const IO* __restrict__ vl, const IO* __restrict__ g, float* __restrict__ vfirst, TmixParams P,
+    float* __restrict__ state, int pool_slots, const int32_t* __restrict__ row_slot,
+    IO* __restrict__ out)
+{
+    typedef io_traits<IO> tr;
+    __shared__ float lds[kWaves][7][64];
+    const int wv = threadIdx.x >> 6;
+    const int m = blockIdx.x;
+    const int h = blockIdx.y * kWaves + wv;
+    if (h >= H) return;
+    const int l = threadIdx.x & 63;
+    const int C = H * RWKV7_HEAD;
+    const size_t base = (size_t)m * C + (size_t)h * RWKV7_HEAD;
+    int slot = row_slot[m];
+    if (slot >= pool_slots) slot = -1;
+    if (slot < 0) {  // no sequence on this row
+        out[base + l] = tr::from_f32(0.f);
+        return;
+    }
+
+    // element-wise prep, lane l = element l of the head
+    const int chl = h * RWKV7_HEAD + l;
+    const PrepOut o = tmix_prep_elem(layer0, base + l, chl, r, k, v, wl, al, vl, vfirst, P);
+    const float bonus = wave_sum(o.rkr);
+    float (*sh)[64] = lds[wv];
+    sh[0][l] = tr::to_f32(r[base + l]);
+    sh[1][l] = expf(-expf(o.w_raw));  // decay (wkv7s.cu:27)
+    sh[2][l] = o.k;
+    sh[3][l] = o.a_op;
+    sh[4][l] = o.b_op;
+    sh[5][(l & 3) * 16 + (l >> 2)] = o.v;  // sh[5][gg*16+mm] = v[4mm+gg]
+    __syncthreads();
+
+    const int gq = l >> 4;
+    const int c = l & 15;
+    const f32x4 r4 = *reinterpret_cast<const f32x4*>(&sh[0][4 * c]);
+    const f32x4 w4 = *reinterpret_cast<const f32x4*>(&sh[1][4 * c]);
+    const f32x4 k4 = *reinterpret_cast<const f32x4*>(&sh[2][4 * c]);
+    const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sh[3][4 * c]);
+    const f32x4 b4 = *reinterpret_cast<const f32x4*>(&sh[4][4 * c]);
+
+    f32x4* sp = reinterpret_cast<f32x4*>(state + ((size_t)slot * H + h) * (RWKV7_HEAD * RWKV7_HEAD));
+    f32x4 S[16];
+#pragma unroll
+    for (int mm = 0; mm < 16; ++mm) S[mm] = sp[64 * mm + l];
+
+    float p[16];
+#pragma unroll
+    for (int mm = 0; mm < 16; ++mm) p[mm] = fast_dot4(a4, S[mm]);
+    sh[6][gq * 16 + c] = row16_reduce_scatter(p, c);  // sa[4c+gq]
+    __syncthreads();
+
+    const f32x4* vq = reinterpret_cast<const f32x4*>(&sh[5][gq * 16]);
+    const f32x4* sq = reinterpret_cast<const f32x4*>(&sh[6][gq * 16]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const f32x4 vv = vq[q];
+        const f32x4 ss = sq[q];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int mm = 4 * q + e;
+            const float vi = vv[e];
+            const float si = ss[e];
+            f32x4 x = S[mm];
+            x.x = fmaf(si, b4.x, fmaf(k4.x, vi, x.x * w4.x));
+            x.y = fmaf(si, b4.y, fmaf(k4.y, vi, x.y * w4.y));
+            x.z = fmaf(si, b4.z, fmaf(k4.z, vi, x.z * w4.z));
+            x.w = fmaf(si, b4.w, fmaf(k4.w, vi, x.w * w4.w));
+            S[mm] = x;
+            p[mm] = fast_dot4(x, r4);
+        }
+    }
+#pragma unroll
+    for (int mm = 0; mm < 16; ++mm) sp[64 * mm + l] = S[mm];
+
+    // y of row i = 4c + gq, then GroupNorm over the head, bonus and gate
+    const int i = 4 * c + gq;
+    const float yi = row16_reduce_scatter(p, c);
+    const float mean = wave_sum(yi) * (1.0f / 64.0f);
+    const float d = yi - mean;
+    const float var = wave_sum(d * d) * (1.0f / 64.0f);
+    const int chi = h * RWKV7_HEAD + i;
+    const float yn = d / sqrtf(var + 64e-5f) * P.lnx_w[chi] + P.lnx_b[chi];
+    const float vi = sh[5][(i & 3) * 16 + (i >> 2)];
+    out[base + i] = tr::from_f32((yn + bonus * vi) * tr::to_f32(g[base + i]));
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// launchers (called from capi.hip)
+// ---------------------------------------------------------------------------
+
+template <typename IO>
+hipError_t launch_shift_mix(int M, int C, const float* x_in, const void* add, const int64_t* tokens,
+                            const void* emb, int64_t vocab, const float* ln0_w, const float* ln0_b,
+                            float* x_out, const float* ln_w, const float* ln_b, float* prev_pool,
+                            int pool_slots, const int32_t* row_slot, const int32_t* row_last,
+                            int n_mix, const float* mix, void* out, hipStream_t st)
+{
+    ResidualSrc<IO> src{x_in, (const IO*)add, tokens, (const IO*)emb, vocab, ln0_w, ln0_b};
+    const size_t smem = (2 * (size_t)C + kWaves) * sizeof(float);
+    hipLaunchKernelGGL(shift_mix_kernel<IO>, dim3(M), dim3(kThreads), smem, st, M, C, src, x_out,
+                       ln_w, ln_b, prev_pool, pool_slots, row_slot, row_last, n_mix, mix, (IO*)out);
+    return hipGetLastError();
+}
+
+template <typename IO>
+hipError_t launch_final_norm(int n, int C, const float* x_in, const void* add, const int32_t* rows,
+                             const float* ln_w, const float* ln_b, void* out, hipStream_t st)
+{
+    ResidualSrc<IO> src{x_in, (const IO*)add, nullptr, nullptr, 0, nullptr, nullptr};
+    const size_t smem = ((size_t)C + kWaves) * sizeof(float);
+    hipLaunchKernelGGL(final_norm_kernel<IO>, dim3(n), dim3(kThreads), smem, st, C, src, rows, ln_w,
+                       ln_b, (IO*)out);
+    return hipGetLastError();
+}
+
+template <typename IO>
+hipError_t launch_activation(int kind, int64_t n, void* x, hipStream_t st)
+{
+    const unsigned grid = (unsigned)((n + 255) / 256);
+    hipLaunchKernelGGL(activation_kernel<IO>, dim3(grid), dim3(256), 0, st, kind, n, (IO*)x);
+    return hipGetLastError();
+}
+
+static TmixParams make_params(const float* const* p) {
+    return TmixParams{p[0], p[1], p[2], p[3], p[4], p[5], p[6], p[7]};
+}
+
+template <typename IO>
+hipError_t launch_tmix_prep(int M, int H, int layer0, const void* r, const void* k, const void* v,
+                            const void* wl, const void* al, const void* vl, float* vfirst,
+                            const float* const* params, float* const* ops, hipStream_t st)
+{
+    dim3 grid(M, (H + kWaves - 1) / kWaves);
+    hipLaunchKernelGGL(tmix_prep_kernel<IO>, grid, dim3(kThreads), 0, st, M, H, layer0,
+                       (const IO*)r, (const IO*)k, (const IO*)v, (const IO*)wl, (const IO*)al,
+                       (const IO*)vl, vfirst, make_params(params), ops[0], ops[1], ops[2], ops[3],
+                       ops[4], ops[5]);
+    return hipGetLastError();
+}
+
+template <typename IO>
+hipError_t launch_tmix_post(int M, int H, const float* y, const float* r_op, const float* k_op,
+                            const float* v_op, const void* g, const float* const* params, void* out,
+                            hipStream_t st)
+{
+    dim3 grid(M, (H + kWaves - 1) / kWaves);
+    hipLaunchKernelGGL(tmix_post_kernel<IO>, grid, dim3(kThreads), 0, st, M, H, y, r_op, k_op, v_op,
+                       (const IO*)g, make_params(params), (IO*)out);
+    return hipGetLastError();
+}
+
+template <typename IO>
+hipError_t launch_tmix_decode(int M, int H, int layer0, const void* r, const void* k, const void* v,
+                              const void* wl, const void* al, const void* vl, const void* g,
+                              float* vfirst, const float* const* params, float* state, int pool_slots,
+                              const int32_t* row_slot, void* out, hipStream_t st)
+{
+    dim3 grid(M, (H + kWaves - 1) / kWaves);
+    hipLaunchKernelGGL(tmix_decode_kernel<IO>, grid, dim3(kThreads), 0, st, M, H, layer0,
+                       (const IO*)r, (const IO*)k, (const IO*)v, (const IO*)wl, (const IO*)al,
+                       (const IO*)vl, (const IO*)g, vfirst, make_params(params), state, pool_slots,
+                       row_slot, (IO*)out);
+    return hipGetLastError();
+}
+
+#define RWKV7_INST_LAYER(IO)                                                                        \
+    template hipError_t launch_shift_mix<IO>(int, int, const float*, const void*, const int64_t*,  \
+                                             const void*, int64_t, const float*, const float*,     \
+                                             float*, const float*, const float*, float*, int,      \
+                                             const int32_t*, const int32_t*, int, const float*,    \
+                                             void*, hipStream_t);                                  \
+    template hipError_t launch_final_norm<IO>(int, int, const float*, const void*, const int32_t*, \
+                                              const float*, const float*, void*, hipStream_t);     \
+    template hipError_t launch_activation<IO>(int, int64_t, void*, hipStream_t);                   \
+    template hipError_t launch_tmix_prep<IO>(int, int, int, const void*, const void*, const void*, \
+                                             const void*, const void*, const void*, float*,        \
+                                             const float* const*, float* const*, hipStream_t);     \
+    template hipError_t launch_tmix_post<IO>(int, int, const float*, const float*, const float*,   \
+                                             const float*, const void*, const float* const*,       \
+                                             void*, hipStream_t);                                  \
+    template hipError_t launch_tmix_decode<IO>(int, int, int, const void*, const void*,            \
+                                               const void*, const void*, const void*, const void*, \
+                                               const void*, float*, const float* const*, float*,   \
+                                               int, const int32_t*, void*, hipStream_t);
+
+RWKV7_INST_LAYER(float)
+RWKV7_INST_LAYER(bf16_t)
+RWKV7_INST_LAYER(f16_t)

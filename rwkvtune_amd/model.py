@@ -1,0 +1,524 @@
+"""RWKV-7 model for the gfx950 rollout path.
+
+Mirrors ``rwkvtune/models/rwkv7/model.py`` at the interface:
+
+* the module tree and parameter names are the reference's (``emb``,
+  ``blocks.{i}.ln0/ln1/ln2``, ``blocks.{i}.att.{x_r, ..., w0, w1, w2, a0, a1, a2,
+  v0, v1, v2, g1, g2, k_k, k_a, r_k, receptance, key, value, output, ln_x}``,
+  ``blocks.{i}.ffn.{x_k, key, value}``, ``ln_out``, ``head``; ``model.py:34-131,
+  281-302, 346-365, 421-433``), so a reference ``state_dict`` loads unchanged;
+* ``forward_with_state(idx, states)`` / ``init_state(B)`` / ``forward(idx,
+  logits_to_keep)`` keep the reference's signatures and state layout
+  (``model.py:435-520``).
+
+The computation is not the reference's eager op chain.  A layer is five HIP
+kernels from ``librwkv7_hip.so`` (residual + LayerNorm + token shift + lerps,
+LoRA activations, the fused WKV time-mix, the FFN shift, relu^2) around the
+dense projections, which are library GEMMs.  Every call works on a *slot pool*:
+per layer ``att_kv [S, H, 64, 64]``, ``att_x_prev [S, C]``, ``ffn_x_prev [S, C]``,
+all float32, addressed by slot index, so the engine never gathers or scatters
+states (``rwkvtune/inference/scheduler_core.py:377-395``).
+
+Element-wise math is float32 for every model dtype; the dense projections run
+in the model dtype with float32 accumulation.  There is no CPU path: the HIP
+library must be present (``_lib.HipLibraryMissing`` otherwise).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from dataclasses import dataclass, field
+from typing import List, Optional, Sequence
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _lib
+from . import operators as wkv_ops
+
+HEAD_SIZE = 64
+
+
+@dataclass
+class RWKV7Config:
+    """Model fields of the reference's ``SimpleTrainConfig``
+    (``rwkvtune/models/rwkv7/config.py:7-79``, exported as ``RWKV7Config``)."""
+    n_layer: int = 12
+    n_embd: int = 768
+    vocab_size: int = 65536
+    ctx_len: int = 1024
+    head_size_a: int = 64
+    dim_att_lora: int = 0
+    dim_gate_lora: int = 0
+    dim_mv_lora: int = 0
+    dim_att: int = field(init=False)
+
+    def __post_init__(self):
+        self.dim_att = self.n_embd
+        if self.head_size_a != HEAD_SIZE:
+            raise ValueError(f"head_size_a must be {HEAD_SIZE}")
+        if self.n_embd % (4 * HEAD_SIZE) != 0:
+            raise ValueError("n_embd must be a multiple of 256 (H a multiple of 4)")
+
+    @property
+    def n_head(self) -> int:
+        return self.n_embd // HEAD_SIZE
+
+    def lora_dims(self):
+        """(decay, a, value, gate) LoRA ranks; the defaults are the reference's
+        formulas (``model.py:71-99``)."""
+        C = self.n_embd
+        dw = self.dim_att_lora if self.dim_att_lora > 0 else max(32, int(round((2.0 * C ** 0.5) / 32) * 32))
+        dv = self.dim_mv_lora if self.dim_mv_lora > 0 else max(32, int(round((1.4 * C ** 0.5) / 32) * 32))
+        dg = self.dim_gate_lora if self.dim_gate_lora > 0 else max(32, int(round((5.6 * C ** 0.5) / 32) * 32))
+        return dw, dw, dv, dg
+
+
+# Model presets of the benchmark configurations (architecture and LoRA ranks of
+# rwkvtune/configs/models/rwkv7-{0.1b,1.5b,7.2b}.json).  cfg1 keeps the
+# reference's default LoRA formula (dim_* = 0).
+PRESETS = {
+    "rwkv7-0.1b": dict(n_layer=12, n_embd=768),
+    "rwkv7-0.4b": dict(n_layer=24, n_embd=1024, dim_att_lora=64, dim_gate_lora=128, dim_mv_lora=32),
+    "rwkv7-1.5b": dict(n_layer=24, n_embd=2048, dim_att_lora=96, dim_gate_lora=256, dim_mv_lora=64),
+    "rwkv7-2.9b": dict(n_layer=32, n_embd=2560, dim_att_lora=96, dim_gate_lora=320, dim_mv_lora=64),
+    "rwkv7-7.2b": dict(n_layer=32, n_embd=4096, dim_att_lora=128, dim_gate_lora=480, dim_mv_lora=96),
+}
+
+
+def config_from_preset(name: str, **over) -> RWKV7Config:
+    kw = dict(PRESETS[name])
+    kw.update(over)
+    return RWKV7Config(**kw)
+
+
+class RWKV7TimeMix(nn.Module):
+    """Parameter container of ``RWKV7TimeMix`` (``model.py:34-131``)."""
+
+    def __init__(self, config: RWKV7Config, layer_id: int):
+        super().__init__()
+        C, H, N = config.n_embd, config.n_head, HEAD_SIZE
+        dw, da, dv, dg = config.lora_dims()
+        self.layer_id = layer_id
+        self.head_size = N
+        self.n_head = H
+        for name in ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g", "w0", "a0", "k_k", "k_a"):
+            setattr(self, name, nn.Parameter(torch.empty(1, 1, C)))
+        self.w1 = nn.Parameter(torch.empty(C, dw))
+        self.w2 = nn.Parameter(torch.empty(dw, C))
+        self.a1 = nn.Parameter(torch.empty(C, da))
+        self.a2 = nn.Parameter(torch.empty(da, C))
+        if layer_id > 0:
+            self.v0 = nn.Parameter(torch.empty(1, 1, C))
+            self.v1 = nn.Parameter(torch.empty(C, dv))
+            self.v2 = nn.Parameter(torch.empty(dv, C))
+        self.g1 = nn.Parameter(torch.empty(C, dg))
+        self.g2 = nn.Parameter(torch.empty(dg, C))
+        self.r_k = nn.Parameter(torch.empty(H, N))
+        self.receptance = nn.Linear(C, C, bias=False)
+        self.key = nn.Linear(C, C, bias=False)
+        self.value = nn.Linear(C, C, bias=False)
+        self.output = nn.Linear(C, C, bias=False)
+        self.ln_x = nn.GroupNorm(H, C, eps=64e-5)
+
+
+class RWKV7ChannelMix(nn.Module):
+    """Parameter container of ``RWKV7ChannelMix`` (``model.py:281-302``)."""
+
+    def __init__(self, config: RWKV7Config, layer_id: int):
+        super().__init__()
+        C = config.n_embd
+        self.layer_id = layer_id
+        self.x_k = nn.Parameter(torch.empty(1, 1, C))
+        self.key = nn.Linear(C, 4 * C, bias=False)
+        self.value = nn.Linear(4 * C, C, bias=False)
+
+
+class RWKV7Block(nn.Module):
+    """Parameter container of ``RWKV7Block`` (``model.py:346-365``)."""
+
+    def __init__(self, config: RWKV7Config, layer_id: int):
+        super().__init__()
+        self.layer_id = layer_id
+        self.ln1 = nn.LayerNorm(config.n_embd)
+        self.ln2 = nn.LayerNorm(config.n_embd)
+        self.skip_ln0 = False
+        if layer_id == 0:
+            self.ln0 = nn.LayerNorm(config.n_embd)
+        self.att = RWKV7TimeMix(config, layer_id)
+        self.ffn = RWKV7ChannelMix(config, layer_id)
+
+
+# ---------------------------------------------------------------------------
+# Seeded dense initialisation
+# ---------------------------------------------------------------------------
+
+@torch.no_grad()
+def init_dense_(model: "RWKV7Model", seed: int = 0, device=None) -> "RWKV7Model":
+    """Seeded dense random init.
+
+    The per-channel structured parameters follow the reference formulas
+    (``model.py:48-104, 288-293``); every matrix (and the embedding) is drawn
+    N(0, (0.5/sqrt(fan_in))^2) instead of the reference's zero / orthogonal init
+    (the reference zeroes ``output``, ``ffn.value`` and the LoRA down
+    projections, ``model.py:76-117, 302``, which would make every logit
+    independent of the recurrence).  LayerNorm / GroupNorm weights are
+    1 + N(0, 0.1^2) and biases N(0, 0.1^2), so every parameter reaches the output.
+    Draws happen on ``device`` (default: the model's) with a seeded generator.
+    """
+    cfg = model.config
+    dev = torch.device(device) if device is not None else next(model.parameters()).device
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    C, N, L = cfg.n_embd, HEAD_SIZE, cfg.n_layer
+
+    def normal_(p, std):
+        p.copy_(torch.randn(p.shape, generator=gen, device=dev, dtype=torch.float32) * std)
+
+    def mat_(p, fan_in):
+        normal_(p, 0.5 / math.sqrt(fan_in))
+
+    ddd = torch.arange(C, dtype=torch.float64, device=dev) / C
+    n = torch.arange(C, dtype=torch.float64, device=dev)
+    linear = n / (C - 1) - 0.5
+    zig = ((n % N) - (N - 1) / 2) / ((N - 1) / 2)
+    zig = zig * zig.abs()
+
+    def set_(p, v):
+        p.copy_(v.reshape(p.shape).to(torch.float32))
+
+    normal_(model.emb.weight, 1.0)
+    for i, blk in enumerate(model.blocks):
+        r01 = i / (L - 1) if L > 1 else 0.0
+        r1a0 = 1.0 - i / L
+        att, ffn = blk.att, blk.ffn
+        for ln in [blk.ln1, blk.ln2] + ([blk.ln0] if i == 0 else []):
+            set_(ln.weight, 1.0 + 0.1 * torch.randn(C, generator=gen, device=dev))
+            set_(ln.bias, 0.1 * torch.randn(C, generator=gen, device=dev))
+        set_(att.x_r, 1.0 - ddd ** (0.2 * r1a0))
+        set_(att.x_w, 1.0 - ddd ** (0.9 * r1a0))
+        set_(att.x_k, 1.0 - ddd ** (0.7 * r1a0))
+        set_(att.x_v, 1.0 - ddd ** (0.7 * r1a0))
+        set_(att.x_a, 1.0 - ddd ** (0.9 * r1a0))
+        set_(att.x_g, 1.0 - ddd ** (0.2 * r1a0))
+        www = -6 + 6 * (n / (C - 1)) ** (1 + 1 * r01 ** 0.3)
+        set_(att.w0, www + 0.5 + zig * 2.5)
+        set_(att.a0, -0.19 + zig * 0.3 + linear * 0.4)
+        if i > 0:
+            set_(att.v0, 0.73 - linear * 0.4)
+        set_(att.k_k, 0.71 - linear * 0.1)
+        set_(att.k_a, torch.full((C,), 1.02, dtype=torch.float64, device=dev))
+        set_(att.r_k, torch.full((C,), -0.04, dtype=torch.float64, device=dev))
+        for name in ("w1", "a1", "g1") + (("v1",) if i > 0 else ()):
+            mat_(getattr(att, name), C)
+        for name in ("w2", "a2", "g2") + (("v2",) if i > 0 else ()):
+            p = getattr(att, name)
+            mat_(p, p.shape[0])
+        for lin in (att.receptance, att.key, att.value, att.output, ffn.key, ffn.value):
+            mat_(lin.weight, lin.weight.shape[1])
+        set_(att.ln_x.weight, 1.0 + 0.1 * torch.randn(C, generator=gen, device=dev))
+        set_(att.ln_x.bias, 0.1 * torch.randn(C, generator=gen, device=dev))
+        set_(ffn.x_k, 1.0 - ddd ** (r1a0 ** 4))
+    set_(model.ln_out.weight, 1.0 + 0.1 * torch.randn(C, generator=gen, device=dev))
+    set_(model.ln_out.bias, 0.1 * torch.randn(C, generator=gen, device=dev))
+    mat_(model.head.weight, C)
+    model.invalidate()
+    return model
+
+
+# ---------------------------------------------------------------------------
+# Slot pool
+# ---------------------------------------------------------------------------
+
+class StatePool:
+    """Per-layer recurrent state of ``n_slots`` sequences, float32:
+    ``kv [L, S, H, 64, 64]``, ``att_x [L, S, C]``, ``ffn_x [L, S, C]``
+    (the pool of ``scheduler_core.py:180-205``, with x_prev kept in float32)."""
+
+    def __init__(self, config: RWKV7Config, n_slots: int, device):
+        L, C, H = config.n_layer, config.n_embd, config.n_head
+        self.n_slots = n_slots
+        self.kv = torch.zeros((L, n_slots, H, HEAD_SIZE, HEAD_SIZE), dtype=torch.float32, device=device)
+        self.att_x = torch.zeros((L, n_slots, C), dtype=torch.float32, device=device)
+        self.ffn_x = torch.zeros((L, n_slots, C), dtype=torch.float32, device=device)
+
+    def zero_(self, slots=None):
+        if slots is None:
+            self.kv.zero_()
+            self.att_x.zero_()
+            self.ffn_x.zero_()
+        else:
+            self.kv[:, slots] = 0
+            self.att_x[:, slots] = 0
+            self.ffn_x[:, slots] = 0
+
+    def copy_slots_(self, dst_slots, src: "StatePool", src_slots):
+        """dst[dst_slots] <- src[src_slots] on every layer (index tensors on device)."""
+        self.kv[:, dst_slots] = src.kv[:, src_slots]
+        self.att_x[:, dst_slots] = src.att_x[:, src_slots]
+        self.ffn_x[:, dst_slots] = src.ffn_x[:, src_slots]
+
+
+# ---------------------------------------------------------------------------
+# The model
+# ---------------------------------------------------------------------------
+
+class _LayerPack:
+    """float32 copies of one layer's per-channel parameters, laid out for the kernels."""
+
+    def __init__(self, blk: RWKV7Block, C: int):
+        att, ffn = blk.att, blk.ffn
+
+        def f32(t):
+            return t.detach().reshape(-1).to(torch.float32).contiguous()
+
+        self.layer0 = blk.layer_id == 0
+        self.use_ln0 = self.layer0 and not blk.skip_ln0
+        self.ln0 = (f32(blk.ln0.weight), f32(blk.ln0.bias)) if self.use_ln0 else None
+        self.ln1 = (f32(blk.ln1.weight), f32(blk.ln1.bias))
+        self.ln2 = (f32(blk.ln2.weight), f32(blk.ln2.bias))
+        self.mix6 = torch.stack([f32(getattr(att, n)) for n in ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g")])
+        self.mixk = f32(ffn.x_k).reshape(1, C)
+        zero = torch.zeros(C, dtype=torch.float32, device=self.mix6.device)
+        self.tvecs = [f32(att.w0), f32(att.a0), f32(att.v0) if not self.layer0 else zero,
+                      f32(att.k_k), f32(att.k_a), f32(att.r_k), f32(att.ln_x.weight), f32(att.ln_x.bias)]
+        ptrs = [t.data_ptr() for t in self.tvecs]
+        if self.layer0:
+            ptrs[2] = 0
+        self.tparams = (ctypes.c_void_p * 8)(*ptrs)
+
+
+class RWKV7Model(nn.Module):
+    """RWKV-7 language model on the HIP library (interface of ``model.py:421-520``)."""
+
+    def __init__(self, config: RWKV7Config):
+        super().__init__()
+        self.config = config
+        self.emb = nn.Embedding(config.vocab_size, config.n_embd)
+        self.blocks = nn.ModuleList([RWKV7Block(config, i) for i in range(config.n_layer)])
+        self.ln_out = nn.LayerNorm(config.n_embd)
+        self.head = nn.Linear(config.n_embd, config.vocab_size, bias=False)
+        self._packs = None
+
+    # -- bookkeeping ---------------------------------------------------------
+
+    def invalidate(self):
+        """Drop cached float32 parameter packs (call after changing parameters)."""
+        self._packs = None
+
+    def _apply(self, fn, *args, **kwargs):
+        self._packs = None
+        return super()._apply(fn, *args, **kwargs)
+
+    def load_state_dict(self, state_dict, strict: bool = True, assign: bool = False):
+        """Loads a reference state dict: ``r_k`` may be flat (``model.py:577-584``);
+        layer-0 ``v0/v1/v2`` are dropped (``model.py:586-599``); without ``ln0`` in
+        the source the embedding is taken as already normalised (``skip_ln0``,
+        ``model.py:601-609``)."""
+        sd = dict(state_dict)
+        H, N = self.config.n_head, HEAD_SIZE
+        for key in list(sd):
+            if key.endswith("att.r_k") and sd[key].ndim == 1:
+                sd[key] = sd[key].view(H, N)
+        for s in ("0", "1", "2"):
+            sd.pop(f"blocks.0.att.v{s}", None)
+        has_ln0 = "blocks.0.ln0.weight" in state_dict and "blocks.0.ln0.bias" in state_dict
+        res = super().load_state_dict(sd, strict=False, assign=assign)
+        if len(self.blocks) > 0:
+            self.blocks[0].skip_ln0 = not has_ln0
+        self.invalidate()
+        return res
+
+    @property
+    def device(self):
+        return self.emb.weight.device
+
+    @property
+    def dtype(self):
+        return self.emb.weight.dtype
+
+    def _check_device(self):
+        if self.device.type != "cuda":
+            raise RuntimeError("RWKV7Model runs on the HIP library only; move it to a GPU device first")
+        _lib.load()
+
+    def packs(self):
+        if self._packs is None:
+            self._check_device()
+            C = self.config.n_embd
+            with torch.no_grad():
+                self._packs = [_LayerPack(b, C) for b in self.blocks]
+                self._ln_out = (self.ln_out.weight.detach().float().contiguous(),
+                                self.ln_out.bias.detach().float().contiguous())
+        return self._packs
+
+    def init_state(self, batch_size: int):
+        """Per-layer states as in ``model.py:499-520`` (x_prev in float32 here)."""
+        C, H, N = self.config.n_embd, self.config.n_head, HEAD_SIZE
+        dev = self.device
+        return [{"att_x_prev": torch.zeros(batch_size, C, dtype=torch.float32, device=dev),
+                 "att_kv": torch.zeros(batch_size, H, N, N, dtype=torch.float32, device=dev),
+                 "ffn_x_prev": torch.zeros(batch_size, C, dtype=torch.float32, device=dev)}
+                for _ in range(self.config.n_layer)]
+
+    # -- pooled forward ------------------------------------------------------
+
+    def _lin(self, x, weight):
+        return F.linear(x, weight)
+
+    @torch.no_grad()
+    def forward_pooled(self, tokens: torch.Tensor, row_slot: torch.Tensor, row_last: torch.Tensor,
+                       pool: StatePool, *, decode: bool, cu_seqlens: Optional[torch.Tensor] = None,
+                       seq_slot: Optional[torch.Tensor] = None,
+                       logit_rows: Optional[torch.Tensor] = None, n_logit_rows: Optional[int] = None,
+                       return_hidden: bool = False):
+        """Run every layer over ``M`` packed rows on the slot pool.
+
+        tokens [M] int64; row_slot / row_last [M] int32 (see ``rwkv7_shift_mix``).
+        decode=True: one token per sequence (row m is sequence m), fused WKV
+        time-mix.  decode=False: ragged prefill; ``cu_seqlens`` [nseq+1] and
+        ``seq_slot`` [nseq] int32 describe the sequences.  ``logit_rows``: int32
+        rows whose logits are returned (None: all rows).  No host synchronisation.
+        """
+        cfg = self.config
+        C, H, L = cfg.n_embd, cfg.n_head, cfg.n_layer
+        M = tokens.shape[0]
+        dt = self.dtype
+        code = _lib.dtype_code(dt)
+        dev = tokens.device
+        st = _lib.stream_of(tokens)
+        P = _lib.ptr
+        packs = self.packs()
+        if M == 0:
+            raise ValueError("forward_pooled needs at least one row")
+
+        x_res = torch.empty((M, C), dtype=torch.float32, device=dev)
+        x_mid = torch.empty((M, C), dtype=torch.float32, device=dev)
+        mixes = torch.empty((6, M, C), dtype=dt, device=dev)
+        xk_ffn = torch.empty((1, M, C), dtype=dt, device=dev)
+        v_first = torch.empty((M, C), dtype=torch.float32, device=dev)
+        if not decode:
+            ops = torch.empty((6, M, C), dtype=torch.float32, device=dev)
+            ops_ptrs = (ctypes.c_void_p * 6)(*[ops[i].data_ptr() for i in range(6)])
+            y = torch.empty((M, C), dtype=torch.float32, device=dev)
+        ffn_out = None
+        S = pool.n_slots
+        for l in range(L):
+            blk = self.blocks[l]
+            att, ffn, pk = blk.att, blk.ffn, packs[l]
+            kv, ax, fx = pool.kv[l], pool.att_x[l], pool.ffn_x[l]
+            # residual (+ previous FFN) -> ln0/ln1 -> shift -> 6 lerps
+            if l == 0:
+                _lib.call("rwkv7_shift_mix", code, M, C, None, None, P(tokens), P(self.emb.weight),
+                          cfg.vocab_size, P(pk.ln0[0]) if pk.ln0 else None, P(pk.ln0[1]) if pk.ln0 else None,
+                          P(x_res), P(pk.ln1[0]), P(pk.ln1[1]), P(ax), S, P(row_slot), P(row_last), 6,
+                          P(pk.mix6), P(mixes), st)
+            else:
+                _lib.call("rwkv7_shift_mix", code, M, C, P(x_mid), P(ffn_out), None, None, 0, None, None,
+                          P(x_res), P(pk.ln1[0]), P(pk.ln1[1]), P(ax), S, P(row_slot), P(row_last), 6,
+                          P(pk.mix6), P(mixes), st)
+            xr, xw, xk, xv, xa, xg = mixes.unbind(0)
+            r = self._lin(xr, att.receptance.weight)
+            k = self._lin(xk, att.key.weight)
+            v = self._lin(xv, att.value.weight)
+            hw = xw @ att.w1
+            ha = xa @ att.a1
+            hg = xg @ att.g1
+            _lib.call("rwkv7_activation", code, 0, hw.numel(), P(hw), st)
+            _lib.call("rwkv7_activation", code, 1, hg.numel(), P(hg), st)
+            wl = hw @ att.w2
+            al = ha @ att.a2
+            g = hg @ att.g2
+            vl = (xv @ att.v1) @ att.v2 if l > 0 else None
+            o = torch.empty((M, C), dtype=dt, device=dev)
+            if decode:
+                _lib.call("rwkv7_tmix_decode", code, M, H, int(l == 0), P(r), P(k), P(v), P(wl), P(al),
+                          P(vl), P(g), P(v_first), pk.tparams, P(kv), S, P(row_slot), P(o), st)
+            else:
+                _lib.call("rwkv7_tmix_prep", code, M, H, int(l == 0), P(r), P(k), P(v), P(wl), P(al),
+                          P(vl), P(v_first), pk.tparams, ops_ptrs, st)
+                wkv_ops.wkv7_prefill(kv, seq_slot, cu_seqlens, *ops.unbind(0), y=y)
+                _lib.call("rwkv7_tmix_post", code, M, H, P(y), P(ops[0]), P(ops[2]), P(ops[3]), P(g),
+                          pk.tparams, P(o), st)
+            att_out = self._lin(o, att.output.weight)
+            # residual + attention -> ln2 -> FFN shift/lerp
+            _lib.call("rwkv7_shift_mix", code, M, C, P(x_res), P(att_out), None, None, 0, None, None,
+                      P(x_mid), P(pk.ln2[0]), P(pk.ln2[1]), P(fx), S, P(row_slot), P(row_last), 1,
+                      P(pk.mixk), P(xk_ffn), st)
+            hk = self._lin(xk_ffn[0], ffn.key.weight)
+            _lib.call("rwkv7_activation", code, 2, hk.numel(), P(hk), st)
+            ffn_out = self._lin(hk, ffn.value.weight)
+        n_out = M if logit_rows is None else (n_logit_rows if n_logit_rows is not None else logit_rows.numel())
+        xo = torch.empty((n_out, C), dtype=dt, device=dev)
+        _lib.call("rwkv7_final_norm", code, n_out, C, P(x_mid), P(ffn_out), P(logit_rows),
+                  P(self._ln_out[0]), P(self._ln_out[1]), P(xo), st)
+        if return_hidden:
+            return xo
+        return self._lin(xo, self.head.weight)
+
+    # -- reference-compatible entry points ------------------------------------
+
+    @staticmethod
+    def _meta_uniform(B: int, T: int, dev):
+        idx = torch.arange(B * T, dtype=torch.int32)
+        last = torch.full((B * T,), -1, dtype=torch.int32)
+        last[0::T] = idx[T - 1::T]
+        slot = (idx // T).to(torch.int32)
+        cu = torch.arange(0, (B + 1) * T, T, dtype=torch.int32)
+        return (slot.to(dev), last.to(dev), cu.to(dev), torch.arange(B, dtype=torch.int32).to(dev))
+
+    @torch.no_grad()
+    def forward_with_state(self, idx: torch.Tensor, states=None):
+        """``(logits [B, T, V], new_states)``: the contract of ``model.py:468-497``.
+
+        ``states`` is a list of per-layer dicts (``init_state``); the returned
+        states are new float32 tensors (the inputs are not modified)."""
+        self._check_device()
+        if idx.ndim != 2:
+            raise ValueError(f"idx must be [B, T], got {tuple(idx.shape)}")
+        B, T = idx.shape
+        if T == 0 or B == 0:
+            raise ValueError("forward_with_state needs B > 0 and T > 0")
+        dev = self.device
+        cfg = self.config
+        pool = StatePool(cfg, B, dev)
+        if states is not None:
+            if len(states) != cfg.n_layer:
+                raise ValueError(f"expected {cfg.n_layer} layer states, got {len(states)}")
+            for l, s in enumerate(states):
+                pool.att_x[l].copy_(s["att_x_prev"].reshape(B, -1))
+                pool.kv[l].copy_(s["att_kv"].reshape(pool.kv[l].shape))
+                pool.ffn_x[l].copy_(s["ffn_x_prev"].reshape(B, -1))
+        tokens = idx.to(device=dev, dtype=torch.int64).reshape(-1).contiguous()
+        slot, last, cu, seq_slot = self._meta_uniform(B, T, dev)
+        logits = self.forward_pooled(tokens, slot, last, pool, decode=(T == 1), cu_seqlens=cu,
+                                     seq_slot=seq_slot)
+        new_states = [{"att_x_prev": pool.att_x[l], "att_kv": pool.kv[l], "ffn_x_prev": pool.ffn_x[l]}
+                      for l in range(cfg.n_layer)]
+        return logits.view(B, T, -1), new_states
+
+    @torch.no_grad()
+    def forward(self, idx: torch.Tensor, logits_to_keep: Optional[int] = None):
+        """Stateless full-sequence logits (``model.py:435-466``), zero initial state."""
+        self._check_device()
+        B, T = idx.shape
+        pool = StatePool(self.config, B, self.device)
+        tokens = idx.to(device=self.device, dtype=torch.int64).reshape(-1).contiguous()
+        slot, last, cu, seq_slot = self._meta_uniform(B, T, self.device)
+        keep = T if (logits_to_keep is None or logits_to_keep >= T) else logits_to_keep
+        rows = (torch.arange(B, device=self.device)[:, None] * T
+                + torch.arange(T - keep, T, device=self.device)[None, :]).reshape(-1).to(torch.int32)
+        logits = self.forward_pooled(tokens, slot, last, pool, decode=(T == 1), cu_seqlens=cu,
+                                     seq_slot=seq_slot, logit_rows=rows)
+        return logits.view(B, keep, -1)
+
+
+def build_model(config: RWKV7Config, dtype=torch.bfloat16, device="cuda", seed: int = 0) -> RWKV7Model:
+    """Allocate a model on ``device`` in ``dtype`` and apply the seeded dense init."""
+    with torch.device("meta"):
+        m = RWKV7Model(config)
+    m = m.to_empty(device=device)
+    m = m.to(dtype)
+    init_dense_(m, seed=seed, device=device)
+    return m
