@@ -164,6 +164,43 @@ int rwkv7_tmix_decode(int dtype, int64_t M, int64_t H, int layer0, const void *r
                       float *state_pool, int64_t pool_slots, const int32_t *row_slot,
                       void *out, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Sampling
+ * ------------------------------------------------------------------------ */
+
+/*
+ * One token per row of logits [M, V] (row stride ld >= V, V <= 65536, dtype of
+ * the logits) into out_tok (int64 [M]) and out_logp (float32 [M]).  Per row:
+ * temperature[m] (< 1e-6: greedy), top_p[m], top_k[m] (0 = off); ids above
+ * max_valid_id are banned (negative: no ban).  Optional logit bias in CSR form:
+ * bias_ids / bias_val [bias_off[m] .. bias_off[m+1]) (bias_off NULL: none).
+ * active (uint8 [M], nullable): rows with 0 are skipped.  Draws use a
+ * counter-based hash of (seed, rng_key[m], rng_ctr[m]).  rule 1 =
+ * TokenSampler.sample (rwkvtune/inference/core.py:40-137), rule 0 =
+ * TokenSampler.sample_batch (core.py:142-236); see sampler.hip for the exact
+ * rules.  Replaces both methods' torch op chains (softmax, sort, cumsum,
+ * multinomial, gather) and their per-sequence .item() synchronisations.
+ */
+int rwkv7_sample(int dtype, int64_t M, int64_t V, const void *logits, int64_t ld, int rule,
+                 int64_t max_valid_id, const float *temperature, const float *top_p,
+                 const int32_t *top_k, const int32_t *bias_off, const int32_t *bias_ids,
+                 const float *bias_val, const uint8_t *active, uint64_t seed,
+                 const int64_t *rng_key, const int32_t *rng_ctr, int64_t *out_tok,
+                 float *out_logp, void *stream);
+
+/*
+ * In-place repetition penalty on float32 logits [M, V] (row stride ld): for
+ * every occurrence of an id in row m's history, logit / penalty if logit > 0
+ * else logit * penalty.  History of row m: hist[hist_off[m] .. hist_off[m+1])
+ * then, when hist2 is non-NULL, hist2[hist2_off[m] .. hist2_off[m] + hist2_len[m]).
+ * penalty == 1 or <= 0 is a no-op.  Replaces _apply_repetition_penalty
+ * (rwkvtune/inference/grpo_batch_generator.py:25-42).
+ */
+int rwkv7_repetition_penalty(int64_t M, int64_t V, float *logits, int64_t ld, float penalty,
+                             const int32_t *hist, const int64_t *hist_off, const int32_t *hist2,
+                             const int64_t *hist2_off, const int32_t *hist2_len,
+                             const uint8_t *active, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,6 +39,9 @@ SIGNATURES = {
     "rwkv7_tmix_prep": (_I32, [_I32, _I64, _I64, _I32] + [_P] * 6 + [_P, _P, _P, _P]),
     "rwkv7_tmix_post": (_I32, [_I32, _I64, _I64] + [_P] * 5 + [_P, _P, _P]),
     "rwkv7_tmix_decode": (_I32, [_I32, _I64, _I64, _I32] + [_P] * 7 + [_P, _P, _P, _I64, _P, _P, _P]),
+    "rwkv7_sample": (_I32, [_I32, _I64, _I64, _P, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P,
+                            ctypes.c_uint64, _P, _P, _P, _P, _P]),
+    "rwkv7_repetition_penalty": (_I32, [_I64, _I64, _P, _I64, ctypes.c_float, _P, _P, _P, _P, _P, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -278,3 +278,71 @@ extern "C" int rwkv7_tmix_decode(int dtype, int64_t M, int64_t H, int layer0, co
                                                   out, (hipStream_t)stream)));
     return launch_status(e, "tmix_decode_kernel");
 }
+
+// ---------------------------------------------------------------------------
+// Sampling (sampler.hip)
+// ---------------------------------------------------------------------------
+
+template <typename LT>
+hipError_t launch_sample(int M, int V, const void* logits, int64_t ld, int rule, int max_valid_id,
+                         const float* temperature, const float* top_p, const int32_t* top_k,
+                         const int32_t* bias_off, const int32_t* bias_ids, const float* bias_val,
+                         const uint8_t* active, uint64_t seed, const int64_t* rng_key,
+                         const int32_t* rng_ctr, int64_t* out_tok, float* out_logp, hipStream_t st);
+hipError_t launch_rep_penalty(int M, int V, float* logits, int64_t ld, float penalty, const int32_t* hist,
+                              const int64_t* hist_off, const int32_t* hist2, const int64_t* hist2_off,
+                              const int32_t* hist2_len, const uint8_t* active, hipStream_t st);
+int sampler_max_vocab();
+
+extern "C" int rwkv7_sample(int dtype, int64_t M, int64_t V, const void* logits, int64_t ld, int rule,
+                            int64_t max_valid_id, const float* temperature, const float* top_p,
+                            const int32_t* top_k, const int32_t* bias_off, const int32_t* bias_ids,
+                            const float* bias_val, const uint8_t* active, uint64_t seed,
+                            const int64_t* rng_key, const int32_t* rng_ctr, int64_t* out_tok,
+                            float* out_logp, void* stream) {
+    if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_sample: bad dtype code %d", dtype);
+    if (M < 0 || M > kMaxInt || V <= 0 || V > sampler_max_vocab() || ld < V)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_sample: bad sizes M=%lld V=%lld ld=%lld (V <= %d)", (long long)M,
+                    (long long)V, (long long)ld, sampler_max_vocab());
+    if (rule != 0 && rule != 1) return fail(RWKV7_ERR_INVALID, "rwkv7_sample: rule must be 0 (batch) or 1 (single)");
+    if (M == 0) return ok();
+    if (!logits || !temperature || !top_p || !top_k || !rng_key || !rng_ctr || !out_tok || !out_logp)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_sample: null pointer");
+    if (bias_off != nullptr && (bias_ids == nullptr || bias_val == nullptr))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_sample: bias_off needs bias_ids and bias_val");
+    const int mv = max_valid_id < 0 ? (int)(V - 1) : (int)(max_valid_id < V ? max_valid_id : V - 1);
+    hipError_t e;
+    switch (dtype) {
+        case RWKV7_DTYPE_F32:
+            e = launch_sample<float>((int)M, (int)V, logits, ld, rule, mv, temperature, top_p, top_k, bias_off,
+                                     bias_ids, bias_val, active, seed, rng_key, rng_ctr, out_tok, out_logp,
+                                     (hipStream_t)stream);
+            break;
+        case RWKV7_DTYPE_F16:
+            e = launch_sample<f16_t>((int)M, (int)V, logits, ld, rule, mv, temperature, top_p, top_k, bias_off,
+                                     bias_ids, bias_val, active, seed, rng_key, rng_ctr, out_tok, out_logp,
+                                     (hipStream_t)stream);
+            break;
+        default:
+            e = launch_sample<bf16_t>((int)M, (int)V, logits, ld, rule, mv, temperature, top_p, top_k, bias_off,
+                                      bias_ids, bias_val, active, seed, rng_key, rng_ctr, out_tok, out_logp,
+                                      (hipStream_t)stream);
+            break;
+    }
+    return launch_status(e, "sample_kernel");
+}
+
+extern "C" int rwkv7_repetition_penalty(int64_t M, int64_t V, float* logits, int64_t ld, float penalty,
+                                        const int32_t* hist, const int64_t* hist_off, const int32_t* hist2,
+                                        const int64_t* hist2_off, const int32_t* hist2_len,
+                                        const uint8_t* active, void* stream) {
+    if (M < 0 || M > kMaxInt || V <= 0 || V > kMaxInt || ld < V)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_repetition_penalty: bad sizes");
+    if (penalty == 1.0f || penalty <= 0.0f || M == 0) return ok();  // no-op, as the reference
+    if (!logits || !hist || !hist_off) return fail(RWKV7_ERR_INVALID, "rwkv7_repetition_penalty: null pointer");
+    if (hist2 != nullptr && (hist2_off == nullptr || hist2_len == nullptr))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_repetition_penalty: hist2 needs hist2_off and hist2_len");
+    return launch_status(launch_rep_penalty((int)M, (int)V, logits, ld, penalty, hist, hist_off, hist2, hist2_off,
+                                            hist2_len, active, (hipStream_t)stream),
+                         "rep_penalty_kernel");
+}

@@ -1,0 +1,168 @@
+"""GPU sampler (rwkv7_sample / rwkv7_repetition_penalty) against the CPU
+restatement of the reference's rules (oracle/sampler.py).
+
+Checks:
+  greedy: token ids identical (exact argmax, lowest index on ties); logp within 1e-4.
+  sampled rules: every draw lies in the oracle's kept set; the empirical
+      frequencies of 8192 draws of one row pass a chi-square test against the
+      oracle distribution (the draws are a fixed function of the seed, so the test
+      is deterministic; threshold = chi2 0.999 quantile); returned logp within
+      1e-4 of the oracle's log-probability of the drawn token.
+  repetition penalty: equal to the oracle to float32 rounding (1e-6 relative).
+"""
+
+import math
+
+import pytest
+import torch
+from scipy.stats import chi2
+
+from oracle import sampler as osm
+from rwkvtune_amd import sampler as dsm
+
+pytestmark = pytest.mark.gpu
+
+V = 65536
+
+
+def draws(gpu_device, row, n, *, temperature, top_p, top_k, rule, max_valid_id=None, logit_bias=None, seed=1):
+    logits = row.to(gpu_device).float().expand(n, -1).contiguous()
+    buf = dsm.SamplerBuffers(n, gpu_device)
+    buf.set_uniform(temperature, top_p, top_k)
+    buf.set_bias(logit_bias, n)
+    buf.rng_key.fill_(7)
+    buf.rng_ctr.copy_(torch.arange(n, dtype=torch.int32, device=gpu_device))
+    tok = torch.empty(n, dtype=torch.int64, device=gpu_device)
+    lp = torch.empty(n, dtype=torch.float32, device=gpu_device)
+    dsm.sample_rows(logits, buf, rule=rule, max_valid_id=max_valid_id, seed=seed, out_tok=tok, out_logp=lp)
+    torch.cuda.synchronize()
+    return tok.cpu(), lp.cpu()
+
+
+def peaked_row(seed, n_big=40):
+    """A row whose mass sits on ~n_big tokens (so 8192 draws resolve it)."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(V, generator=g) - 12.0
+    idx = torch.randperm(V, generator=g)[:n_big]
+    x[idx] = torch.randn(n_big, generator=g) * 1.2
+    return x
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_greedy_matches_argmax(gpu_device, dtype):
+    print(f"[case] greedy {dtype}", flush=True)
+    g = torch.Generator().manual_seed(3)
+    logits = (torch.randn(64, V, generator=g) * 3).to(dtype)
+    logits[5, 100] = logits[5, 200] = 50.0  # tie: lowest index wins
+    logits[6, 65534] = 80.0                  # banned id is never chosen
+    d = logits.to(gpu_device)
+    buf = dsm.SamplerBuffers(64, gpu_device)
+    buf.set_uniform(0.0, 1.0, 0)
+    tok = torch.empty(64, dtype=torch.int64, device=gpu_device)
+    lp = torch.empty(64, dtype=torch.float32, device=gpu_device)
+    dsm.sample_rows(d, buf, rule=osm.RULE_BATCH, max_valid_id=65529, seed=0, out_tok=tok, out_logp=lp)
+    torch.cuda.synchronize()
+    for i in range(64):
+        t, l = osm.greedy(logits[i].float(), max_valid_id=65529)
+        assert int(tok[i]) == t
+        assert abs(float(lp[i]) - l) < 1e-4
+    assert int(tok[5]) == 100 and int(tok[6]) != 65534
+
+
+CASES = [
+    # (rule, temperature, top_p, top_k)
+    (osm.RULE_BATCH, 1.0, 1.0, 0),
+    (osm.RULE_BATCH, 1.0, 0.95, 0),
+    (osm.RULE_BATCH, 0.7, 0.8, 0),
+    (osm.RULE_BATCH, 1.0, 1.0, 10),
+    (osm.RULE_BATCH, 1.3, 0.7, 12),
+    (osm.RULE_SINGLE, 1.0, 0.95, 0),
+    (osm.RULE_SINGLE, 0.9, 0.6, 0),
+    (osm.RULE_SINGLE, 1.0, 0.9, 8),
+    (osm.RULE_SINGLE, 1.0, 1.0, 0),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_sampled_distribution(gpu_device, case):
+    rule, temp, top_p, top_k = case
+    print(f"[case] sample rule={rule} T={temp} p={top_p} k={top_k}", flush=True)
+    row = peaked_row(100 + CASES.index(case))
+    n = 8192
+    tok, lp = draws(gpu_device, row, n, temperature=temp, top_p=top_p, top_k=top_k, rule=rule,
+                    max_valid_id=65529)
+    dist = osm.distribution(row, temperature=temp, top_p=top_p, top_k=top_k, max_valid_id=65529, rule=rule)
+    kept = dist > 0
+    assert bool(kept[tok].all()), "a draw fell outside the kept set"
+    for i in range(0, n, 257):
+        t = int(tok[i])
+        assert abs(float(lp[i]) - osm.logp(dist, t, rule)) < 1e-4
+    counts = torch.bincount(tok, minlength=V).double()
+    # chi-square over kept tokens with expected count >= 5, the rest pooled
+    exp = dist * n
+    big = exp >= 5
+    obs_b, exp_b = counts[big], exp[big]
+    stat = float(((obs_b - exp_b) ** 2 / exp_b).sum())
+    rest_e = float(exp[~big].sum())
+    dof = int(big.sum()) - 1
+    if rest_e > 0:
+        rest_o = float(counts[~big].sum())
+        stat += (rest_o - rest_e) ** 2 / max(rest_e, 1e-9)
+        dof += 1
+    assert stat < chi2.ppf(0.999, max(dof, 1)), f"chi2 {stat:.1f} dof {dof}"
+
+
+def test_bias_and_ban(gpu_device):
+    print("[case] logit bias and ban", flush=True)
+    row = peaked_row(7)
+    row[65531] = 30.0  # banned
+    tok, _ = draws(gpu_device, row, 1024, temperature=1.0, top_p=1.0, top_k=0, rule=osm.RULE_BATCH,
+                   max_valid_id=65529, logit_bias={"17": 100.0, "18": -1000.0})
+    assert int((tok == 17).sum()) > 1000
+    assert not bool((tok >= 65530).any())
+
+
+def test_token_sampler_api(gpu_device):
+    print("[case] TokenSampler API", flush=True)
+    dsm.TokenSampler._max_valid_token_id = 65529
+    try:
+        row = peaked_row(9).to(gpu_device)
+        t, l = dsm.TokenSampler.sample(row.clone(), temperature=0.0)
+        assert t == int(torch.argmax(row[:65530]))
+        t, l = dsm.TokenSampler.sample(row.clone(), temperature=1.0, top_p=0.9)
+        assert isinstance(t, int) and isinstance(l, float) and l <= 0
+        toks, lps = dsm.TokenSampler.sample_batch(row.expand(4, -1).contiguous(), temperature=0.8, top_p=0.95)
+        assert toks.shape == (4,) and toks.dtype == torch.int64 and lps.shape == (4,)
+        with pytest.raises(ValueError):
+            dsm.TokenSampler.sample(row.expand(2, -1))
+        with pytest.raises(ValueError):
+            dsm.TokenSampler.sample_batch(row)
+    finally:
+        dsm.TokenSampler._max_valid_token_id = None
+
+
+def test_repetition_penalty(gpu_device):
+    print("[case] repetition penalty", flush=True)
+    g = torch.Generator().manual_seed(5)
+    M, Vs = 8, 5000
+    logits = torch.randn(M, Vs, generator=g) * 4
+    hists = [torch.randint(0, Vs, (int(n),), generator=g).tolist() for n in torch.randint(0, 300, (M,), generator=g)]
+    hists[0] = [3, 3, 3, 7, 7]
+    gen = [torch.randint(0, Vs, (int(n),), generator=g).tolist() for n in torch.randint(0, 50, (M,), generator=g)]
+    flat = [t for h in hists for t in h]
+    off = [0]
+    for h in hists:
+        off.append(off[-1] + len(h))
+    gmax = 64
+    gbuf = torch.zeros(M, gmax, dtype=torch.int32)
+    for i, h in enumerate(gen):
+        gbuf[i, :len(h)] = torch.tensor(h, dtype=torch.int32)
+    d = logits.to(gpu_device)
+    dsm.repetition_penalty_(d, 1.3, torch.tensor(flat, dtype=torch.int32, device=gpu_device),
+                            torch.tensor(off, dtype=torch.int64, device=gpu_device),
+                            gbuf.reshape(-1).to(gpu_device),
+                            torch.arange(0, M * gmax, gmax, dtype=torch.int64, device=gpu_device),
+                            torch.tensor([len(h) for h in gen], dtype=torch.int32, device=gpu_device))
+    torch.cuda.synchronize()
+    ref = osm.repetition_penalty(logits, [h + q for h, q in zip(hists, gen)], 1.3)
+    assert torch.allclose(d.cpu().double(), ref, rtol=1e-6, atol=1e-6)
