@@ -191,15 +191,80 @@ int rwkv7_sample(int dtype, int64_t M, int64_t V, const void *logits, int64_t ld
 /*
  * In-place repetition penalty on float32 logits [M, V] (row stride ld): for
  * every occurrence of an id in row m's history, logit / penalty if logit > 0
- * else logit * penalty.  History of row m: hist[hist_off[m] .. hist_off[m+1])
- * then, when hist2 is non-NULL, hist2[hist2_off[m] .. hist2_off[m] + hist2_len[m]).
+ * else logit * penalty.  History of row m: hist[hist_start[m] .. + hist_len[m])
+ * then, when hist2 is non-NULL, hist2[hist2_start[m] .. + hist2_len[m]).
  * penalty == 1 or <= 0 is a no-op.  Replaces _apply_repetition_penalty
  * (rwkvtune/inference/grpo_batch_generator.py:25-42).
  */
 int rwkv7_repetition_penalty(int64_t M, int64_t V, float *logits, int64_t ld, float penalty,
-                             const int32_t *hist, const int64_t *hist_off, const int32_t *hist2,
-                             const int64_t *hist2_off, const int32_t *hist2_len,
-                             const uint8_t *active, void *stream);
+                             const int32_t *hist, const int64_t *hist_start, const int32_t *hist_len,
+                             const int32_t *hist2, const int64_t *hist2_start,
+                             const int32_t *hist2_len, const uint8_t *active, void *stream);
+
+/* ------------------------------------------------------------------------
+ * GPU slot table of the rollout.  Replaces the Python bookkeeping of the
+ * reference's decode loops - active-sequence lists, EOS / length retirement,
+ * admission of waiting sequences into free slots and the per-step state
+ * gather / scatter (rwkvtune/inference/grpo_batch_generator.py:458-610,
+ * rwkvtune/inference/scheduler_core.py:250-299, 363-395, 445-511) - so decode
+ * steps run back to back with no host round trip.
+ *
+ * Device tables (n sequences, S slots, maxlen token columns):
+ *   seq_prompt[n] int32   index of the sequence's prompt state in the store
+ *   seq_max_new[n] int32  token cap;  seq_ngen[n] int32  tokens so far
+ *   seq_done[n] uint8;    out_tok / out_logp / out_step [n, maxlen]
+ *                         (int32 / float32 / int32: token, its sampling
+ *                         log-probability, the decode step that made it)
+ *   slot_seq[S] int32     sequence in the slot, -1 = free
+ *   row_slot[S] int32     slot index or -1: the row_slot of the model kernels
+ *   tok_in[S] int64       next input token of the slot
+ *   counters[4] int32     next waiting sequence, finished sequences, decode
+ *                         steps committed, admissions of the current step
+ *   admit_slot / admit_src [S] int32: this step's admissions (slot <- store entry)
+ * ------------------------------------------------------------------------ */
+
+/* Record each sequence's first token (sampled from its prompt's last logits):
+ * out_tok[q][0] = tok[q], seq_ngen[q] = 1; with first_can_finish, EOS (eos >= 0)
+ * or a cap of 1 finishes the sequence (SchedulerCore); without it the first
+ * token never does (GRPOBatchGenerator, grpo_batch_generator.py:283-285). */
+int rwkv7_rollout_first(int64_t n, int64_t maxlen, const int64_t *tok, const float *logp,
+                        const int32_t *seq_max_new, int32_t *seq_ngen, uint8_t *seq_done,
+                        int32_t *out_tok, float *out_logp, int32_t *out_step, int64_t eos,
+                        int first_can_finish, int32_t *counters, void *stream);
+
+/* One block: with have_sample, append tok[s] / logp[s] to the sequence in slot
+ * s, finish it on EOS or its cap; then every free slot takes the next waiting,
+ * unfinished sequence (index order) and lists the state copy it needs.  S <= 1024. */
+int rwkv7_rollout_commit(int64_t S, int64_t n, int64_t maxlen, int have_sample, const int64_t *tok,
+                         const float *logp, int32_t *slot_seq, int32_t *row_slot, int64_t *tok_in,
+                         const int32_t *seq_prompt, const int32_t *seq_max_new, int32_t *seq_ngen,
+                         uint8_t *seq_done, int32_t *out_tok, float *out_logp, int32_t *out_step,
+                         int64_t eos, int32_t *counters, int32_t *admit_slot, int32_t *admit_src,
+                         void *stream);
+
+/* Per-slot sampler inputs of the step: active[s], rng_key[s] = sequence,
+ * rng_ctr[s] = its position; optionally (hist_start non-NULL) the two history
+ * segments of the repetition penalty (prompt ids in a packed prompt array at
+ * prompt_start[p] / prompt_len[p]; generated ids in out_tok), and optionally
+ * (seq_temp non-NULL) per-sequence temperature / top_p / top_k copied to the
+ * slot's row. */
+int rwkv7_rollout_prepare(int64_t S, int64_t maxlen, const int32_t *slot_seq, const int32_t *seq_ngen,
+                          const int32_t *seq_prompt, const int64_t *prompt_start,
+                          const int32_t *prompt_len, uint8_t *active, int64_t *rng_key,
+                          int32_t *rng_ctr, int64_t *hist_start, int32_t *hist_len,
+                          int64_t *hist2_start, int32_t *hist2_len, const float *seq_temp,
+                          const float *seq_top_p, const int32_t *seq_top_k, float *temp,
+                          float *top_p, int32_t *top_k, void *stream);
+
+/* Fork-on-admit: copy every layer's state (kv [L][U or S][kv_elems], att_x /
+ * ffn_x [L][U or S][C], float32) of store entry admit_src[i] into slot
+ * admit_slot[i], for the counters[3] admissions of the step.  Replaces the
+ * index copies of grpo_batch_generator.py:233-260 and the slot reset / load of
+ * scheduler_core.py:301-350. */
+int rwkv7_admit_copy(const int32_t *counters, const int32_t *admit_slot, const int32_t *admit_src,
+                     int64_t L, int64_t S, int64_t U, int64_t kv_elems, int64_t C,
+                     const float *src_kv, const float *src_ax, const float *src_fx,
+                     float *dst_kv, float *dst_ax, float *dst_fx, void *stream);
 
 #ifdef __cplusplus
 }

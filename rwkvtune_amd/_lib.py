@@ -41,7 +41,11 @@ SIGNATURES = {
     "rwkv7_tmix_decode": (_I32, [_I32, _I64, _I64, _I32] + [_P] * 7 + [_P, _P, _P, _I64, _P, _P, _P]),
     "rwkv7_sample": (_I32, [_I32, _I64, _I64, _P, _I64, _I32, _I64, _P, _P, _P, _P, _P, _P, _P,
                             ctypes.c_uint64, _P, _P, _P, _P, _P]),
-    "rwkv7_repetition_penalty": (_I32, [_I64, _I64, _P, _I64, ctypes.c_float, _P, _P, _P, _P, _P, _P, _P]),
+    "rwkv7_repetition_penalty": (_I32, [_I64, _I64, _P, _I64, ctypes.c_float] + [_P] * 7 + [_P]),
+    "rwkv7_rollout_first": (_I32, [_I64, _I64] + [_P] * 8 + [_I64, _I32, _P, _P]),
+    "rwkv7_rollout_commit": (_I32, [_I64, _I64, _I64, _I32] + [_P] * 12 + [_I64, _P, _P, _P, _P]),
+    "rwkv7_rollout_prepare": (_I32, [_I64, _I64] + [_P] * 18 + [_P]),
+    "rwkv7_admit_copy": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64] + [_P] * 6 + [_P]),
 }
 
 _lock = threading.Lock()

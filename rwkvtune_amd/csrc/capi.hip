@@ -290,8 +290,9 @@ hipError_t launch_sample(int M, int V, const void* logits, int64_t ld, int rule,
                          const uint8_t* active, uint64_t seed, const int64_t* rng_key,
                          const int32_t* rng_ctr, int64_t* out_tok, float* out_logp, hipStream_t st);
 hipError_t launch_rep_penalty(int M, int V, float* logits, int64_t ld, float penalty, const int32_t* hist,
-                              const int64_t* hist_off, const int32_t* hist2, const int64_t* hist2_off,
-                              const int32_t* hist2_len, const uint8_t* active, hipStream_t st);
+                              const int64_t* hist_start, const int32_t* hist_len, const int32_t* hist2,
+                              const int64_t* hist2_start, const int32_t* hist2_len, const uint8_t* active,
+                              hipStream_t st);
 int sampler_max_vocab();
 
 extern "C" int rwkv7_sample(int dtype, int64_t M, int64_t V, const void* logits, int64_t ld, int rule,
@@ -333,16 +334,110 @@ extern "C" int rwkv7_sample(int dtype, int64_t M, int64_t V, const void* logits,
 }
 
 extern "C" int rwkv7_repetition_penalty(int64_t M, int64_t V, float* logits, int64_t ld, float penalty,
-                                        const int32_t* hist, const int64_t* hist_off, const int32_t* hist2,
-                                        const int64_t* hist2_off, const int32_t* hist2_len,
-                                        const uint8_t* active, void* stream) {
+                                        const int32_t* hist, const int64_t* hist_start, const int32_t* hist_len,
+                                        const int32_t* hist2, const int64_t* hist2_start,
+                                        const int32_t* hist2_len, const uint8_t* active, void* stream) {
     if (M < 0 || M > kMaxInt || V <= 0 || V > kMaxInt || ld < V)
         return fail(RWKV7_ERR_INVALID, "rwkv7_repetition_penalty: bad sizes");
     if (penalty == 1.0f || penalty <= 0.0f || M == 0) return ok();  // no-op, as the reference
-    if (!logits || !hist || !hist_off) return fail(RWKV7_ERR_INVALID, "rwkv7_repetition_penalty: null pointer");
-    if (hist2 != nullptr && (hist2_off == nullptr || hist2_len == nullptr))
-        return fail(RWKV7_ERR_INVALID, "rwkv7_repetition_penalty: hist2 needs hist2_off and hist2_len");
-    return launch_status(launch_rep_penalty((int)M, (int)V, logits, ld, penalty, hist, hist_off, hist2, hist2_off,
-                                            hist2_len, active, (hipStream_t)stream),
+    if (!logits || !hist || !hist_start || !hist_len)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_repetition_penalty: null pointer");
+    if (hist2 != nullptr && (hist2_start == nullptr || hist2_len == nullptr))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_repetition_penalty: hist2 needs hist2_start and hist2_len");
+    return launch_status(launch_rep_penalty((int)M, (int)V, logits, ld, penalty, hist, hist_start, hist_len, hist2,
+                                            hist2_start, hist2_len, active, (hipStream_t)stream),
                          "rep_penalty_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// Slot table (slots.hip)
+// ---------------------------------------------------------------------------
+
+hipError_t launch_rollout_first(int n, int maxlen, const int64_t* tok, const float* logp, const int32_t* seq_max_new,
+                                int32_t* seq_ngen, uint8_t* seq_done, int32_t* out_tok, float* out_logp,
+                                int32_t* out_step, int64_t eos, int first_can_finish, int32_t* counters,
+                                hipStream_t st);
+hipError_t launch_rollout_commit(int S, int n, int maxlen, int have_sample, const int64_t* tok, const float* logp,
+                                 int32_t* slot_seq, int32_t* row_slot, int64_t* tok_in, const int32_t* seq_prompt,
+                                 const int32_t* seq_max_new, int32_t* seq_ngen, uint8_t* seq_done,
+                                 int32_t* out_tok, float* out_logp, int32_t* out_step, int64_t eos,
+                                 int32_t* counters, int32_t* admit_slot, int32_t* admit_src, hipStream_t st);
+hipError_t launch_rollout_prepare(int S, int maxlen, const int32_t* slot_seq, const int32_t* seq_ngen,
+                                  const int32_t* seq_prompt, const int64_t* prompt_start,
+                                  const int32_t* prompt_len, uint8_t* active, int64_t* rng_key,
+                                  int32_t* rng_ctr, int64_t* hist_start, int32_t* hist_len,
+                                  int64_t* hist2_start, int32_t* hist2_len, const float* seq_temp,
+                                  const float* seq_top_p, const int32_t* seq_top_k, float* temp, float* top_p,
+                                  int32_t* top_k, hipStream_t st);
+hipError_t launch_admit_copy(const int32_t* counters, const int32_t* admit_slot, const int32_t* admit_src, int L,
+                             int S, int U, int64_t kv_elems, int64_t C, const float* src_kv, const float* src_ax,
+                             const float* src_fx, float* dst_kv, float* dst_ax, float* dst_fx, hipStream_t st);
+
+extern "C" int rwkv7_rollout_first(int64_t n, int64_t maxlen, const int64_t* tok, const float* logp,
+                                   const int32_t* seq_max_new, int32_t* seq_ngen, uint8_t* seq_done,
+                                   int32_t* out_tok, float* out_logp, int32_t* out_step, int64_t eos,
+                                   int first_can_finish, int32_t* counters, void* stream) {
+    if (n < 0 || n > kMaxInt || maxlen < 1 || maxlen > kMaxInt || n * maxlen > ((int64_t)1 << 40))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_first: bad sizes");
+    if (n == 0) return ok();
+    if (!tok || !logp || !seq_max_new || !seq_ngen || !seq_done || !out_tok || !out_logp || !counters)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_first: null pointer");
+    return launch_status(launch_rollout_first((int)n, (int)maxlen, tok, logp, seq_max_new, seq_ngen, seq_done, out_tok,
+                                              out_logp, out_step, eos, first_can_finish, counters,
+                                              (hipStream_t)stream),
+                         "rollout_first_kernel");
+}
+
+extern "C" int rwkv7_rollout_commit(int64_t S, int64_t n, int64_t maxlen, int have_sample, const int64_t* tok,
+                                    const float* logp, int32_t* slot_seq, int32_t* row_slot, int64_t* tok_in,
+                                    const int32_t* seq_prompt, const int32_t* seq_max_new, int32_t* seq_ngen,
+                                    uint8_t* seq_done, int32_t* out_tok, float* out_logp, int32_t* out_step,
+                                    int64_t eos, int32_t* counters, int32_t* admit_slot, int32_t* admit_src,
+                                    void* stream) {
+    if (S < 1 || S > 1024 || n < 0 || n > kMaxInt || maxlen < 1 || maxlen > kMaxInt)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_commit: bad sizes (1 <= S <= 1024)");
+    if (have_sample && (!tok || !logp)) return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_commit: null sample");
+    if (!slot_seq || !row_slot || !tok_in || !seq_prompt || !seq_max_new || !seq_ngen || !seq_done || !out_tok ||
+        !out_logp || !counters || !admit_slot || !admit_src)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_commit: null pointer");
+    return launch_status(launch_rollout_commit((int)S, (int)n, (int)maxlen, have_sample, tok, logp, slot_seq, row_slot,
+                                               tok_in, seq_prompt, seq_max_new, seq_ngen, seq_done, out_tok,
+                                               out_logp, out_step, eos, counters, admit_slot, admit_src,
+                                               (hipStream_t)stream),
+                         "rollout_commit_kernel");
+}
+
+extern "C" int rwkv7_rollout_prepare(int64_t S, int64_t maxlen, const int32_t* slot_seq, const int32_t* seq_ngen,
+                                     const int32_t* seq_prompt, const int64_t* prompt_start,
+                                     const int32_t* prompt_len, uint8_t* active, int64_t* rng_key,
+                                     int32_t* rng_ctr, int64_t* hist_start, int32_t* hist_len,
+                                     int64_t* hist2_start, int32_t* hist2_len, const float* seq_temp,
+                                     const float* seq_top_p, const int32_t* seq_top_k, float* temp,
+                                     float* top_p, int32_t* top_k, void* stream) {
+    if (S < 1 || S > kMaxInt || maxlen < 1 || maxlen > kMaxInt)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_prepare: bad sizes");
+    if (!slot_seq || !seq_ngen || !active || !rng_key || !rng_ctr)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_prepare: null pointer");
+    if (hist_start && (!seq_prompt || !prompt_start || !prompt_len || !hist_len || !hist2_start || !hist2_len))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_prepare: history outputs need the prompt table");
+    if (seq_temp && (!seq_top_p || !seq_top_k || !temp || !top_p || !top_k))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_prepare: per-sequence parameters come as a set");
+    return launch_status(launch_rollout_prepare((int)S, (int)maxlen, slot_seq, seq_ngen, seq_prompt, prompt_start,
+                                                prompt_len, active, rng_key, rng_ctr, hist_start, hist_len,
+                                                hist2_start, hist2_len, seq_temp, seq_top_p, seq_top_k, temp,
+                                                top_p, top_k, (hipStream_t)stream),
+                         "rollout_prepare_kernel");
+}
+
+extern "C" int rwkv7_admit_copy(const int32_t* counters, const int32_t* admit_slot, const int32_t* admit_src,
+                                int64_t L, int64_t S, int64_t U, int64_t kv_elems, int64_t C, const float* src_kv,
+                                const float* src_ax, const float* src_fx, float* dst_kv, float* dst_ax,
+                                float* dst_fx, void* stream) {
+    if (L < 1 || S < 1 || U < 1 || kv_elems < 4 || (kv_elems % 4) || C < 4 || (C % 4) || S > kMaxInt || U > kMaxInt)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_admit_copy: bad sizes");
+    if (!counters || !admit_slot || !admit_src || !src_kv || !src_ax || !src_fx || !dst_kv || !dst_ax || !dst_fx)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_admit_copy: null pointer");
+    return launch_status(launch_admit_copy(counters, admit_slot, admit_src, (int)L, (int)S, (int)U, kv_elems, C,
+                                           src_kv, src_ax, src_fx, dst_kv, dst_ax, dst_fx, (hipStream_t)stream),
+                         "admit_copy_kernel");
 }

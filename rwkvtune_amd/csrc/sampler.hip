@@ -344,15 +344,16 @@ __global__ __launch_bounds__(kT) void greedy_kernel(
 
 // Repetition penalty, in place, once per occurrence of each id in the row's
 // history (grpo_batch_generator.py:25-42): logit / p if logit > 0 else logit * p.
-// The history of row m is hist[hist_off[m] .. hist_off[m+1]) followed by
-// hist2[hist2_off[m] .. hist2_off[m] + hist2_len[m]) (nullable second segment).
-// Repeated applications to one logit commute, so the atomic updates give the
-// same result in any order.
+// The history of row m is hist[hist_start[m] .. + hist_len[m]) followed by
+// hist2[hist2_start[m] .. + hist2_len[m]) (second segment nullable).  Repeated
+// applications to one logit commute (the sign never changes), so the atomic
+// updates give the same result in any order.
 __global__ __launch_bounds__(256) void rep_penalty_kernel(
     int M, int V, float* __restrict__ logits, int64_t ld, float penalty,
-    const int32_t* __restrict__ hist, const int64_t* __restrict__ hist_off,
-    const int32_t* __restrict__ hist2, const int64_t* __restrict__ hist2_off,
-    const int32_t* __restrict__ hist2_len, const uint8_t* __restrict__ active)
+    const int32_t* __restrict__ hist, const int64_t* __restrict__ hist_start,
+    const int32_t* __restrict__ hist_len, const int32_t* __restrict__ hist2,
+    const int64_t* __restrict__ hist2_start, const int32_t* __restrict__ hist2_len,
+    const uint8_t* __restrict__ active)
 {
     const int row = blockIdx.x;
     if (active != nullptr && active[row] == 0) return;
@@ -368,10 +369,11 @@ __global__ __launch_bounds__(256) void rep_penalty_kernel(
             old = atomicCAS(addr, assumed, __float_as_uint(nf));
         } while (old != assumed);
     };
-    const int64_t a0 = hist_off[row], a1 = hist_off[row + 1];
+    const int64_t a0 = hist_start[row];
+    const int64_t a1 = a0 + hist_len[row];
     for (int64_t q = a0 + threadIdx.x; q < a1; q += blockDim.x) apply(hist[q]);
     if (hist2 != nullptr) {
-        const int64_t b0 = hist2_off[row];
+        const int64_t b0 = hist2_start[row];
         const int64_t b1 = b0 + hist2_len[row];
         for (int64_t q = b0 + threadIdx.x; q < b1; q += blockDim.x) apply(hist2[q]);
     }
@@ -410,11 +412,12 @@ template hipError_t launch_sample<f16_t>(int, int, const void*, int64_t, int, in
                                          float*, hipStream_t);
 
 hipError_t launch_rep_penalty(int M, int V, float* logits, int64_t ld, float penalty, const int32_t* hist,
-                              const int64_t* hist_off, const int32_t* hist2, const int64_t* hist2_off,
-                              const int32_t* hist2_len, const uint8_t* active, hipStream_t st)
+                              const int64_t* hist_start, const int32_t* hist_len, const int32_t* hist2,
+                              const int64_t* hist2_start, const int32_t* hist2_len, const uint8_t* active,
+                              hipStream_t st)
 {
-    hipLaunchKernelGGL(rep_penalty_kernel, dim3(M), dim3(256), 0, st, M, V, logits, ld, penalty, hist, hist_off,
-                       hist2, hist2_off, hist2_len, active);
+    hipLaunchKernelGGL(rep_penalty_kernel, dim3(M), dim3(256), 0, st, M, V, logits, ld, penalty, hist, hist_start,
+                       hist_len, hist2, hist2_start, hist2_len, active);
     return hipGetLastError();
 }
 

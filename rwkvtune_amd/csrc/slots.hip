@@ -1,0 +1,226 @@
+// GPU-resident slot table for ragged continuous-batching rollout.
+//
+// The reference keeps this bookkeeping in Python: finished sequences leave the
+// decode batch and free their slot, waiting sequences take free slots, and every
+// step reads each sampled token back to the host (.item() per sequence,
+// rwkvtune/inference/grpo_batch_generator.py:458-610,
+// rwkvtune/inference/scheduler_core.py:250-299, 363-371, 445-511).  Here it is
+// device state updated by kernels inside the decode step, so steps run back to
+// back with no host round trip:
+//
+//   sequence table  seq_prompt[n] (index of the prefilled prompt state),
+//                   seq_max_new[n], seq_ngen[n], seq_done[n],
+//                   out_tok / out_logp / out_step [n, maxlen]
+//   slot table      slot_seq[S] (-1 = free), row_slot[S] (slot or -1, what the
+//                   model kernels read), tok_in[S] (next input token)
+//   counters        [0] next waiting sequence, [1] finished sequences,
+//                   [2] decode steps committed, [3] admissions of this step
+//   admit list      admit_slot[S], admit_src[S] for the state copy
+//
+// Admission takes waiting sequences in index order (sequences finished at their
+// first token are skipped); a sequence's tokens depend only on its own state and
+// its (sequence, position) random stream, never on which slot it runs in.
+#include "common.hpp"
+
+namespace {
+
+enum { C_NEXT = 0, C_DONE = 1, C_STEP = 2, C_NADMIT = 3 };
+
+// First generated token of every sequence (sampled from its prompt's logits).
+__global__ void rollout_first_kernel(int n, int maxlen, const int64_t* __restrict__ tok,
+                                     const float* __restrict__ logp, const int32_t* __restrict__ seq_max_new,
+                                     int32_t* __restrict__ seq_ngen, uint8_t* __restrict__ seq_done,
+                                     int32_t* __restrict__ out_tok, float* __restrict__ out_logp,
+                                     int32_t* __restrict__ out_step, int64_t eos, int first_can_finish,
+                                     int32_t* __restrict__ counters)
+{
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= n) return;
+    const int64_t t = tok[q];
+    out_tok[(size_t)q * maxlen] = (int32_t)t;
+    out_logp[(size_t)q * maxlen] = logp[q];
+    if (out_step != nullptr) out_step[(size_t)q * maxlen] = 0;
+    seq_ngen[q] = 1;
+    const bool fin = first_can_finish && ((eos >= 0 && t == eos) || seq_max_new[q] <= 1 || maxlen <= 1);
+    seq_done[q] = fin ? 1 : 0;
+    if (fin) atomicAdd(&counters[C_DONE], 1);
+}
+
+// One block of >= S threads.  Commits the step's sampled tokens (have_sample),
+// retires finished sequences and admits waiting ones into free slots.
+__global__ __launch_bounds__(1024) void rollout_commit_kernel(
+    int S, int n, int maxlen, int have_sample, const int64_t* __restrict__ tok,
+    const float* __restrict__ logp, int32_t* __restrict__ slot_seq, int32_t* __restrict__ row_slot,
+    int64_t* __restrict__ tok_in, const int32_t* __restrict__ seq_prompt,
+    const int32_t* __restrict__ seq_max_new, int32_t* __restrict__ seq_ngen, uint8_t* __restrict__ seq_done,
+    int32_t* __restrict__ out_tok, float* __restrict__ out_logp, int32_t* __restrict__ out_step, int64_t eos,
+    int32_t* __restrict__ counters, int32_t* __restrict__ admit_slot, int32_t* __restrict__ admit_src)
+{
+    const int s = threadIdx.x;
+    if (s == 0) atomicExch(&counters[C_NADMIT], 0);
+    __syncthreads();
+    const int step = counters[C_STEP];
+    if (s < S) {
+        const int q = slot_seq[s];
+        bool admit = q < 0;
+        if (q >= 0 && have_sample) {
+            const int64_t t = tok[s];
+            const int pos = seq_ngen[q];
+            if (pos < maxlen) {
+                out_tok[(size_t)q * maxlen + pos] = (int32_t)t;
+                out_logp[(size_t)q * maxlen + pos] = logp[s];
+                if (out_step != nullptr) out_step[(size_t)q * maxlen + pos] = step + 1;
+            }
+            seq_ngen[q] = pos + 1;
+            const bool fin = (eos >= 0 && t == eos) || pos + 1 >= seq_max_new[q] || pos + 1 >= maxlen;
+            if (fin) {
+                seq_done[q] = 1;
+                atomicAdd(&counters[C_DONE], 1);
+                admit = true;
+            } else {
+                tok_in[s] = t;
+            }
+        }
+        if (admit) {
+            int q2;
+            for (;;) {
+                q2 = atomicAdd(&counters[C_NEXT], 1);
+                if (q2 >= n || !seq_done[q2]) break;
+            }
+            if (q2 >= n) {
+                slot_seq[s] = -1;
+                row_slot[s] = -1;
+                tok_in[s] = 0;
+            } else {
+                slot_seq[s] = q2;
+                row_slot[s] = s;
+                const int last = seq_ngen[q2] - 1;
+                tok_in[s] = out_tok[(size_t)q2 * maxlen + (last < 0 ? 0 : last)];
+                const int i = atomicAdd(&counters[C_NADMIT], 1);
+                admit_slot[i] = s;
+                admit_src[i] = seq_prompt[q2];
+            }
+        }
+    }
+    __syncthreads();
+    if (s == 0 && have_sample) counters[C_STEP] = step + 1;
+}
+
+// Per-slot inputs of the sampler and the repetition penalty for this step.
+// seq_temp / seq_top_p / seq_top_k (nullable together): per-sequence sampling
+// parameters copied to the slot's row.
+__global__ void rollout_prepare_kernel(int S, int maxlen, const int32_t* __restrict__ slot_seq,
+                                       const int32_t* __restrict__ seq_ngen,
+                                       const int32_t* __restrict__ seq_prompt,
+                                       const int64_t* __restrict__ prompt_start,
+                                       const int32_t* __restrict__ prompt_len, uint8_t* __restrict__ active,
+                                       int64_t* __restrict__ rng_key, int32_t* __restrict__ rng_ctr,
+                                       int64_t* __restrict__ hist_start, int32_t* __restrict__ hist_len,
+                                       int64_t* __restrict__ hist2_start, int32_t* __restrict__ hist2_len,
+                                       const float* __restrict__ seq_temp, const float* __restrict__ seq_top_p,
+                                       const int32_t* __restrict__ seq_top_k, float* __restrict__ temp,
+                                       float* __restrict__ top_p, int32_t* __restrict__ top_k)
+{
+    const int s = blockIdx.x * blockDim.x + threadIdx.x;
+    if (s >= S) return;
+    const int q = slot_seq[s];
+    const bool on = q >= 0;
+    active[s] = on ? 1 : 0;
+    rng_key[s] = on ? q : 0;
+    rng_ctr[s] = on ? seq_ngen[q] : 0;
+    if (seq_temp != nullptr && on) {
+        temp[s] = seq_temp[q];
+        top_p[s] = seq_top_p[q];
+        top_k[s] = seq_top_k[q];
+    }
+    if (hist_start != nullptr) {
+        const int p = on ? seq_prompt[q] : 0;
+        hist_start[s] = on ? prompt_start[p] : 0;
+        hist_len[s] = on ? prompt_len[p] : 0;
+        hist2_start[s] = on ? (int64_t)q * maxlen : 0;
+        hist2_len[s] = on ? seq_ngen[q] : 0;
+    }
+}
+
+// Copy the prefilled prompt state admit_src[i] into slot admit_slot[i], every
+// layer: kv [L, U|S, kv_elems], att_x / ffn_x [L, U|S, C].  Fixed grid; the
+// blocks stride over the admissions counted by the commit kernel.
+__global__ __launch_bounds__(256) void admit_copy_kernel(
+    const int32_t* __restrict__ counters, const int32_t* __restrict__ admit_slot,
+    const int32_t* __restrict__ admit_src, int L, int S, int U, int64_t kv4, int64_t c4,
+    const f32x4* __restrict__ src_kv, const f32x4* __restrict__ src_ax, const f32x4* __restrict__ src_fx,
+    f32x4* __restrict__ dst_kv, f32x4* __restrict__ dst_ax, f32x4* __restrict__ dst_fx)
+{
+    const int na = counters[C_NADMIT];
+    const int64_t per = kv4 + 2 * c4;  // float4s of one (slot, layer)
+    const int64_t total = (int64_t)na * L * per;
+    for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < total;
+         w += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t a = w / ((int64_t)L * per);
+        const int64_t rem = w - a * (int64_t)L * per;
+        const int l = (int)(rem / per);
+        const int64_t e = rem - (int64_t)l * per;
+        const int ds = admit_slot[a];
+        const int ss = admit_src[a];
+        if (ds < 0 || ds >= S || ss < 0 || ss >= U) continue;
+        if (e < kv4) {
+            dst_kv[((int64_t)l * S + ds) * kv4 + e] = src_kv[((int64_t)l * U + ss) * kv4 + e];
+        } else if (e < kv4 + c4) {
+            const int64_t c = e - kv4;
+            dst_ax[((int64_t)l * S + ds) * c4 + c] = src_ax[((int64_t)l * U + ss) * c4 + c];
+        } else {
+            const int64_t c = e - kv4 - c4;
+            dst_fx[((int64_t)l * S + ds) * c4 + c] = src_fx[((int64_t)l * U + ss) * c4 + c];
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_rollout_first(int n, int maxlen, const int64_t* tok, const float* logp, const int32_t* seq_max_new,
+                                int32_t* seq_ngen, uint8_t* seq_done, int32_t* out_tok, float* out_logp,
+                                int32_t* out_step, int64_t eos, int first_can_finish, int32_t* counters,
+                                hipStream_t st)
+{
+    hipLaunchKernelGGL(rollout_first_kernel, dim3((n + 255) / 256), dim3(256), 0, st, n, maxlen, tok, logp,
+                       seq_max_new, seq_ngen, seq_done, out_tok, out_logp, out_step, eos, first_can_finish,
+                       counters);
+    return hipGetLastError();
+}
+
+hipError_t launch_rollout_commit(int S, int n, int maxlen, int have_sample, const int64_t* tok, const float* logp,
+                                 int32_t* slot_seq, int32_t* row_slot, int64_t* tok_in, const int32_t* seq_prompt,
+                                 const int32_t* seq_max_new, int32_t* seq_ngen, uint8_t* seq_done,
+                                 int32_t* out_tok, float* out_logp, int32_t* out_step, int64_t eos,
+                                 int32_t* counters, int32_t* admit_slot, int32_t* admit_src, hipStream_t st)
+{
+    const int threads = ((S + 63) / 64) * 64;
+    hipLaunchKernelGGL(rollout_commit_kernel, dim3(1), dim3(threads), 0, st, S, n, maxlen, have_sample, tok, logp,
+                       slot_seq, row_slot, tok_in, seq_prompt, seq_max_new, seq_ngen, seq_done, out_tok,
+                       out_logp, out_step, eos, counters, admit_slot, admit_src);
+    return hipGetLastError();
+}
+
+hipError_t launch_rollout_prepare(int S, int maxlen, const int32_t* slot_seq, const int32_t* seq_ngen,
+                                  const int32_t* seq_prompt, const int64_t* prompt_start,
+                                  const int32_t* prompt_len, uint8_t* active, int64_t* rng_key,
+                                  int32_t* rng_ctr, int64_t* hist_start, int32_t* hist_len,
+                                  int64_t* hist2_start, int32_t* hist2_len, const float* seq_temp,
+                                  const float* seq_top_p, const int32_t* seq_top_k, float* temp, float* top_p,
+                                  int32_t* top_k, hipStream_t st)
+{
+    hipLaunchKernelGGL(rollout_prepare_kernel, dim3((S + 255) / 256), dim3(256), 0, st, S, maxlen, slot_seq,
+                       seq_ngen, seq_prompt, prompt_start, prompt_len, active, rng_key, rng_ctr, hist_start,
+                       hist_len, hist2_start, hist2_len, seq_temp, seq_top_p, seq_top_k, temp, top_p, top_k);
+    return hipGetLastError();
+}
+
+hipError_t launch_admit_copy(const int32_t* counters, const int32_t* admit_slot, const int32_t* admit_src, int L,
+                             int S, int U, int64_t kv_elems, int64_t C, const float* src_kv, const float* src_ax,
+                             const float* src_fx, float* dst_kv, float* dst_ax, float* dst_fx, hipStream_t st)
+{
+    hipLaunchKernelGGL(admit_copy_kernel, dim3(1024), dim3(256), 0, st, counters, admit_slot, admit_src, L, S, U,
+                       kv_elems / 4, C / 4, (const f32x4*)src_kv, (const f32x4*)src_ax, (const f32x4*)src_fx,
+                       (f32x4*)dst_kv, (f32x4*)dst_ax, (f32x4*)dst_fx);
+    return hipGetLastError();
+}

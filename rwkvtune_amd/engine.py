@@ -1,0 +1,338 @@
+"""Device-resident rollout engine: ragged prefill, fork-on-admit into a slot
+pool, and a decode loop whose slot bookkeeping never leaves the GPU.
+
+Used by the drop-in front ends (``GRPOBatchGenerator``, ``SchedulerCore``,
+``BatchGenerator``).  One ``run`` is:
+
+1. **Prefill** every distinct prompt once (ragged, packed, no padding and no
+   length grouping) into a *prompt store* - a ``StatePool`` with one entry per
+   distinct prompt - in passes of at most ``chunk_size`` tokens per prompt and
+   ``max_batch_tokens`` tokens per forward.  The logits of each prompt's last
+   token are kept.  (The reference prefills per exact-length group,
+   ``grpo_batch_generator.py:353-431``, and the scheduler per slot,
+   ``scheduler_core.py:513-600``.)
+2. **First token** of every sequence from its prompt's logits, all sequences in
+   one sampler launch (``grpo_batch_generator.py:262-310``).
+3. **Decode**: ``n_slots`` slots hold live sequences.  A step is the model's
+   fused single-token forward over every slot, the sampler, and the commit
+   kernel that appends tokens, retires finished sequences (EOS or per-sequence
+   length) and admits waiting ones into the freed slots by copying their
+   prompt's state from the store (fork-on-admit: G generations of one prompt
+   share one prefill).  The step is captured once in a HIP graph and replayed;
+   the host only polls the finished-sequence counter every few steps through an
+   asynchronous copy, so steps run back to back.
+4. **Collect**: one copy of the token table back to the host.
+
+Every sequence's tokens depend only on its prompt state and its own
+(sequence, position) random stream, so results do not depend on slot
+assignment, slot count or polling cadence.
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence
+
+import torch
+
+from . import _lib
+from .model import RWKV7Model, StatePool
+from .sampler import RULE_BATCH, RULE_SINGLE, SamplerBuffers, repetition_penalty_, sample_rows
+
+C_NEXT, C_DONE, C_STEP, C_NADMIT = 0, 1, 2, 3
+
+
+@dataclass
+class RolloutResult:
+    tokens: List[List[int]]            # generated ids per sequence
+    logps: List[List[float]]           # sampling log-probabilities per token
+    steps: List[List[int]]             # decode step that produced each token (0 = prefill)
+    n_decode_steps: int
+    timings: Dict[str, float] = field(default_factory=dict)
+    prompt_tokens: int = 0
+
+
+def _i32(x, dev):
+    return torch.as_tensor(x, dtype=torch.int32).to(dev)
+
+
+class RolloutEngine:
+    """Slot-pool rollout on one GPU for a ``RWKV7Model``."""
+
+    def __init__(self, model: RWKV7Model, n_slots: int, *, eos_token_id: Optional[int] = None,
+                 max_valid_id: Optional[int] = None, use_graph: bool = True, poll_every: int = 8):
+        if n_slots < 1 or n_slots > 1024:
+            raise ValueError("n_slots must be in [1, 1024]")
+        self.model = model
+        self.n_slots = n_slots
+        self.eos = -1 if eos_token_id is None else int(eos_token_id)
+        self.max_valid_id = max_valid_id
+        self.use_graph = use_graph
+        self.poll_every = max(1, int(poll_every))
+        self.dev = model.device
+        self.pool = None
+
+    # -- prefill ---------------------------------------------------------------
+
+    def prefill_store(self, prompts: Sequence[Sequence[int]], chunk_size: int, max_batch_tokens: int,
+                      max_seqs_per_forward: int = 0):
+        """Prefill ``prompts`` into a new store; returns (store, last-token logits [U, V] float32)."""
+        m = self.model
+        dev = self.dev
+        U = len(prompts)
+        store = StatePool(m.config, U, dev)
+        V = m.config.vocab_size
+        last_logits = torch.empty((U, V), dtype=torch.float32, device=dev)
+        lens = [len(p) for p in prompts]
+        if any(L == 0 for L in lens):
+            raise ValueError("empty prompts are not supported")
+        chunk = max(1, int(chunk_size))
+        budget = max(1, int(max_batch_tokens))
+        off = [0] * U
+        while True:
+            pending = [u for u in range(U) if off[u] < lens[u]]
+            if not pending:
+                break
+            # one pass: every pending prompt advances by up to `chunk` tokens,
+            # split into forwards of at most `budget` tokens
+            group, gtok = [], 0
+            groups = []
+            for u in pending:
+                n = min(chunk, lens[u] - off[u], budget)
+                if group and (gtok + n > budget or 0 < max_seqs_per_forward <= len(group)):
+                    groups.append(group)
+                    group, gtok = [], 0
+                group.append((u, n))
+                gtok += n
+            if group:
+                groups.append(group)
+            for grp in groups:
+                self._prefill_group(prompts, grp, off, lens, store, last_logits)
+            for grp in groups:
+                for u, n in grp:
+                    off[u] += n
+        return store, last_logits
+
+    def _prefill_group(self, prompts, grp, off, lens, store, last_logits):
+        dev = self.dev
+        toks, row_slot, row_last, cu, seq_slot, logit_rows, logit_dst = [], [], [], [0], [], [], []
+        for u, n in grp:
+            base = cu[-1]
+            toks.extend(prompts[u][off[u]:off[u] + n])
+            row_slot.extend([u] * n)
+            row_last.extend([base + n - 1] + [-1] * (n - 1))
+            cu.append(base + n)
+            seq_slot.append(u)
+            if off[u] + n == lens[u]:
+                logit_rows.append(base + n - 1)
+                logit_dst.append(u)
+        tokens = torch.tensor(toks, dtype=torch.int64).to(dev, non_blocking=True)
+        out = self.model.forward_pooled(tokens, _i32(row_slot, dev), _i32(row_last, dev), store, decode=False,
+                                        cu_seqlens=_i32(cu, dev), seq_slot=_i32(seq_slot, dev),
+                                        logit_rows=_i32(logit_rows, dev), n_logit_rows=len(logit_rows))
+        if logit_rows:
+            last_logits[torch.tensor(logit_dst, device=dev)] = out.float()
+
+    # -- full rollout ------------------------------------------------------------
+
+    @torch.no_grad()
+    def run(self, prompts: Sequence[Sequence[int]], seq_prompt: Sequence[int], max_new_tokens,
+            *, temperature: float = 1.0, top_p: float = 1.0, top_k: int = 0, logit_bias: Optional[dict] = None,
+            repetition_penalty: float = 1.0, first_rule: int = RULE_SINGLE, decode_rule: int = RULE_BATCH,
+            first_can_finish: bool = True, chunk_size: int = 2048, max_batch_tokens: int = 1 << 20,
+            seed: int = 0, max_len_cap: Optional[int] = None, per_seq_sampling=None,
+            max_seqs_per_forward: int = 0) -> RolloutResult:
+        """Roll out ``len(seq_prompt)`` sequences; sequence q continues prompt
+        ``prompts[seq_prompt[q]]``.  ``per_seq_sampling``: optional
+        ``(temperature[n], top_p[n], top_k[n])`` overriding the scalars per sequence."""
+        m = self.model
+        dev = self.dev
+        V = m.config.vocab_size
+        n = len(seq_prompt)
+        S = self.n_slots
+        if isinstance(max_new_tokens, int):
+            max_new = [int(max_new_tokens)] * n
+        else:
+            max_new = [int(x) for x in max_new_tokens]
+        if n == 0:
+            return RolloutResult([], [], [], 0)
+        if min(max_new) < 1:
+            raise ValueError("max_new_tokens must be >= 1")
+        # a sequence whose first token cannot finish it makes at least one decode step
+        maxlen = max(max(max_new), 1 if first_can_finish else 2)
+        if max_len_cap is not None:
+            maxlen = min(maxlen, max_len_cap)
+        timings = {}
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+
+        # 1. prefill distinct prompts
+        store, last_logits = self.prefill_store(prompts, chunk_size, max_batch_tokens, max_seqs_per_forward)
+        torch.cuda.synchronize(dev)
+        t1 = time.perf_counter()
+        timings["prefill_s"] = t1 - t0
+
+        # sequence table
+        sp = _i32(seq_prompt, dev)
+        seq_max_new = _i32(max_new, dev)
+        seq_ngen = torch.zeros(n, dtype=torch.int32, device=dev)
+        seq_done = torch.zeros(n, dtype=torch.uint8, device=dev)
+        out_tok = torch.zeros((n, maxlen), dtype=torch.int32, device=dev)
+        out_lp = torch.zeros((n, maxlen), dtype=torch.float32, device=dev)
+        out_step = torch.zeros((n, maxlen), dtype=torch.int32, device=dev)
+        counters = torch.zeros(4, dtype=torch.int32, device=dev)
+        # prompt table for the repetition penalty
+        plen = [len(p) for p in prompts]
+        pstart = [0]
+        for L in plen[:-1]:
+            pstart.append(pstart[-1] + L)
+        use_pen = repetition_penalty != 1.0 and repetition_penalty > 0
+        if use_pen:
+            flat = torch.tensor([t for p in prompts for t in p], dtype=torch.int32).to(dev)
+            p_start = torch.tensor(pstart, dtype=torch.int64).to(dev)
+            p_len = _i32(plen, dev)
+
+        # 2. first token of every sequence
+        P = _lib.ptr
+        cur = lambda: _lib.stream_of(counters)  # the stream current at call time (graph capture changes it)
+        fbuf = SamplerBuffers(n, dev)
+        fbuf.set_uniform(temperature, top_p, top_k)
+        if per_seq_sampling is not None:
+            s_temp = torch.tensor(per_seq_sampling[0], dtype=torch.float32).to(dev)
+            s_topp = torch.tensor(per_seq_sampling[1], dtype=torch.float32).to(dev)
+            s_topk = torch.tensor(per_seq_sampling[2], dtype=torch.int32).to(dev)
+            fbuf.temperature.copy_(s_temp)
+            fbuf.top_p.copy_(s_topp)
+            fbuf.top_k.copy_(s_topk)
+        else:
+            s_temp = s_topp = s_topk = None
+        fbuf.set_bias(logit_bias, n)
+        fbuf.rng_key.copy_(torch.arange(n, dtype=torch.int64, device=dev))
+        fbuf.rng_ctr.zero_()
+        f_tok = torch.empty(n, dtype=torch.int64, device=dev)
+        f_lp = torch.empty(n, dtype=torch.float32, device=dev)
+        CH = 1024
+        for a in range(0, n, CH):
+            b = min(n, a + CH)
+            lg = last_logits.index_select(0, sp[a:b].long())
+            if use_pen:
+                idx = sp[a:b].long()
+                repetition_penalty_(lg, repetition_penalty, flat, p_start[idx], p_len[idx])
+            sub = SamplerBuffers.__new__(SamplerBuffers)
+            sub.temperature, sub.top_p, sub.top_k = fbuf.temperature[a:b], fbuf.top_p[a:b], fbuf.top_k[a:b]
+            sub.rng_key, sub.rng_ctr = fbuf.rng_key[a:b], fbuf.rng_ctr[a:b]
+            sub.bias_off = fbuf.bias_off[: b - a + 1] if fbuf.bias_off is not None else None
+            sub.bias_ids, sub.bias_val = fbuf.bias_ids, fbuf.bias_val
+            sample_rows(lg, sub, rule=first_rule, max_valid_id=self.max_valid_id, seed=seed,
+                        out_tok=f_tok[a:b], out_logp=f_lp[a:b])
+        _lib.call("rwkv7_rollout_first", n, maxlen, P(f_tok), P(f_lp), P(seq_max_new), P(seq_ngen), P(seq_done),
+                  P(out_tok), P(out_lp), P(out_step), self.eos, int(first_can_finish), P(counters), cur())
+        del last_logits
+
+        # 3. decode
+        if self.pool is None or self.pool.n_slots != S:
+            self.pool = StatePool(m.config, S, dev)
+        pool = self.pool
+        slot_seq = torch.full((S,), -1, dtype=torch.int32, device=dev)
+        row_slot = torch.full((S,), -1, dtype=torch.int32, device=dev)
+        row_last = torch.arange(S, dtype=torch.int32, device=dev)
+        tok_in = torch.zeros(S, dtype=torch.int64, device=dev)
+        admit_slot = torch.zeros(S, dtype=torch.int32, device=dev)
+        admit_src = torch.zeros(S, dtype=torch.int32, device=dev)
+        s_tok = torch.zeros(S, dtype=torch.int64, device=dev)
+        s_lp = torch.zeros(S, dtype=torch.float32, device=dev)
+        buf = SamplerBuffers(S, dev)
+        buf.set_uniform(temperature, top_p, top_k)
+        buf.set_bias(logit_bias, S)
+        active = torch.zeros(S, dtype=torch.uint8, device=dev)
+        if use_pen:
+            h_start = torch.zeros(S, dtype=torch.int64, device=dev)
+            h_len = torch.zeros(S, dtype=torch.int32, device=dev)
+            h2_start = torch.zeros(S, dtype=torch.int64, device=dev)
+            h2_len = torch.zeros(S, dtype=torch.int32, device=dev)
+        cfg = m.config
+        kv_elems = cfg.n_head * 64 * 64
+        U = store.n_slots
+
+        def commit(have_sample):
+            st = cur()
+            _lib.call("rwkv7_rollout_commit", S, n, maxlen, int(have_sample), P(s_tok), P(s_lp), P(slot_seq),
+                      P(row_slot), P(tok_in), P(sp), P(seq_max_new), P(seq_ngen), P(seq_done), P(out_tok),
+                      P(out_lp), P(out_step), self.eos, P(counters), P(admit_slot), P(admit_src), st)
+            _lib.call("rwkv7_admit_copy", P(counters), P(admit_slot), P(admit_src), cfg.n_layer, S, U, kv_elems,
+                      cfg.n_embd, P(store.kv), P(store.att_x), P(store.ffn_x), P(pool.kv), P(pool.att_x),
+                      P(pool.ffn_x), st)
+
+        def step():
+            logits = m.forward_pooled(tok_in, row_slot, row_last, pool, decode=True)
+            st = cur()
+            if use_pen:
+                _lib.call("rwkv7_rollout_prepare", S, maxlen, P(slot_seq), P(seq_ngen), P(sp), P(p_start),
+                          P(p_len), P(active), P(buf.rng_key), P(buf.rng_ctr), P(h_start), P(h_len),
+                          P(h2_start), P(h2_len), P(s_temp), P(s_topp), P(s_topk), P(buf.temperature),
+                          P(buf.top_p), P(buf.top_k), st)
+                logits = logits.float()
+                repetition_penalty_(logits, repetition_penalty, flat, h_start, h_len, out_tok.view(-1),
+                                    h2_start, h2_len, active)
+            else:
+                _lib.call("rwkv7_rollout_prepare", S, maxlen, P(slot_seq), P(seq_ngen), None, None, None,
+                          P(active), P(buf.rng_key), P(buf.rng_ctr), None, None, None, None, P(s_temp),
+                          P(s_topp), P(s_topk), P(buf.temperature), P(buf.top_p), P(buf.top_k), st)
+            sample_rows(logits, buf, rule=decode_rule, max_valid_id=self.max_valid_id, seed=seed,
+                        out_tok=s_tok, out_logp=s_lp, active=active)
+            commit(True)
+
+        commit(False)  # initial admission
+        torch.cuda.synchronize(dev)
+        t2 = time.perf_counter()
+        timings["first_token_s"] = t2 - t1
+
+        h_done = torch.zeros(2, dtype=torch.int32).pin_memory()
+        cap = n * maxlen + 16
+        n_steps = 0
+        graph = None
+        pending_evt = None
+        done = False
+        while not done and n_steps < cap:
+            for _ in range(self.poll_every):
+                if graph is None and self.use_graph and n_steps >= 1:
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph):
+                        step()
+                if graph is not None:
+                    graph.replay()
+                else:
+                    step()
+                n_steps += 1
+            # read the counters copied one polling period ago (already complete
+            # unless the GPU is behind), then queue a fresh copy
+            if pending_evt is not None:
+                pending_evt.synchronize()
+                if int(h_done[0]) >= n:
+                    done = True
+            h_done[0:2].copy_(counters[1:3], non_blocking=True)
+            pending_evt = torch.cuda.Event()
+            pending_evt.record()
+        torch.cuda.synchronize(dev)
+        if int(h_done[0]) < n:
+            h = counters.cpu()
+            if int(h[C_DONE]) < n:
+                raise RuntimeError(f"rollout did not finish: {int(h[C_DONE])}/{n} sequences after {n_steps} steps")
+        t3 = time.perf_counter()
+        timings["decode_s"] = t3 - t2
+
+        # 4. collect
+        ng = seq_ngen.cpu().tolist()
+        ot = out_tok.cpu()
+        ol = out_lp.cpu()
+        os_ = out_step.cpu()
+        n_dec = int(counters[C_STEP].item())
+        toks = [ot[q, :ng[q]].tolist() for q in range(n)]
+        lps = [ol[q, :ng[q]].tolist() for q in range(n)]
+        stp = [os_[q, :ng[q]].tolist() for q in range(n)]
+        t4 = time.perf_counter()
+        timings["collect_s"] = t4 - t3
+        timings["total_s"] = t4 - t0
+        timings["decode_steps_issued"] = n_steps
+        return RolloutResult(toks, lps, stp, n_dec, timings, prompt_tokens=sum(plen))

@@ -450,6 +450,8 @@ class RWKV7Model(nn.Module):
             _lib.call("rwkv7_activation", code, 2, hk.numel(), P(hk), st)
             ffn_out = self._lin(hk, ffn.value.weight)
         n_out = M if logit_rows is None else (n_logit_rows if n_logit_rows is not None else logit_rows.numel())
+        if n_out == 0:
+            return None
         xo = torch.empty((n_out, C), dtype=dt, device=dev)
         _lib.call("rwkv7_final_norm", code, n_out, C, P(x_mid), P(ffn_out), P(logit_rows),
                   P(self._ln_out[0]), P(self._ln_out[1]), P(xo), st)

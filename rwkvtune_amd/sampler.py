@@ -86,10 +86,12 @@ def ctypes_u64(x: int):
     return ctypes.c_uint64(int(x) & 0xFFFFFFFFFFFFFFFF)
 
 
-def repetition_penalty_(logits: torch.Tensor, penalty: float, hist: torch.Tensor, hist_off: torch.Tensor,
-                        hist2=None, hist2_off=None, hist2_len=None, active=None, n_rows=None):
-    """In-place repetition penalty on float32 ``logits [M, V]`` over each row's id
-    history (``grpo_batch_generator.py:25-42``: every occurrence applies once)."""
+def repetition_penalty_(logits: torch.Tensor, penalty: float, hist: torch.Tensor, hist_start: torch.Tensor,
+                        hist_len: torch.Tensor, hist2=None, hist2_start=None, hist2_len=None, active=None,
+                        n_rows=None):
+    """In-place repetition penalty on float32 ``logits [M, V]``; row m's history is
+    ``hist[hist_start[m]:+hist_len[m]]`` then ``hist2[hist2_start[m]:+hist2_len[m]]``
+    (``grpo_batch_generator.py:25-42``: every occurrence applies once)."""
     if penalty == 1.0 or penalty <= 0:
         return logits
     if logits.dtype != torch.float32:
@@ -98,8 +100,8 @@ def repetition_penalty_(logits: torch.Tensor, penalty: float, hist: torch.Tensor
     P = _lib.ptr
     import ctypes
     _lib.call("rwkv7_repetition_penalty", M, logits.shape[-1], P(logits), logits.stride(0),
-              ctypes.c_float(penalty), P(hist), P(hist_off), P(hist2), P(hist2_off), P(hist2_len),
-              P(active), _lib.stream_of(logits))
+              ctypes.c_float(penalty), P(hist), P(hist_start), P(hist_len), P(hist2), P(hist2_start),
+              P(hist2_len), P(active), _lib.stream_of(logits))
     return logits
 
 

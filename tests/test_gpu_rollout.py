@@ -1,0 +1,153 @@
+"""GPU slot-table rollout (rwkvtune_amd.engine and its front ends) against the
+CPU restatement of the reference loops (oracle/rollout.py).
+
+Greedy decoding is deterministic, so token ids must be identical per sequence
+(float32 model).  Sampled decoding is checked for invariance: the tokens of every
+sequence depend only on its prompt and its (sequence, position) random stream,
+so changing the slot count, the HIP-graph switch or the polling cadence must not
+change a single token (the race detector for the slot table).
+"""
+
+import pytest
+import torch
+
+from oracle import model as om
+from oracle import rollout as orl
+from rwkvtune_amd.batch_generator import BatchGenerator, GenerationConfig
+from rwkvtune_amd.engine import RolloutEngine
+from rwkvtune_amd.grpo_batch_generator import GRPOBatchGenerator
+from rwkvtune_amd.model import RWKV7Config, build_model
+from rwkvtune_amd.sampler import RULE_BATCH, RULE_SINGLE, TokenSampler
+from rwkvtune_amd.scheduler_core import SchedulerCore, SequenceState
+
+pytestmark = pytest.mark.gpu
+
+V = 1000
+
+
+class TinyTok:
+    """Stand-in tokenizer: ids 0..V-4 decodable, so the top 3 ids are banned."""
+    eos_token_id = None
+
+    def __init__(self, eos=None):
+        self.idx2token = {i: str(i).encode() for i in range(V - 3)}
+        self.eos_token_id = eos
+
+    def decode(self, ids):
+        return " ".join(str(i) for i in ids)
+
+    def encode(self, s):
+        return [int(x) for x in s.split()]
+
+
+@pytest.fixture(scope="module")
+def tiny(gpu_device):
+    cfg = RWKV7Config(n_layer=2, n_embd=256, vocab_size=V, dim_att_lora=32, dim_gate_lora=64, dim_mv_lora=32)
+    m = build_model(cfg, dtype=torch.float32, device="cuda", seed=21)
+    sd = om.cast_state_dict(m.state_dict(), torch.float32)
+    return m, sd
+
+
+def prompts(seed, n, lo, hi):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (n,), generator=g).tolist()
+    return [torch.randint(0, V - 3, (L,), generator=g).tolist() for L in lens]
+
+
+def test_grpo_greedy_matches_reference_loop(tiny):
+    print("[case] GRPO greedy parity", flush=True)
+    m, sd = tiny
+    ps = prompts(1, 4, 3, 40)
+    ps.append(list(ps[1]))  # a duplicate prompt: prefilled once, forked
+    G, max_new = 3, 12
+    caps = [max_new - (i % 5) for i in range(len(ps) * G)]
+    free, _ = orl.grpo_rollout(sd, ps, max_new, G, max_valid_id=V - 4, caps=caps)
+    eos = free[0][3]  # a token greedy decoding produces, so the EOS path is exercised
+    ref, _ = orl.grpo_rollout(sd, ps, max_new, G, eos=eos, max_valid_id=V - 4, caps=caps)
+    gen = GRPOBatchGenerator(m, TinyTok(), chunk_size=16, max_decode_batch_size=4, eos_token_id=eos, verbose=False)
+    out = gen.generate(ps, max_new, num_generations=G, temperature=0.0, top_p=1.0, max_new_tokens_per_seq=caps)
+    ids, masks = out["completion_ids"].cpu(), out["masks"].cpu()
+    assert ids.shape[0] == len(ps) * G and ids.dtype == torch.long and masks.dtype == torch.bool
+    for q, r in enumerate(ref):
+        n = int(masks[q].sum())
+        assert ids[q, :n].tolist() == r, f"path {q}"
+        assert bool((ids[q, n:] == 0).all())
+        assert out["completions"][q] == " ".join(map(str, r))
+    assert any(r[-1] == eos and len(r) < caps[q] for q, r in enumerate(ref)), "EOS path not exercised"
+
+
+def test_scheduler_and_batch_generator_greedy(tiny):
+    print("[case] SchedulerCore / BatchGenerator greedy parity", flush=True)
+    m, sd = tiny
+    ps = prompts(2, 6, 1, 30)
+    free = orl.scheduler_rollout(sd, ps, 10, max_valid_id=V - 4)
+    eos = free[2][4]
+    ref = orl.scheduler_rollout(sd, ps, 10, eos=eos, max_valid_id=V - 4)
+    sch = SchedulerCore(m, TinyTok(eos), max_batch_size=3, max_batch_tokens=50, prefill_chunk_size=7)
+    seqs = [SequenceState(seq_id=i, prompt_tokens=p, max_new_tokens=10, temperature=0.0, eos_token_id=eos)
+            for i, p in enumerate(ps)]
+    sch.add_sequences(seqs)
+    got = {i: [] for i in range(len(ps))}
+    for upd in sch.run_to_completion_sync():
+        for sid, t in upd:
+            got[sid].append(t)
+    assert not sch.has_pending_work()
+    for i, r in enumerate(ref):
+        assert got[i] == r and seqs[i].generated_tokens == r
+    # BatchGenerator strips a trailing EOS and returns float masks
+    bg = BatchGenerator(m, TinyTok(eos))
+    res = bg.generate(input_ids=ps, generation_config=GenerationConfig(max_length=10, temperature=0.0,
+                                                                      chunk_size=9, num_generations=2))
+    assert res["masks"].dtype == torch.float32 and res["completion_ids"].shape[0] == 2 * len(ps)
+    for i, r in enumerate(ref):
+        exp = r[:-1] if r[-1] == eos else r
+        for g in range(2):
+            row = res["completion_ids"][2 * i + g].cpu()
+            n = int(res["masks"][2 * i + g].sum())
+            assert row[:n].tolist() == exp
+
+
+@pytest.mark.parametrize("rule", [RULE_BATCH, RULE_SINGLE])
+def test_sampled_rollout_invariant_to_slots_and_graphs(tiny, rule):
+    print(f"[case] sampled rollout invariance rule={rule}", flush=True)
+    m, _ = tiny
+    ps = prompts(3, 5, 5, 60)
+    seq_prompt = [i // 4 for i in range(20)]
+    caps = [3 + (7 * i) % 17 for i in range(20)]
+    kw = dict(temperature=1.0, top_p=0.95, top_k=0, first_rule=RULE_SINGLE, decode_rule=rule,
+              first_can_finish=False, chunk_size=13, seed=1234)
+    runs = []
+    for slots, graph, poll in ((3, True, 2), (20, True, 8), (7, False, 1)):
+        eng = RolloutEngine(m, slots, eos_token_id=None, max_valid_id=V - 4, use_graph=graph, poll_every=poll)
+        res = eng.run(ps, seq_prompt, caps, **kw)
+        runs.append(res)
+        for q, t in enumerate(res.tokens):
+            assert len(t) == caps[q]
+            assert max(t) <= V - 4 and min(t) >= 0
+            assert all(lp <= 1e-6 for lp in res.logps[q])
+    for r in runs[1:]:
+        assert r.tokens == runs[0].tokens
+
+
+def test_repetition_penalty_greedy(tiny):
+    """Greedy GRPO with a strong repetition penalty equals the reference loop
+    with the penalty applied to prompt + generated ids."""
+    print("[case] repetition penalty rollout", flush=True)
+    m, sd = tiny
+    ps = prompts(4, 3, 4, 20)
+    pen = 3.0
+
+    def ref_one(p, n):
+        from oracle import sampler as osm
+        lg, st = om.forward_with_state(sd, torch.tensor([p]), None, torch.float32)
+        toks = []
+        while len(toks) < n:
+            row = osm.repetition_penalty(lg[0, -1:], [p + toks], pen)[0]
+            toks.append(osm.greedy(row, V - 4)[0])
+            lg, st = om.forward_with_state(sd, torch.tensor([[toks[-1]]]), st, torch.float32)
+        return toks
+
+    gen = GRPOBatchGenerator(m, TinyTok(), max_decode_batch_size=2, verbose=False)
+    out = gen.generate(ps, 8, num_generations=1, temperature=0.0, repetition_penalty=pen)
+    for i, p in enumerate(ps):
+        assert out["completion_ids"][i].cpu().tolist() == ref_one(p, 8)

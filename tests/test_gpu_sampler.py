@@ -158,11 +158,13 @@ def test_repetition_penalty(gpu_device):
     for i, h in enumerate(gen):
         gbuf[i, :len(h)] = torch.tensor(h, dtype=torch.int32)
     d = logits.to(gpu_device)
-    dsm.repetition_penalty_(d, 1.3, torch.tensor(flat, dtype=torch.int32, device=gpu_device),
-                            torch.tensor(off, dtype=torch.int64, device=gpu_device),
-                            gbuf.reshape(-1).to(gpu_device),
-                            torch.arange(0, M * gmax, gmax, dtype=torch.int64, device=gpu_device),
-                            torch.tensor([len(h) for h in gen], dtype=torch.int32, device=gpu_device))
+    dev = gpu_device
+    dsm.repetition_penalty_(d, 1.3, torch.tensor(flat, dtype=torch.int32, device=dev),
+                            torch.tensor(off[:-1], dtype=torch.int64, device=dev),
+                            torch.tensor([len(h) for h in hists], dtype=torch.int32, device=dev),
+                            gbuf.reshape(-1).to(dev),
+                            torch.arange(0, M * gmax, gmax, dtype=torch.int64, device=dev),
+                            torch.tensor([len(h) for h in gen], dtype=torch.int32, device=dev))
     torch.cuda.synchronize()
     ref = osm.repetition_penalty(logits, [h + q for h, q in zip(hists, gen)], 1.3)
     assert torch.allclose(d.cpu().double(), ref, rtol=1e-6, atol=1e-6)
