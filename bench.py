@@ -1,15 +1,33 @@
 #!/usr/bin/env python3
-"""Benchmark of the WKV7 decode / prefill / rollout hot path on one MI355X.
+"""Benchmark of rwkvtune's batched-generation hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|decode]
 
-Prints ONE JSON line (see the keys at the end of main()).  One GPU only:
-``--gpus N`` with N > 1 exits with a message.
+Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a message.
 
 Workloads
 ---------
-decode   isolated WKV7 decode step: B=256 slots, H=32, N=64, fp32 state, bf16 I/O,
-         a "step" is one kernel launch over all 8192 (slot, head) units.
+rollout (default)  GRPO rollout on RWKV-7 1.5B (L=24, C=2048, H=32, V=65536), bf16
+    weights from the seeded dense init, fp32 recurrent state: 64 random prompts of
+    length U(256, 2048) x 8 generations = 512 sequences, temperature 1.0, top_p 0.95,
+    at most 512 new tokens, per-sequence stop length ~ Geometric(mean 300) capped at
+    512, 256 decode slots with continuous refill, through
+    ``GRPOBatchGenerator.generate``.  A step is one whole rollout; value = generated
+    tokens / wall time over the K timed rollouts (prefill, first token, decode and
+    result assembly included).
+decode             isolated WKV7 decode kernel at B=256 slots, H=32 (cfg2); a step is
+    one launch; value = algorithmic GB/s.
+
+Both workloads also time the dominant rollout kernel - the fused single-token
+time-mix (``tmix_decode_kernel``: WKV step + decay/LoRA element-wise + GroupNorm /
+bonus / gate) at the rollout's shape (256 slots, H=32) - with HIP events on its
+launch stream, rotating over 24 layer pools (3.2 GB) so no state is served from
+the 256 MB last-level cache; that is the ``roofline`` object.  ``wkv7_decode_cfg2``
+reports the stand-alone WKV kernel the same way (8 pools, 1.07 GB).
+
+The CPU baseline is the reference's CPU path restated in ``oracle/`` (float32,
+``torch.set_num_threads(os.cpu_count())``) timed on a bounded sample of the same
+workload (rollout: one prompt's prefill forked to 256 paths plus decode steps).
 """
 
 from __future__ import annotations
@@ -29,49 +47,172 @@ import torch  # noqa: E402
 PEAK_HBM_GBS = 8000.0          # MI355X datasheet HBM3E bandwidth
 METRIC = "rollout tokens/s (RWKV7-1.5B, 512 seqs); WKV7 decode HBM GB/s vs peak"
 N = 64
-# algorithmic bytes of one decode (slot, head) unit: fp32 state read + write,
-# six bf16 inputs of N, bf16 output of N
-DECODE_BYTES_PER_UNIT = 2 * N * N * 4 + 6 * N * 2 + N * 2
+# algorithmic bytes per (slot, head) unit of one decode step
+WKV_BYTES_PER_UNIT = 2 * N * N * 4 + 6 * N * 2 + N * 2          # state r+w, 6 bf16 inputs, bf16 y
+TMIX_BYTES_PER_UNIT = 2 * N * N * 4 + 7 * N * 2 + N * 4 + N * 2  # state r+w, 7 bf16 inputs, fp32 v_first, bf16 out
+MAX_VALID_ID = 65529
 
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def decode_cfg2(steps: int, warmup: int, dev):
-    """Time `steps` decode launches at B=256, H=32 with HIP events on the launch stream."""
-    from rwkvtune_amd import operators as ops
-    from rwkvtune_amd.workloads import wkv_inputs, wkv_state
+class NullTokenizer:
+    """Synthetic-id tokenizer: decodable ids 0..65529 (the reference vocabulary's
+    range), so 65530..65535 are banned as with the real tokenizer."""
 
-    B, H = 256, 32
-    inp = wkv_inputs((B,), H, N, seed=1000).to(dev)
-    pool = wkv_state(B, H, N, seed=1001).to(dev)
-    y = torch.empty_like(inp.r)
-    args = inp.as_tuple()
-    for _ in range(warmup):
-        ops.wkv7_decode(pool, None, *args, y=y)
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream(dev)
+    def __init__(self, max_id=MAX_VALID_ID):
+        self.idx2token = {max_id: b""}
+        self.eos_token_id = None
+
+    def decode(self, ids):
+        return ""
+
+
+def cfg4_workload(seed=4):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(256, 2049, (64,), generator=g).tolist()
+    prompts = [torch.randint(1, MAX_VALID_ID + 1, (L,), generator=g).tolist() for L in lens]
+    # Geometric(p = 1/300) on {1, 2, ...}, capped at 512
+    u = torch.rand(64 * 8, generator=g, dtype=torch.float64)
+    caps = torch.clamp(torch.ceil(torch.log1p(-u) / torch.log1p(torch.tensor(-1.0 / 300))), 1, 512)
+    return prompts, [int(c) for c in caps]
+
+
+def time_launches(fn, n_iter, stream):
+    """Average duration of fn() launches with HIP events on `stream`."""
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record(stream)
-    for _ in range(steps):
-        ops.wkv7_decode(pool, None, *args, y=y)
+    for i in range(n_iter):
+        fn(i)
     e1.record(stream)
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1)
-    us = ms * 1e3 / steps
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / n_iter  # us
+
+
+def tmix_decode_leg(dev, iters=480):
+    """Fused single-token time-mix at the rollout shape, 24 rotating layer pools."""
+    from rwkvtune_amd import _lib
+    from rwkvtune_amd.workloads import wkv_state
+    S, H, L = 256, 32, 24
+    C = H * N
+    g = torch.Generator(device=dev).manual_seed(5)
+    rnd = lambda *s: torch.randn(*s, generator=g, device=dev)
+    r, k, v, wl, al, vl, gg = (rnd(S, C).to(torch.bfloat16) for _ in range(7))
+    vfirst = rnd(S, C)
+    params = [rnd(C) * 0.5 for _ in range(8)]
+    ptrs = (__import__("ctypes").c_void_p * 8)(*[p.data_ptr() for p in params])
+    pools = torch.randn((L, S, H, N, N), generator=g, device=dev) * 0.1
+    row_slot = torch.arange(S, dtype=torch.int32, device=dev)
+    out = torch.empty(S, C, dtype=torch.bfloat16, device=dev)
+    P = _lib.ptr
+    st = torch.cuda.current_stream(dev)
+
+    def launch(i):
+        _lib.call("rwkv7_tmix_decode", 2, S, H, 0, P(r), P(k), P(v), P(wl), P(al), P(vl), P(gg), P(vfirst),
+                  ptrs, P(pools[i % L]), S, P(row_slot), P(out), _lib.stream_of(out))
+    for i in range(48):
+        launch(i)
+    us = time_launches(launch, iters, st)
+    units = S * H
+    gbs = units * TMIX_BYTES_PER_UNIT / (us * 1e-6) / 1e9
+    return {"kernel": "tmix_decode_kernel<bf16> (fused WKV decode time-mix)", "slots": S, "H": H,
+            "us_per_launch": us, "bytes_per_launch": units * TMIX_BYTES_PER_UNIT, "GBs": gbs,
+            "frac": gbs / PEAK_HBM_GBS, "launches": iters}
+
+
+def wkv_decode_leg(dev, iters=800, pools_n=8):
+    """Stand-alone WKV7 decode kernel, cfg2 shape, rotating over `pools_n` pools."""
+    from rwkvtune_amd import operators as ops
+    from rwkvtune_amd.workloads import wkv_inputs, wkv_state
+    B, H = 256, 32
+    inp = wkv_inputs((B,), H, N, seed=1000).to(dev)
+    pools = [wkv_state(B, H, N, seed=1001 + i).to(dev) for i in range(pools_n)]
+    y = torch.empty_like(inp.r)
+    args = inp.as_tuple()
+    st = torch.cuda.current_stream(dev)
+    for i in range(50):
+        ops.wkv7_decode(pools[i % pools_n], None, *args, y=y)
+    us = time_launches(lambda i: ops.wkv7_decode(pools[i % pools_n], None, *args, y=y), iters, st)
     units = B * H
-    gbs = units * DECODE_BYTES_PER_UNIT / (us * 1e-6) / 1e9
-    return {"B": B, "H": H, "us_per_step": us, "bytes_per_step": units * DECODE_BYTES_PER_UNIT,
-            "achieved_GBs": gbs, "frac": gbs / PEAK_HBM_GBS, "steps": steps}
+    gbs = units * WKV_BYTES_PER_UNIT / (us * 1e-6) / 1e9
+    return {"kernel": "wkv7_seq_kernel<bf16> (T=1)", "B": B, "H": H, "us_per_step": us,
+            "bytes_per_step": units * WKV_BYTES_PER_UNIT, "GBs": gbs, "frac": gbs / PEAK_HBM_GBS,
+            "pools": pools_n, "launches": iters}
+
+
+def rollout(steps, warmup, dev):
+    from rwkvtune_amd.grpo_batch_generator import GRPOBatchGenerator
+    from rwkvtune_amd.model import build_model, config_from_preset
+    cfg = config_from_preset("rwkv7-1.5b")
+    log("[bench] building RWKV-7 1.5B (bf16, seeded dense init) ...")
+    model = build_model(cfg, dtype=torch.bfloat16, device=dev, seed=1234)
+    prompts, caps = cfg4_workload()
+    tok = NullTokenizer()
+    gen = GRPOBatchGenerator(model, tok, chunk_size=2048, max_decode_batch_size=256, eos_token_id=None,
+                             verbose=False)
+    kw = dict(max_new_tokens=512, num_generations=8, temperature=1.0, top_p=0.95, top_k=0,
+              max_new_tokens_per_seq=caps)
+    # warm-up: one small rollout (kernels, GEMM heuristics, graph capture), then W full ones
+    gen.generate(prompts[:2], 8, num_generations=4, temperature=1.0, top_p=0.95)
+    for i in range(warmup):
+        log(f"[bench] warm-up rollout {i + 1}/{warmup}")
+        gen.generate(prompts, **kw)
+    torch.cuda.synchronize(dev)
+    total_gen, total_s, stats = 0, 0.0, []
+    for i in range(steps):
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        out = gen.generate(prompts, **kw)
+        torch.cuda.synchronize(dev)
+        dt = time.perf_counter() - t0
+        n_gen = int(out["masks"].sum())
+        total_gen += n_gen
+        total_s += dt
+        st = dict(gen.last_stats)
+        stats.append(st)
+        log(f"[bench] rollout {i + 1}/{steps}: {n_gen} tokens in {dt:.3f} s = {n_gen / dt:.0f} tok/s "
+            f"(prefill {st['prefill_s']:.3f}s, decode {st['decode_s']:.3f}s, {st['decode_steps']} steps)")
+    return model, prompts, caps, {"tokens": total_gen, "seconds": total_s, "value": total_gen / total_s,
+                                  "ms_per_step": total_s / steps * 1e3, "runs": stats}
+
+
+def cpu_baseline_rollout(model, prompts, paths=256, decode_steps=2):
+    """The reference CPU rollout (oracle/: fp32 forward_with_state, batched
+    sample_batch rules) on a bounded sample: one prompt prefilled, forked to
+    `paths` generation paths, first token, then `decode_steps` lockstep steps."""
+    from oracle import model as om
+    from oracle import sampler as osm
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    sd = om.cast_state_dict(model.state_dict(), torch.float32)
+    p = prompts[0][:512]
+    g = torch.Generator().manual_seed(0)
+    t0 = time.perf_counter()
+    lg, st = om.forward_with_state(sd, torch.tensor([p]), None, torch.float32)
+    t1 = time.perf_counter()
+    states = [{k: v.expand(paths, *v.shape[1:]).clone() for k, v in layer.items()} for layer in st]
+    tok, _ = osm.sample_batch_torch(lg[:, -1].expand(paths, -1), 1.0, 0.95, 0, MAX_VALID_ID, g)
+    generated = paths
+    for _ in range(decode_steps):
+        lg, states = om.forward_with_state(sd, tok[:, None], states, torch.float32)
+        tok, _ = osm.sample_batch_torch(lg[:, -1], 1.0, 0.95, 0, MAX_VALID_ID, g)
+        generated += paths
+    t2 = time.perf_counter()
+    wall = t2 - t0
+    return {"value": generated / wall, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": (f"GRPO rollout sample on the restated reference CPU path (fp32): prefill of one "
+                       f"{len(p)}-token prompt ({t1 - t0:.1f} s), fork to {paths} paths, first token + "
+                       f"{decode_steps} lockstep decode steps ({t2 - t1:.1f} s); {generated} generated tokens "
+                       f"in {wall:.1f} s; prefill {len(p) / (t1 - t0):.0f} tok/s, decode "
+                       f"{paths * decode_steps / (t2 - t1):.0f} tok/s")}
 
 
 def cpu_baseline_decode(reps: int = 3):
     """The reference CPU operator (restated in oracle/) for one cfg2 step, fp32."""
     from oracle.wkv7 import wkv7_cpu
     from rwkvtune_amd.workloads import wkv_inputs, wkv_state
-
     cores = os.cpu_count() or 1
     torch.set_num_threads(cores)
     B, H = 256, 32
@@ -82,23 +223,24 @@ def cpu_baseline_decode(reps: int = 3):
     for _ in range(reps):
         wkv7_cpu(*inp.as_tuple(), N, S0)
     dt = (time.perf_counter() - t0) / reps
-    gbs = B * H * DECODE_BYTES_PER_UNIT / dt / 1e9
+    gbs = B * H * WKV_BYTES_PER_UNIT / dt / 1e9
     return {"value": gbs, "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"one cfg2 decode step (B=256,H=32) through the restated wkv_cpu.py path, "
-                      f"fp32, mean of {reps}; {dt * 1e3:.1f} ms/step"}
+            "sample": f"one cfg2 decode step (B=256, H=32) through the restated wkv_cpu.py path, fp32, "
+                      f"mean of {reps}; {dt * 1e3:.1f} ms/step"}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000)
-    ap.add_argument("--warmup", type=int, default=50)
-    ap.add_argument("--workload", default="decode", choices=["decode"])
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--workload", default="rollout", choices=["rollout", "decode"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {a.gpus}); the rollout shards "
-              "by sequence with no cross-GPU exchange, see DESIGN.md", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (asked for --gpus {a.gpus}): this build measures one GPU's "
+              "share; the rollout shards by sequence with no cross-GPU exchange (see DESIGN.md)",
+              file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
@@ -108,31 +250,53 @@ def main():
     from rwkvtune_amd import _lib
     _lib.load()
 
-    log("[bench] decode cfg2 ...")
-    dec = decode_cfg2(a.steps, a.warmup, dev)
-    log(f"[bench] decode: {dec['us_per_step']:.2f} us/step, {dec['achieved_GBs']:.0f} GB/s")
-    cpu = None
-    if not a.no_cpu_baseline:
-        log("[bench] cpu baseline ...")
-        cpu = cpu_baseline_decode()
-    out = {
-        "metric": METRIC,
-        "value": dec["achieved_GBs"],
-        "unit": "GB/s",
-        "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
-        "ms_per_step": dec["us_per_step"] / 1e3,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16 I/O, fp32 state",
-        "data": "synthetic",
-        "config": {"workload": "wkv7 decode step, B=256 slots, H=32, N=64 (cfg2)"},
-        "roofline": {"bound": "hbm", "achieved": dec["achieved_GBs"], "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": dec["frac"], "traffic": None},
-        "cpu_baseline": cpu,
-    }
+    if a.workload == "rollout":
+        steps = 3 if a.steps is None else a.steps
+        warmup = 1 if a.warmup is None else a.warmup
+        model, prompts, caps, ro = rollout(steps, warmup, dev)
+        log("[bench] fused decode time-mix kernel (roofline) ...")
+        tm = tmix_decode_leg(dev)
+        log(f"[bench] tmix_decode: {tm['us_per_launch']:.2f} us/launch, {tm['GBs']:.0f} GB/s")
+        wk = wkv_decode_leg(dev)
+        log(f"[bench] wkv7 decode cfg2: {wk['us_per_step']:.2f} us/step, {wk['GBs']:.0f} GB/s")
+        cpu = None
+        if not a.no_cpu_baseline:
+            log("[bench] cpu baseline (restated reference rollout, bounded sample) ...")
+            cpu = cpu_baseline_rollout(model, prompts)
+            log(f"[bench] cpu: {cpu['sample']}")
+        out = {
+            "metric": METRIC, "value": ro["value"], "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": ro["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16 weights/activations, fp32 WKV state and element-wise",
+            "data": "synthetic (random prompts, seeded dense random-init weights)",
+            "config": {"workload": "cfg4 GRPO rollout: RWKV7-1.5B, 64 prompts U(256,2048) x 8 = 512 seqs, "
+                                   "temp 1.0, top_p 0.95, max 512 new, geometric(300) stops, 256 slots",
+                       "global_batch": 512, "seq_len": 2048 + 512, "parallelism": "none (1 GPU)",
+                       "generated_tokens": ro["tokens"] // steps, "prompt_tokens": sum(len(p) for p in prompts),
+                       "decode_steps": ro["runs"][-1]["decode_steps"],
+                       "prefill_s": ro["runs"][-1]["prefill_s"], "decode_s": ro["runs"][-1]["decode_s"]},
+            "roofline": {"bound": "hbm", "achieved": tm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": tm["frac"], "traffic": None, "kernel": tm["kernel"],
+                         "us_per_launch": tm["us_per_launch"]},
+            "wkv7_decode_cfg2": {"GBs": wk["GBs"], "frac": wk["frac"], "us_per_step": wk["us_per_step"]},
+            "cpu_baseline": cpu,
+        }
+    else:
+        steps = 1000 if a.steps is None else a.steps
+        warmup = 50 if a.warmup is None else a.warmup
+        wk = wkv_decode_leg(dev, iters=steps)
+        tm = tmix_decode_leg(dev)
+        cpu = None if a.no_cpu_baseline else cpu_baseline_decode()
+        out = {
+            "metric": METRIC, "value": wk["GBs"], "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": wk["us_per_step"] / 1e3, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16 I/O, fp32 state", "data": "synthetic",
+            "config": {"workload": "cfg2 WKV7 decode step, B=256 slots, H=32, N=64, 8 rotating state pools"},
+            "roofline": {"bound": "hbm", "achieved": wk["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": wk["frac"], "traffic": None, "kernel": wk["kernel"]},
+            "tmix_decode": {"GBs": tm["GBs"], "frac": tm["frac"], "us_per_launch": tm["us_per_launch"]},
+            "cpu_baseline": cpu,
+        }
     print(json.dumps(out), flush=True)
 
 

@@ -99,7 +99,8 @@ int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t total_tokens,
  * sequence (negative: no state, x_prev = 0, nothing written).  row_last[m] >= 0
  * marks the first row of a sequence in this call and holds the index of the
  * sequence's last row; -1 on every other row.  Small per-channel parameters
- * are float32; activations use `dtype`.  C <= 8000; H a multiple of 4.
+ * are float32; activations use `dtype`.  C <= 8000 and a multiple of 4; H a
+ * multiple of 4; n_mix is 1 or 6.
  * ------------------------------------------------------------------------ */
 
 /*

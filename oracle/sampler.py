@@ -104,3 +104,33 @@ def repetition_penalty(logits, histories, penalty):
             if 0 <= t < out.shape[1]:
                 out[i, t] = out[i, t] / penalty if out[i, t] > 0 else out[i, t] * penalty
     return out
+
+
+def sample_batch_torch(logits, temperature=1.0, top_p=1.0, top_k=0, max_valid_id=None, gen=None):
+    """Batched float32 restatement of ``TokenSampler.sample_batch``
+    (``core.py:142-236``) in torch CPU ops, as the reference runs it on CPU: ban,
+    temperature, top-k mask, sort + softmax + cumsum nucleus mask (first entry
+    kept), restore order, softmax, multinomial, gathered log-softmax.  Used by
+    the timed CPU baseline."""
+    x = logits.float().clone()
+    V = x.shape[1]
+    if max_valid_id is not None and max_valid_id + 1 < V:
+        x[:, max_valid_id + 1:] = float("-inf")
+    if temperature == 0 or temperature < 1e-6:
+        tok = x.argmax(-1)
+        return tok, torch.log_softmax(x, -1).gather(1, tok[:, None])[:, 0]
+    if temperature != 1.0:
+        x = x / temperature
+    if top_k > 0:
+        vals, idx = torch.topk(x, top_k, dim=-1)
+        x = torch.full_like(x, float("-inf")).scatter_(-1, idx, vals)
+    if top_p < 1.0:
+        sl, si = torch.sort(x, descending=True, dim=-1)
+        cs = torch.cumsum(torch.softmax(sl, -1), -1)
+        keep = cs <= top_p
+        keep[:, 0] = True
+        sl = sl.masked_fill(~keep, float("-inf"))
+        _, restore = torch.sort(si, dim=-1)
+        x = torch.gather(sl, -1, restore)
+    tok = torch.multinomial(torch.softmax(x, -1), 1, generator=gen)[:, 0]
+    return tok, torch.log_softmax(x, -1).gather(1, tok[:, None])[:, 0]

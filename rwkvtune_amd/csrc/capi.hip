@@ -177,9 +177,9 @@ extern "C" int rwkv7_shift_mix(int dtype, int64_t M, int64_t C, const float* x_i
                                int64_t pool_slots, const int32_t* row_slot, const int32_t* row_last,
                                int n_mix, const float* mix, void* out, void* stream) {
     if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: bad dtype code %d", dtype);
-    if (M < 0 || bad_c(C) || n_mix < 1 || n_mix > 8 || pool_slots < 0 || M > kMaxInt)
-        return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: bad sizes M=%lld C=%lld n_mix=%d", (long long)M,
-                    (long long)C, n_mix);
+    if (M < 0 || bad_c(C) || (C % 4) != 0 || (n_mix != 1 && n_mix != 6) || pool_slots < 0 || M > kMaxInt)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: bad sizes M=%lld C=%lld n_mix=%d (C %% 4 == 0, n_mix 1 or 6)",
+                    (long long)M, (long long)C, n_mix);
     if (M == 0) return ok();
     if (tokens == nullptr && x_in == nullptr)
         return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: need x_in or tokens+emb");
@@ -200,7 +200,7 @@ extern "C" int rwkv7_final_norm(int dtype, int64_t n, int64_t C, const float* x_
                                 const int32_t* rows, const float* ln_w, const float* ln_b, void* out,
                                 void* stream) {
     if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_final_norm: bad dtype code %d", dtype);
-    if (n < 0 || bad_c(C) || n > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_final_norm: bad sizes");
+    if (n < 0 || bad_c(C) || (C % 4) != 0 || n > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_final_norm: bad sizes");
     if (n == 0) return ok();
     if (!x_in || !ln_w || !ln_b || !out) return fail(RWKV7_ERR_INVALID, "rwkv7_final_norm: null pointer");
     hipError_t e;

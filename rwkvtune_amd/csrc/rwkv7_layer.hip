@@ -47,23 +47,6 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     return s;
 }
 
-// In-place LayerNorm of row[0..C) (LDS), two-pass mean / biased variance.
-__device__ void layer_norm_row(float* row, int C, const float* __restrict__ w,
-                               const float* __restrict__ b, float eps, float* red) {
-    float s = 0.f;
-    for (int i = threadIdx.x; i < C; i += kThreads) s += row[i];
-    const float mean = block_sum(s, red) / (float)C;
-    float q = 0.f;
-    for (int i = threadIdx.x; i < C; i += kThreads) {
-        const float d = row[i] - mean;
-        q += d * d;
-    }
-    const float var = block_sum(q, red) / (float)C;
-    const float inv = 1.0f / sqrtf(var + eps);
-    for (int i = threadIdx.x; i < C; i += kThreads) row[i] = (row[i] - mean) * inv * w[i] + b[i];
-    __syncthreads();
-}
-
 template <typename IO>
 struct ResidualSrc {
     const float* x_in;      // [M, C] fp32 residual, or null when tokens/emb are used
@@ -75,95 +58,221 @@ struct ResidualSrc {
     const float* ln0_b;
 };
 
-// row[0..C) <- residual stream of row m (emb lookup or x_in + add, then ln0)
-template <typename IO>
-__device__ void load_residual(const ResidualSrc<IO>& src, int m, int C, float* row, float* red) {
-    typedef io_traits<IO> tr;
-    if (src.tokens != nullptr) {
-        const int64_t t = src.tokens[m];
-        const bool ok = t >= 0 && t < src.vocab;
-        const IO* e = src.emb + (ok ? t : 0) * (int64_t)C;
-        for (int i = threadIdx.x; i < C; i += kThreads) row[i] = ok ? tr::to_f32(e[i]) : 0.f;
-    } else {
-        const float* x = src.x_in + (size_t)m * C;
-        if (src.add != nullptr) {
-            const IO* ad = src.add + (size_t)m * C;
-            for (int i = threadIdx.x; i < C; i += kThreads) row[i] = x[i] + tr::to_f32(ad[i]);
-        } else {
-            for (int i = threadIdx.x; i < C; i += kThreads) row[i] = x[i];
-        }
+// ---------------------------------------------------------------------------
+// shift_mix, register-resident: thread t owns the float4 chunks t, t+256, ...
+// of the row (NV chunks at most), every operand is loaded once up front, and a
+// LayerNorm costs two block reductions.  Latency, not bandwidth, bounds this
+// kernel at decode sizes (one row per block), so the loads are issued together.
+// ---------------------------------------------------------------------------
+
+template <typename IO> struct vec4io;
+template <> struct vec4io<float> {
+    static __device__ __forceinline__ f32x4 load(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+    static __device__ __forceinline__ void store(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+};
+template <> struct vec4io<bf16_t> {
+    static __device__ __forceinline__ f32x4 load(const bf16_t* p) { return io_traits<bf16_t>::load4(p); }
+    static __device__ __forceinline__ void store(bf16_t* p, f32x4 v) {
+        uint2 u;
+        u.x = (uint32_t)f32_to_bf16(v.x) | ((uint32_t)f32_to_bf16(v.y) << 16);
+        u.y = (uint32_t)f32_to_bf16(v.z) | ((uint32_t)f32_to_bf16(v.w) << 16);
+        *reinterpret_cast<uint2*>(p) = u;
+    }
+};
+template <> struct vec4io<f16_t> {
+    static __device__ __forceinline__ f32x4 load(const f16_t* p) { return io_traits<f16_t>::load4(p); }
+    static __device__ __forceinline__ void store(f16_t* p, f32x4 v) {
+        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+        h4 h;
+        h.x = (_Float16)v.x; h.y = (_Float16)v.y; h.z = (_Float16)v.z; h.w = (_Float16)v.w;
+        *reinterpret_cast<h4*>(p) = h;
+    }
+};
+
+// two block sums at once (LDS red: 2 * kWaves floats)
+__device__ __forceinline__ f32x2 block_sum2(f32x2 v, float* red) {
+    v.x = wave_sum(v.x);
+    v.y = wave_sum(v.y);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+        red[threadIdx.x >> 6] = v.x;
+        red[kWaves + (threadIdx.x >> 6)] = v.y;
     }
     __syncthreads();
-    if (src.ln0_w != nullptr) layer_norm_row(row, C, src.ln0_w, src.ln0_b, 1e-5f, red);
+    f32x2 s = {0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) {
+        s.x += red[i];
+        s.y += red[kWaves + i];
+    }
+    return s;
 }
 
-template <typename IO>
+template <typename IO, int NV>
+struct RowRegs {
+    f32x4 v[NV];
+};
+
+// residual of row m into registers (emb lookup or x_in + add)
+template <typename IO, int NV>
+__device__ __forceinline__ void load_row(const ResidualSrc<IO>& src, int m, int C4, RowRegs<IO, NV>& r) {
+    const int t = threadIdx.x;
+    if (src.tokens != nullptr) {
+        const int64_t tk = src.tokens[m];
+        const bool ok = tk >= 0 && tk < src.vocab;
+        const IO* e = src.emb + (ok ? tk : 0) * (int64_t)C4 * 4;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = t + j * kThreads;
+            f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            r.v[j] = (c < C4 && ok) ? vec4io<IO>::load(e + 4 * c) : z;
+        }
+    } else {
+        const float* x = src.x_in + (size_t)m * C4 * 4;
+        const IO* ad = src.add != nullptr ? src.add + (size_t)m * C4 * 4 : nullptr;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = t + j * kThreads;
+            f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            f32x4 a = (c < C4) ? *reinterpret_cast<const f32x4*>(x + 4 * c) : z;
+            if (ad != nullptr && c < C4) a += vec4io<IO>::load(ad + 4 * c);
+            r.v[j] = a;
+        }
+    }
+}
+
+// in-place LayerNorm of register rows a (and b when two) with weight/bias w, bv
+template <int NV>
+__device__ __forceinline__ void ln_regs(f32x4 (&a)[NV], f32x4 (&b)[NV], bool two, int C4, const float* w,
+                                        const float* bv, float* red) {
+    const int t = threadIdx.x;
+    const float invC = 1.0f / (float)(C4 * 4);
+    f32x2 s = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if (t + j * kThreads < C4) {
+            s.x += a[j].x + a[j].y + a[j].z + a[j].w;
+            if (two) s.y += b[j].x + b[j].y + b[j].z + b[j].w;
+        }
+    }
+    s = block_sum2(s, red);
+    const float ma = s.x * invC, mb = s.y * invC;
+    f32x2 q = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        if (t + j * kThreads < C4) {
+            f32x4 da = a[j] - ma;
+            q.x += da.x * da.x + da.y * da.y + da.z * da.z + da.w * da.w;
+            if (two) {
+                f32x4 db = b[j] - mb;
+                q.y += db.x * db.x + db.y * db.y + db.z * db.z + db.w * db.w;
+            }
+        }
+    }
+    q = block_sum2(q, red);
+    const float ia = 1.0f / sqrtf(q.x * invC + 1e-5f);
+    const float ib = 1.0f / sqrtf(q.y * invC + 1e-5f);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = t + j * kThreads;
+        if (c < C4) {
+            const f32x4 ww = *reinterpret_cast<const f32x4*>(w + 4 * c);
+            const f32x4 bb = *reinterpret_cast<const f32x4*>(bv + 4 * c);
+            a[j] = (a[j] - ma) * ia * ww + bb;
+            if (two) b[j] = (b[j] - mb) * ib * ww + bb;
+        }
+    }
+}
+
+template <typename IO, int NV, int NMIX>
 __global__ __launch_bounds__(kThreads) void shift_mix_kernel(
     int M, int C, ResidualSrc<IO> src, float* __restrict__ x_out,
     const float* __restrict__ ln_w, const float* __restrict__ ln_b,
     float* __restrict__ prev_pool, int pool_slots, const int32_t* __restrict__ row_slot,
-    const int32_t* __restrict__ row_last, int n_mix, const float* __restrict__ mix,
-    IO* __restrict__ out)
+    const int32_t* __restrict__ row_last, const float* __restrict__ mix, IO* __restrict__ out)
 {
-    typedef io_traits<IO> tr;
-    extern __shared__ float sm[];
-    float* cur = sm;
-    float* prv = sm + C;
-    float* red = sm + 2 * C;
+    __shared__ float red[2 * kWaves];
     const int m = blockIdx.x;
-
-    load_residual(src, m, C, cur, red);
-    if (x_out != nullptr)
-        for (int i = threadIdx.x; i < C; i += kThreads) x_out[(size_t)m * C + i] = cur[i];
-    layer_norm_row(cur, C, ln_w, ln_b, 1e-5f, red);
-
+    const int t = threadIdx.x;
+    const int C4 = C >> 2;
     int slot = row_slot[m];
     if (slot >= pool_slots) slot = -1;
     const int last = row_last[m];
-    if (last >= 0 || m == 0) {  // first row of its sequence: x_prev comes from the state
+    const bool first = last >= 0 || m == 0;
+
+    RowRegs<IO, NV> cur, prv;
+    load_row<IO, NV>(src, m, C4, cur);
+    if (first) {
         const float* p = prev_pool + (size_t)(slot < 0 ? 0 : slot) * C;
-        for (int i = threadIdx.x; i < C; i += kThreads) prv[i] = slot < 0 ? 0.f : p[i];
-        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = t + j * kThreads;
+            f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            prv.v[j] = (c < C4 && slot >= 0) ? *reinterpret_cast<const f32x4*>(p + 4 * c) : z;
+        }
     } else {
-        load_residual(src, m - 1, C, prv, red);
-        layer_norm_row(prv, C, ln_w, ln_b, 1e-5f, red);
+        load_row<IO, NV>(src, m - 1, C4, prv);
     }
-    for (int i = threadIdx.x; i < C; i += kThreads) {
-        const float x = cur[i];
-        const float xx = prv[i] - x;
-        for (int j = 0; j < n_mix; ++j)
-            out[((size_t)j * M + m) * C + i] = tr::from_f32(fmaf(xx, mix[(size_t)j * C + i], x));
+    // ln0 on the residual (layer 0); the previous row needs it too
+    if (src.ln0_w != nullptr) ln_regs<NV>(cur.v, prv.v, !first, C4, src.ln0_w, src.ln0_b, red);
+    if (x_out != nullptr) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = t + j * kThreads;
+            if (c < C4) *reinterpret_cast<f32x4*>(x_out + (size_t)m * C + 4 * c) = cur.v[j];
+        }
+    }
+    ln_regs<NV>(cur.v, prv.v, !first, C4, ln_w, ln_b, red);
+
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = t + j * kThreads;
+        if (c < C4) {
+            const f32x4 x = cur.v[j];
+            const f32x4 xx = prv.v[j] - x;
+#pragma unroll
+            for (int q = 0; q < NMIX; ++q) {
+                const f32x4 mu = *reinterpret_cast<const f32x4*>(mix + (size_t)q * C + 4 * c);
+                vec4io<IO>::store(out + ((size_t)q * M + m) * C + 4 * c, x + xx * mu);
+            }
+        }
     }
     // the new x_prev is the normalised last row of the sequence; the first
     // row's block writes it, after it has read the old value
-    if (last >= 0 && slot >= 0 && last < M) {
-        __syncthreads();
+    if (first && slot >= 0 && last >= 0 && last < M) {
         float* dst = prev_pool + (size_t)slot * C;
-        if (last == m) {
-            for (int i = threadIdx.x; i < C; i += kThreads) dst[i] = cur[i];
-        } else {
-            load_residual(src, last, C, prv, red);
-            layer_norm_row(prv, C, ln_w, ln_b, 1e-5f, red);
-            for (int i = threadIdx.x; i < C; i += kThreads) dst[i] = prv[i];
+        if (last != m) {
+            load_row<IO, NV>(src, last, C4, prv);
+            RowRegs<IO, NV> dummy;
+            if (src.ln0_w != nullptr) ln_regs<NV>(prv.v, dummy.v, false, C4, src.ln0_w, src.ln0_b, red);
+            ln_regs<NV>(prv.v, dummy.v, false, C4, ln_w, ln_b, red);
+        }
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            const int c = t + j * kThreads;
+            if (c < C4) *reinterpret_cast<f32x4*>(dst + 4 * c) = (last == m) ? cur.v[j] : prv.v[j];
         }
     }
 }
 
 // y = LN_out(x_in[row] + add[row]) for the n listed rows (rows = null: 0..n-1)
-template <typename IO>
+template <typename IO, int NV>
 __global__ __launch_bounds__(kThreads) void final_norm_kernel(
     int C, ResidualSrc<IO> src, const int32_t* __restrict__ rows, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, IO* __restrict__ out)
 {
-    typedef io_traits<IO> tr;
-    extern __shared__ float sm[];
-    float* cur = sm;
-    float* red = sm + C;
+    __shared__ float red[2 * kWaves];
     const int n = blockIdx.x;
     const int m = rows != nullptr ? rows[n] : n;
-    load_residual(src, m, C, cur, red);
-    layer_norm_row(cur, C, ln_w, ln_b, 1e-5f, red);
-    for (int i = threadIdx.x; i < C; i += kThreads) out[(size_t)n * C + i] = tr::from_f32(cur[i]);
+    const int C4 = C >> 2;
+    RowRegs<IO, NV> cur, dummy;
+    load_row<IO, NV>(src, m, C4, cur);
+    ln_regs<NV>(cur.v, dummy.v, false, C4, ln_w, ln_b, red);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = threadIdx.x + j * kThreads;
+        if (c < C4) vec4io<IO>::store(out + (size_t)n * C + 4 * c, cur.v[j]);
+    }
 }
 
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf(-x)); }
@@ -378,6 +487,23 @@ __global__ __launch_bounds__(kThreads) void tmix_decode_kernel(
 // launchers (called from capi.hip)
 // ---------------------------------------------------------------------------
 
+template <typename IO, int NV>
+static hipError_t launch_shift_mix_nv(int M, int C, const ResidualSrc<IO>& src, float* x_out, const float* ln_w,
+                                      const float* ln_b, float* prev_pool, int pool_slots, const int32_t* row_slot,
+                                      const int32_t* row_last, int n_mix, const float* mix, void* out, hipStream_t st)
+{
+    if (n_mix == 6)
+        hipLaunchKernelGGL((shift_mix_kernel<IO, NV, 6>), dim3(M), dim3(kThreads), 0, st, M, C, src, x_out, ln_w,
+                           ln_b, prev_pool, pool_slots, row_slot, row_last, mix, (IO*)out);
+    else if (n_mix == 1)
+        hipLaunchKernelGGL((shift_mix_kernel<IO, NV, 1>), dim3(M), dim3(kThreads), 0, st, M, C, src, x_out, ln_w,
+                           ln_b, prev_pool, pool_slots, row_slot, row_last, mix, (IO*)out);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// n_mix in {1, 6}; C a multiple of 4 and at most 8 * 1024
 template <typename IO>
 hipError_t launch_shift_mix(int M, int C, const float* x_in, const void* add, const int64_t* tokens,
                             const void* emb, int64_t vocab, const float* ln0_w, const float* ln0_b,
@@ -386,10 +512,22 @@ hipError_t launch_shift_mix(int M, int C, const float* x_in, const void* add, co
                             int n_mix, const float* mix, void* out, hipStream_t st)
 {
     ResidualSrc<IO> src{x_in, (const IO*)add, tokens, (const IO*)emb, vocab, ln0_w, ln0_b};
-    const size_t smem = (2 * (size_t)C + kWaves) * sizeof(float);
-    hipLaunchKernelGGL(shift_mix_kernel<IO>, dim3(M), dim3(kThreads), smem, st, M, C, src, x_out,
-                       ln_w, ln_b, prev_pool, pool_slots, row_slot, row_last, n_mix, mix, (IO*)out);
-    return hipGetLastError();
+    const int nv = (C / 4 + kThreads - 1) / kThreads;
+    switch (nv) {
+        case 1: return launch_shift_mix_nv<IO, 1>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots, row_slot,
+                                                  row_last, n_mix, mix, out, st);
+        case 2: return launch_shift_mix_nv<IO, 2>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots, row_slot,
+                                                  row_last, n_mix, mix, out, st);
+        case 3: return launch_shift_mix_nv<IO, 3>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots, row_slot,
+                                                  row_last, n_mix, mix, out, st);
+        case 4: return launch_shift_mix_nv<IO, 4>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots, row_slot,
+                                                  row_last, n_mix, mix, out, st);
+        case 5: case 6: return launch_shift_mix_nv<IO, 6>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots,
+                                                          row_slot, row_last, n_mix, mix, out, st);
+        case 7: case 8: return launch_shift_mix_nv<IO, 8>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots,
+                                                          row_slot, row_last, n_mix, mix, out, st);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 template <typename IO>
@@ -397,9 +535,19 @@ hipError_t launch_final_norm(int n, int C, const float* x_in, const void* add, c
                              const float* ln_w, const float* ln_b, void* out, hipStream_t st)
 {
     ResidualSrc<IO> src{x_in, (const IO*)add, nullptr, nullptr, 0, nullptr, nullptr};
-    const size_t smem = ((size_t)C + kWaves) * sizeof(float);
-    hipLaunchKernelGGL(final_norm_kernel<IO>, dim3(n), dim3(kThreads), smem, st, C, src, rows, ln_w,
-                       ln_b, (IO*)out);
+    const int nv = (C / 4 + kThreads - 1) / kThreads;
+#define RWKV7_FN(NVV) hipLaunchKernelGGL((final_norm_kernel<IO, NVV>), dim3(n), dim3(kThreads), 0, st, C, src, rows, \
+                                         ln_w, ln_b, (IO*)out)
+    switch (nv) {
+        case 1: RWKV7_FN(1); break;
+        case 2: RWKV7_FN(2); break;
+        case 3: RWKV7_FN(3); break;
+        case 4: RWKV7_FN(4); break;
+        case 5: case 6: RWKV7_FN(6); break;
+        case 7: case 8: RWKV7_FN(8); break;
+        default: return hipErrorInvalidValue;
+    }
+#undef RWKV7_FN
     return hipGetLastError();
 }
 
