@@ -100,7 +100,7 @@ int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t total_tokens,
  * marks the first row of a sequence in this call and holds the index of the
  * sequence's last row; -1 on every other row.  Small per-channel parameters
  * are float32; activations use `dtype`.  C <= 8000 and a multiple of 4; H a
- * multiple of 4; n_mix is 1 or 6.
+ * multiple of 4; n_mix is 1, 6 or 7.
  * ------------------------------------------------------------------------ */
 
 /*
@@ -164,6 +164,28 @@ int rwkv7_tmix_decode(int dtype, int64_t M, int64_t H, int layer0, const void *r
                       const void *g, float *v_first, const float *const *params,
                       float *state_pool, int64_t pool_slots, const int32_t *row_slot,
                       void *out, void *stream);
+
+/*
+ * Grouped bf16 GEMM for decode-sized projections: `count` (1..8) independent
+ * problems in one launch, problem i computing
+ *   C_i[M, N_i] = act_in_i(A_i[M, K_i]) . B_i[N_i, K_i]^T,  then epi_i on C_i,
+ * with A_i, B_i, C_i bf16 row-major with row strides lda_i, ldb_i, ldc_i
+ * (B in nn.Linear [out][in] layout), float32 accumulation.  act_in: 0 none,
+ * 1 tanh, 2 sigmoid; epi: 0 none, 1 relu(x)^2.  K_i % 32 == 0, lda/ldb
+ * multiples of 8 and >= K_i, A/B 16-byte aligned.  The pointer and size
+ * arrays are host arrays of `count` entries.  Problems whose K is split across
+ * blocks write float32 partial tiles to `workspace` (contents need no
+ * initialisation) and a second launch on `stream` reduces them;
+ * rwkv7_gemm_decode_workspace gives the floats a problem set needs (-1 on
+ * invalid sizes).  Calls that share a workspace must not overlap.  Replaces
+ * the decode step's projection chain of model.py:210-221, 269, 337-338, 495
+ * (torch nn.Linear / matmul calls and the tanh / sigmoid / relu^2 between them).
+ */
+int64_t rwkv7_gemm_decode_workspace(int64_t M, int count, const int *N, const int *K);
+int rwkv7_gemm_decode(int64_t M, int count, const void *const *A, const void *const *B,
+                      void *const *C, const int64_t *lda, const int64_t *ldb, const int64_t *ldc,
+                      const int *N, const int *K, const int *act_in, const int *epi,
+                      float *workspace, int64_t workspace_floats, void *stream);
 
 /* ------------------------------------------------------------------------
  * Sampling

@@ -177,8 +177,10 @@ extern "C" int rwkv7_shift_mix(int dtype, int64_t M, int64_t C, const float* x_i
                                int64_t pool_slots, const int32_t* row_slot, const int32_t* row_last,
                                int n_mix, const float* mix, void* out, void* stream) {
     if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: bad dtype code %d", dtype);
-    if (M < 0 || bad_c(C) || (C % 4) != 0 || (n_mix != 1 && n_mix != 6) || pool_slots < 0 || M > kMaxInt)
-        return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: bad sizes M=%lld C=%lld n_mix=%d (C %% 4 == 0, n_mix 1 or 6)",
+    if (M < 0 || bad_c(C) || (C % 4) != 0 || (n_mix != 1 && n_mix != 6 && n_mix != 7) || pool_slots < 0 ||
+        M > kMaxInt)
+        return fail(RWKV7_ERR_INVALID,
+                    "rwkv7_shift_mix: bad sizes M=%lld C=%lld n_mix=%d (C %% 4 == 0, n_mix 1, 6 or 7)",
                     (long long)M, (long long)C, n_mix);
     if (M == 0) return ok();
     if (tokens == nullptr && x_in == nullptr)
@@ -440,4 +442,63 @@ extern "C" int rwkv7_admit_copy(const int32_t* counters, const int32_t* admit_sl
     return launch_status(launch_admit_copy(counters, admit_slot, admit_src, (int)L, (int)S, (int)U, kv_elems, C,
                                            src_kv, src_ax, src_fx, dst_kv, dst_ax, dst_fx, (hipStream_t)stream),
                          "admit_copy_kernel");
+}
+
+// ---------------------------------------------------------------------------
+// Grouped decode GEMM (gemm_decode.hip)
+// ---------------------------------------------------------------------------
+
+hipError_t launch_gemm_decode(int M, int count, const void* const* A, const void* const* B, void* const* C,
+                              const int64_t* lda, const int64_t* ldb, const int64_t* ldc, const int* N,
+                              const int* K, const int* act_in, const int* epi, float* ws, hipStream_t st);
+int gemm_decode_max_problems();
+int64_t gemm_decode_workspace(int M, int count, const int* N, const int* K);
+
+namespace {
+int check_gemm_problems(const char* fn, int64_t M, int count, const int* N, const int* K) {
+    if (count < 1 || count > gemm_decode_max_problems())
+        return fail(RWKV7_ERR_INVALID, "%s: 1 <= count <= %d", fn, gemm_decode_max_problems());
+    if (M < 0 || M > (1 << 20)) return fail(RWKV7_ERR_INVALID, "%s: bad M=%lld", fn, (long long)M);
+    if (!N || !K) return fail(RWKV7_ERR_INVALID, "%s: null array", fn);
+    for (int i = 0; i < count; ++i)
+        if (N[i] <= 0 || K[i] <= 0 || (K[i] % 32) != 0)
+            return fail(RWKV7_ERR_INVALID, "%s: problem %d: N > 0, K > 0 and K %% 32 == 0 required", fn, i);
+    return RWKV7_OK;
+}
+}  // namespace
+
+extern "C" int64_t rwkv7_gemm_decode_workspace(int64_t M, int count, const int* N, const int* K) {
+    if (check_gemm_problems("rwkv7_gemm_decode_workspace", M, count, N, K) != RWKV7_OK) return -1;
+    ok();
+    return gemm_decode_workspace((int)(M > 0 ? M : 1), count, N, K);
+}
+
+extern "C" int rwkv7_gemm_decode(int64_t M, int count, const void* const* A, const void* const* B, void* const* C,
+                                 const int64_t* lda, const int64_t* ldb, const int64_t* ldc, const int* N,
+                                 const int* K, const int* act_in, const int* epi, float* workspace,
+                                 int64_t workspace_floats, void* stream) {
+    if (check_gemm_problems("rwkv7_gemm_decode", M, count, N, K) != RWKV7_OK) return RWKV7_ERR_INVALID;
+    if (M == 0) return ok();
+    if (!A || !B || !C || !lda || !ldb || !ldc || !act_in || !epi)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: null array");
+    int64_t tiles = 0;
+    for (int i = 0; i < count; ++i) {
+        if (!A[i] || !B[i] || !C[i]) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: null pointer in problem %d", i);
+        if (lda[i] < K[i] || ldb[i] < K[i] || ldc[i] < N[i] || (lda[i] % 8) != 0 || (ldb[i] % 8) != 0)
+            return fail(RWKV7_ERR_INVALID,
+                        "rwkv7_gemm_decode: problem %d: lda/ldb >= K and %% 8 == 0, ldc >= N required", i);
+        if ((((uintptr_t)A[i]) | ((uintptr_t)B[i])) & 15)
+            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: A and B must be 16-byte aligned", i);
+        if (act_in[i] < 0 || act_in[i] > 2 || epi[i] < 0 || epi[i] > 1)
+            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: act_in in 0..2, epi in 0..1", i);
+        tiles += ((M + 63) / 64) * (int64_t)((N[i] + 63) / 64) * 16;
+    }
+    if (tiles > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: too many tiles");
+    const int64_t need_ws = gemm_decode_workspace((int)M, count, N, K);
+    if (need_ws > 0 && (workspace == nullptr || workspace_floats < need_ws))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: needs a workspace of %lld floats (have %lld)",
+                    (long long)need_ws, (long long)workspace_floats);
+    return launch_status(launch_gemm_decode((int)M, count, A, B, C, lda, ldb, ldc, N, K, act_in, epi, workspace,
+                                            (hipStream_t)stream),
+                         "gemm_decode_kernel");
 }

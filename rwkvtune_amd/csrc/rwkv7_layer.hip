@@ -492,7 +492,10 @@ static hipError_t launch_shift_mix_nv(int M, int C, const ResidualSrc<IO>& src, 
                                       const float* ln_b, float* prev_pool, int pool_slots, const int32_t* row_slot,
                                       const int32_t* row_last, int n_mix, const float* mix, void* out, hipStream_t st)
 {
-    if (n_mix == 6)
+    if (n_mix == 7)
+        hipLaunchKernelGGL((shift_mix_kernel<IO, NV, 7>), dim3(M), dim3(kThreads), 0, st, M, C, src, x_out, ln_w,
+                           ln_b, prev_pool, pool_slots, row_slot, row_last, mix, (IO*)out);
+    else if (n_mix == 6)
         hipLaunchKernelGGL((shift_mix_kernel<IO, NV, 6>), dim3(M), dim3(kThreads), 0, st, M, C, src, x_out, ln_w,
                            ln_b, prev_pool, pool_slots, row_slot, row_last, mix, (IO*)out);
     else if (n_mix == 1)
@@ -503,7 +506,7 @@ static hipError_t launch_shift_mix_nv(int M, int C, const ResidualSrc<IO>& src, 
     return hipGetLastError();
 }
 
-// n_mix in {1, 6}; C a multiple of 4 and at most 8 * 1024
+// n_mix in {1, 6, 7}; C a multiple of 4 and at most 8 * 1024
 template <typename IO>
 hipError_t launch_shift_mix(int M, int C, const float* x_in, const void* add, const int64_t* tokens,
                             const void* emb, int64_t vocab, const float* ln0_w, const float* ln0_b,

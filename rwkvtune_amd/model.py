@@ -278,15 +278,39 @@ class _LayerPack:
         self.ln0 = (f32(blk.ln0.weight), f32(blk.ln0.bias)) if self.use_ln0 else None
         self.ln1 = (f32(blk.ln1.weight), f32(blk.ln1.bias))
         self.ln2 = (f32(blk.ln2.weight), f32(blk.ln2.bias))
-        self.mix6 = torch.stack([f32(getattr(att, n)) for n in ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g")])
+        # seven mixes, in the order the projections consume them: r, k, v (one
+        # batched GEMM), then the LoRA inputs w, a, g, v (one batched GEMM)
+        self.mix7 = torch.stack([f32(getattr(att, n)) for n in ("x_r", "x_k", "x_v", "x_w", "x_a", "x_g", "x_v")])
         self.mixk = f32(ffn.x_k).reshape(1, C)
-        zero = torch.zeros(C, dtype=torch.float32, device=self.mix6.device)
+        zero = torch.zeros(C, dtype=torch.float32, device=self.mix7.device)
         self.tvecs = [f32(att.w0), f32(att.a0), f32(att.v0) if not self.layer0 else zero,
                       f32(att.k_k), f32(att.k_a), f32(att.r_k), f32(att.ln_x.weight), f32(att.ln_x.bias)]
         ptrs = [t.data_ptr() for t in self.tvecs]
         if self.layer0:
             ptrs[2] = 0
         self.tparams = (ctypes.c_void_p * 8)(*ptrs)
+        # Batched projection weights ([batch][in][out], contiguous: the right
+        # operand of a batched GEMM must not be a transposed view): r/k/v, and the
+        # LoRA pairs zero-padded to a common rank D (padded down-columns give 0,
+        # whose activation meets zero up-rows, so padding adds nothing).
+        with torch.no_grad():
+            self.w_rkv = torch.stack([att.receptance.weight.detach().t(), att.key.weight.detach().t(),
+                                      att.value.weight.detach().t()]).contiguous()
+            downs = [att.w1, att.a1, att.g1] + ([] if self.layer0 else [att.v1])
+            ups = [att.w2, att.a2, att.g2] + ([] if self.layer0 else [att.v2])
+            D = max(d.shape[1] for d in downs)
+            D = (D + 31) // 32 * 32
+            dt = att.w1.dtype
+            self.lora_down = torch.zeros((len(downs), C, D), dtype=dt, device=att.w1.device)
+            self.lora_up = torch.zeros((len(ups), D, C), dtype=dt, device=att.w1.device)
+            for i, (dn, up) in enumerate(zip(downs, ups)):
+                self.lora_down[i, :, :dn.shape[1]] = dn.detach()
+                self.lora_up[i, :up.shape[0], :] = up.detach()
+        # LoRA matrices in [out][in] layout for the grouped decode GEMM (bf16 models)
+        self.lora_t = {}
+        if att.w1.dtype == torch.bfloat16:
+            names = ("w1", "a1", "g1", "w2", "a2", "g2") + (() if self.layer0 else ("v1", "v2"))
+            self.lora_t = {n: getattr(att, n).detach().t().contiguous() for n in names}
 
 
 class RWKV7Model(nn.Module):
@@ -300,6 +324,9 @@ class RWKV7Model(nn.Module):
         self.ln_out = nn.LayerNorm(config.n_embd)
         self.head = nn.Linear(config.n_embd, config.vocab_size, bias=False)
         self._packs = None
+        # the library's grouped MFMA GEMM for decode projections; off by default:
+        # hipBLASLt's batched GEMMs are faster at these shapes on this stack
+        self.use_grouped_gemm = False
 
     # -- bookkeeping ---------------------------------------------------------
 
@@ -367,6 +394,45 @@ class RWKV7Model(nn.Module):
     def _lin(self, x, weight):
         return F.linear(x, weight)
 
+    class GemmWorkspace:
+        """Split-K partial tiles of the grouped decode GEMM (float32).  Launches
+        that share it must be ordered (one stream)."""
+
+        def __init__(self, device, floats: int = 1 << 22):
+            self.ws = torch.empty(floats, dtype=torch.float32, device=device)
+
+        def ensure(self, floats: int):
+            if floats > self.ws.numel():
+                self.ws = torch.empty(max(floats, 2 * self.ws.numel()), dtype=torch.float32, device=self.ws.device)
+
+    _gemm_ws = {}
+
+    @staticmethod
+    def _gemm_group(M: int, probs, stream):
+        """One grouped decode-GEMM launch: probs = [(A, B, C, act_in, epi)], C = act(A) . B^T."""
+        n = len(probs)
+        P = ctypes.c_void_p
+        dev = probs[0][0].device
+        arrA = (P * n)(*[a.data_ptr() for a, _, _, _, _ in probs])
+        arrB = (P * n)(*[b.data_ptr() for _, b, _, _, _ in probs])
+        arrC = (P * n)(*[c.data_ptr() for _, _, c, _, _ in probs])
+        lda = (ctypes.c_int64 * n)(*[a.stride(0) for a, _, _, _, _ in probs])
+        ldb = (ctypes.c_int64 * n)(*[b.stride(0) for _, b, _, _, _ in probs])
+        ldc = (ctypes.c_int64 * n)(*[c.stride(0) for _, _, c, _, _ in probs])
+        N = (ctypes.c_int * n)(*[b.shape[0] for _, b, _, _, _ in probs])
+        K = (ctypes.c_int * n)(*[b.shape[1] for _, b, _, _, _ in probs])
+        act = (ctypes.c_int * n)(*[x for _, _, _, x, _ in probs])
+        epi = (ctypes.c_int * n)(*[x for _, _, _, _, x in probs])
+        need = _lib.load().rwkv7_gemm_decode_workspace(M, n, N, K)
+        if need < 0:
+            raise ValueError("rwkv7_gemm_decode_workspace: " + _lib.load().rwkv7_last_error().decode())
+        ws = RWKV7Model._gemm_ws.get(dev)
+        if ws is None:
+            ws = RWKV7Model._gemm_ws[dev] = RWKV7Model.GemmWorkspace(dev)
+        ws.ensure(need)
+        _lib.call("rwkv7_gemm_decode", M, n, arrA, arrB, arrC, lda, ldb, ldc, N, K, act, epi,
+                  P(ws.ws.data_ptr()), ws.ws.numel(), stream)
+
     @torch.no_grad()
     def forward_pooled(self, tokens: torch.Tensor, row_slot: torch.Tensor, row_last: torch.Tensor,
                        pool: StatePool, *, decode: bool, cu_seqlens: Optional[torch.Tensor] = None,
@@ -395,7 +461,7 @@ class RWKV7Model(nn.Module):
 
         x_res = torch.empty((M, C), dtype=torch.float32, device=dev)
         x_mid = torch.empty((M, C), dtype=torch.float32, device=dev)
-        mixes = torch.empty((6, M, C), dtype=dt, device=dev)
+        mixes = torch.empty((7, M, C), dtype=dt, device=dev)
         xk_ffn = torch.empty((1, M, C), dtype=dt, device=dev)
         v_first = torch.empty((M, C), dtype=torch.float32, device=dev)
         if not decode:
@@ -404,6 +470,9 @@ class RWKV7Model(nn.Module):
             y = torch.empty((M, C), dtype=torch.float32, device=dev)
         ffn_out = None
         S = pool.n_slots
+        # decode rows of a bf16 model use the grouped MFMA GEMM (small M, many
+        # projections); prefill and other dtypes use library GEMMs
+        grouped = decode and dt == torch.bfloat16 and self.use_grouped_gemm and M <= 1024
         for l in range(L):
             blk = self.blocks[l]
             att, ffn, pk = blk.att, blk.ffn, packs[l]
@@ -412,25 +481,47 @@ class RWKV7Model(nn.Module):
             if l == 0:
                 _lib.call("rwkv7_shift_mix", code, M, C, None, None, P(tokens), P(self.emb.weight),
                           cfg.vocab_size, P(pk.ln0[0]) if pk.ln0 else None, P(pk.ln0[1]) if pk.ln0 else None,
-                          P(x_res), P(pk.ln1[0]), P(pk.ln1[1]), P(ax), S, P(row_slot), P(row_last), 6,
-                          P(pk.mix6), P(mixes), st)
+                          P(x_res), P(pk.ln1[0]), P(pk.ln1[1]), P(ax), S, P(row_slot), P(row_last), 7,
+                          P(pk.mix7), P(mixes), st)
             else:
                 _lib.call("rwkv7_shift_mix", code, M, C, P(x_mid), P(ffn_out), None, None, 0, None, None,
-                          P(x_res), P(pk.ln1[0]), P(pk.ln1[1]), P(ax), S, P(row_slot), P(row_last), 6,
-                          P(pk.mix6), P(mixes), st)
-            xr, xw, xk, xv, xa, xg = mixes.unbind(0)
-            r = self._lin(xr, att.receptance.weight)
-            k = self._lin(xk, att.key.weight)
-            v = self._lin(xv, att.value.weight)
-            hw = xw @ att.w1
-            ha = xa @ att.a1
-            hg = xg @ att.g1
-            _lib.call("rwkv7_activation", code, 0, hw.numel(), P(hw), st)
-            _lib.call("rwkv7_activation", code, 1, hg.numel(), P(hg), st)
-            wl = hw @ att.w2
-            al = ha @ att.a2
-            g = hg @ att.g2
-            vl = (xv @ att.v1) @ att.v2 if l > 0 else None
+                          P(x_res), P(pk.ln1[0]), P(pk.ln1[1]), P(ax), S, P(row_slot), P(row_last), 7,
+                          P(pk.mix7), P(mixes), st)
+            xr, xk, xv, xw, xa, xg, _ = mixes.unbind(0)
+            if grouped:
+                # two grouped launches: the seven projections of the six mixes, then
+                # the four LoRA up-projections with tanh / sigmoid on their inputs
+                lt = pk.lora_t
+                r, k, v = (torch.empty((M, C), dtype=dt, device=dev) for _ in range(3))
+                hw = torch.empty((M, lt["w1"].shape[0]), dtype=dt, device=dev)
+                ha = torch.empty((M, lt["a1"].shape[0]), dtype=dt, device=dev)
+                hg = torch.empty((M, lt["g1"].shape[0]), dtype=dt, device=dev)
+                probs = [(xr, att.receptance.weight, r, 0, 0), (xk, att.key.weight, k, 0, 0),
+                         (xv, att.value.weight, v, 0, 0), (xw, lt["w1"], hw, 0, 0), (xa, lt["a1"], ha, 0, 0),
+                         (xg, lt["g1"], hg, 0, 0)]
+                if l > 0:
+                    hv = torch.empty((M, lt["v1"].shape[0]), dtype=dt, device=dev)
+                    probs.append((xv, lt["v1"], hv, 0, 0))
+                self._gemm_group(M, probs, st)
+                wl, al, g = (torch.empty((M, C), dtype=dt, device=dev) for _ in range(3))
+                probs = [(hw, lt["w2"], wl, 1, 0), (ha, lt["a2"], al, 0, 0), (hg, lt["g2"], g, 2, 0)]
+                vl = None
+                if l > 0:
+                    vl = torch.empty((M, C), dtype=dt, device=dev)
+                    probs.append((hv, lt["v2"], vl, 0, 0))
+                self._gemm_group(M, probs, st)
+            else:
+                # batched library GEMMs: r/k/v in one, the LoRA downs in one (with
+                # tanh on w and sigmoid on g between), the LoRA ups in one
+                rkv = torch.bmm(mixes[0:3], pk.w_rkv)
+                r, k, v = rkv.unbind(0)
+                nl = pk.lora_down.shape[0]
+                h = torch.bmm(mixes[3:3 + nl], pk.lora_down)
+                _lib.call("rwkv7_activation", code, 0, h[0].numel(), P(h[0]), st)
+                _lib.call("rwkv7_activation", code, 1, h[2].numel(), P(h[2]), st)
+                up = torch.bmm(h, pk.lora_up)
+                wl, al, g = up[0], up[1], up[2]
+                vl = up[3] if l > 0 else None
             o = torch.empty((M, C), dtype=dt, device=dev)
             if decode:
                 _lib.call("rwkv7_tmix_decode", code, M, H, int(l == 0), P(r), P(k), P(v), P(wl), P(al),
@@ -441,14 +532,24 @@ class RWKV7Model(nn.Module):
                 wkv_ops.wkv7_prefill(kv, seq_slot, cu_seqlens, *ops.unbind(0), y=y)
                 _lib.call("rwkv7_tmix_post", code, M, H, P(y), P(ops[0]), P(ops[2]), P(ops[3]), P(g),
                           pk.tparams, P(o), st)
-            att_out = self._lin(o, att.output.weight)
+            if grouped:
+                att_out = torch.empty((M, C), dtype=dt, device=dev)
+                self._gemm_group(M, [(o, att.output.weight, att_out, 0, 0)], st)
+            else:
+                att_out = self._lin(o, att.output.weight)
             # residual + attention -> ln2 -> FFN shift/lerp
             _lib.call("rwkv7_shift_mix", code, M, C, P(x_res), P(att_out), None, None, 0, None, None,
                       P(x_mid), P(pk.ln2[0]), P(pk.ln2[1]), P(fx), S, P(row_slot), P(row_last), 1,
                       P(pk.mixk), P(xk_ffn), st)
-            hk = self._lin(xk_ffn[0], ffn.key.weight)
-            _lib.call("rwkv7_activation", code, 2, hk.numel(), P(hk), st)
-            ffn_out = self._lin(hk, ffn.value.weight)
+            if grouped:
+                hk = torch.empty((M, ffn.key.weight.shape[0]), dtype=dt, device=dev)
+                self._gemm_group(M, [(xk_ffn[0], ffn.key.weight, hk, 0, 1)], st)  # relu^2 epilogue
+                ffn_out = torch.empty((M, C), dtype=dt, device=dev)
+                self._gemm_group(M, [(hk, ffn.value.weight, ffn_out, 0, 0)], st)
+            else:
+                hk = self._lin(xk_ffn[0], ffn.key.weight)
+                _lib.call("rwkv7_activation", code, 2, hk.numel(), P(hk), st)
+                ffn_out = self._lin(hk, ffn.value.weight)
         n_out = M if logit_rows is None else (n_logit_rows if n_logit_rows is not None else logit_rows.numel())
         if n_out == 0:
             return None
@@ -457,6 +558,10 @@ class RWKV7Model(nn.Module):
                   P(self._ln_out[0]), P(self._ln_out[1]), P(xo), st)
         if return_hidden:
             return xo
+        if grouped:
+            logits = torch.empty((n_out, self.config.vocab_size), dtype=dt, device=dev)
+            self._gemm_group(n_out, [(xo, self.head.weight, logits, 0, 0)], st)
+            return logits
         return self._lin(xo, self.head.weight)
 
     # -- reference-compatible entry points ------------------------------------

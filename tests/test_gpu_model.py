@@ -136,3 +136,24 @@ def test_cfg1_greedy_token_ids_identical(gpu_device):
     gpu_tok = torch.stack(out, 1).cpu()
     print(f"min top-2 gap {float(gaps.min()):.3e}", flush=True)
     assert torch.equal(gpu_tok, ref_tok)
+
+
+def test_grouped_gemm_decode_path(gpu_device):
+    """The optional grouped MFMA GEMM decode path matches the fp64 oracle too."""
+    print("[case] grouped-GEMM decode path", flush=True)
+    m = tiny(torch.bfloat16, seed=14)
+    sd = om.cast_state_dict(m.state_dict(), torch.float64)
+    g = torch.Generator().manual_seed(3)
+    idx = torch.randint(0, V, (5, 6), generator=g)
+    _, st = m.forward_with_state(idx.to(gpu_device))
+    _, ref_s = om.forward_with_state(sd, idx)
+    m.use_grouped_gemm = True
+    try:
+        for step in range(3):
+            tok = torch.randint(0, V, (5, 1), generator=g)
+            logits, st = m.forward_with_state(tok.to(gpu_device), st)
+            ref_l, ref_s = om.forward_with_state(sd, tok, ref_s)
+            assert rel(logits, ref_l) <= 3e-2
+            check_states(st, ref_s, 3e-2)
+    finally:
+        m.use_grouped_gemm = False
