@@ -50,7 +50,7 @@ const char *rwkv7_last_error(void);
  * launched by cuda_forward_template (wkv7s.cu:56-62).  Differences: a dtype
  * code instead of three symbols, an explicit stream, and the precondition
  * C == H*64 (a host assert in the reference, wkv7s.cu:59) is an error return.
- * T == 1 runs the decode kernel; T > 1 runs the prefill path.
+ * T == 1 runs the decode kernel; T > 1 runs the chunked prefill kernel.
  */
 int rwkv7s_forward(int dtype, int64_t B, int64_t T, int64_t C, int64_t H,
                    float *state, const void *r, const void *w, const void *k,
@@ -77,8 +77,11 @@ int rwkv7_wkv_decode(int dtype, int64_t B, int64_t H, float *state_pool,
  * non-decreasing, cu_seqlens[nseq] == total_tokens) and starts from pool slot
  * slot_idx[s] (NULL = identity), which receives its final state.  Malformed
  * rows (cu out of range, slot out of range or negative) are skipped.
- * chunk_len: 0 = library default; otherwise the chunk length of the chunked
- * form (16, 32 or 64).
+ * chunk_len: 0, 16, 32 or 64 = the chunked MFMA form (contractions on bf16
+ * matrix cores with hi/lo operand splitting, exact token-serial fallback for
+ * chunks with a per-token log-decay below -1.25); it tiles by 32 tokens
+ * whatever the value, which only names the caller's chunking and does not
+ * change the result.  1 = the token-serial kernel.
  * Replaces the reference's chunked prefill, which calls the same token-serial
  * kernel once per length group and chunk (rwkvtune/inference/grpo_batch_generator.py:353-456,
  * scheduler_core.py:513-600 -> wkv7s.cu:22).

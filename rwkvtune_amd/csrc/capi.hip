@@ -13,6 +13,11 @@ hipError_t launch_wkv7_seq(int nseq, int H, int T_uniform, const int32_t* cu_seq
                            const void* v, const void* a, const void* b, void* y,
                            hipStream_t stream);
 
+template <typename IO>
+hipError_t launch_wkv7_chunk(int nseq, int H, int T_uniform, const int32_t* cu_seqlens, const int32_t* slot_idx,
+                             int pool_slots, int total_tokens, float* state, const void* r, const void* w,
+                             const void* k, const void* v, const void* a, const void* b, void* y, hipStream_t stream);
+
 namespace {
 
 thread_local char g_err[512] = "";
@@ -63,6 +68,27 @@ int seq_dispatch(int dtype, int nseq, int H, int T_uniform, const int32_t* cu, c
     return launch_status(e, "wkv7_seq_kernel");
 }
 
+int chunk_dispatch(int dtype, int nseq, int H, int T_uniform, const int32_t* cu, const int32_t* slot, int pool_slots,
+                   int total, float* state, const void* r, const void* w, const void* k, const void* v,
+                   const void* a, const void* b, void* y, hipStream_t st) {
+    hipError_t e;
+    switch (dtype) {
+        case RWKV7_DTYPE_F32:
+            e = launch_wkv7_chunk<float>(nseq, H, T_uniform, cu, slot, pool_slots, total, state, r, w, k, v, a, b, y,
+                                         st);
+            break;
+        case RWKV7_DTYPE_F16:
+            e = launch_wkv7_chunk<f16_t>(nseq, H, T_uniform, cu, slot, pool_slots, total, state, r, w, k, v, a, b, y,
+                                         st);
+            break;
+        default:
+            e = launch_wkv7_chunk<bf16_t>(nseq, H, T_uniform, cu, slot, pool_slots, total, state, r, w, k, v, a, b,
+                                          y, st);
+            break;
+    }
+    return launch_status(e, "wkv7_chunk_kernel");
+}
+
 bool any_null(const void* p0, const void* p1, const void* p2, const void* p3, const void* p4,
               const void* p5, const void* p6, const void* p7) {
     return !p0 || !p1 || !p2 || !p3 || !p4 || !p5 || !p6 || !p7;
@@ -87,8 +113,10 @@ extern "C" int rwkv7s_forward(int dtype, int64_t B, int64_t T, int64_t C, int64_
         return fail(RWKV7_ERR_INVALID, "rwkv7s_forward: problem too large");
     if (any_null(state, r, w, k, v, a, b, y)) return fail(RWKV7_ERR_INVALID, "rwkv7s_forward: null pointer");
     hipStream_t st = (hipStream_t)stream;
-    return seq_dispatch(dtype, (int)B, (int)H, (int)T, nullptr, nullptr, (int)B, (int)(B * T), state,
-                        r, w, k, v, a, b, y, st);
+    if (T == 1)
+        return seq_dispatch(dtype, (int)B, (int)H, 1, nullptr, nullptr, (int)B, (int)B, state, r, w, k, v, a, b, y, st);
+    return chunk_dispatch(dtype, (int)B, (int)H, (int)T, nullptr, nullptr, (int)B, (int)(B * T), state, r, w, k, v, a,
+                          b, y, st);
 }
 
 extern "C" int rwkv7_wkv_decode(int dtype, int64_t B, int64_t H, float* state_pool, int64_t pool_slots,
@@ -115,8 +143,8 @@ extern "C" int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t tot
     if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: bad dtype code %d", dtype);
     if (nseq < 0 || H <= 0 || total_tokens < 0 || pool_slots < 0)
         return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: bad sizes");
-    if (chunk_len != 0 && chunk_len != 16 && chunk_len != 32 && chunk_len != 64)
-        return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: chunk_len must be 0, 16, 32 or 64 (got %d)", chunk_len);
+    if (chunk_len != 0 && chunk_len != 1 && chunk_len != 16 && chunk_len != 32 && chunk_len != 64)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: chunk_len must be 0, 1, 16, 32 or 64 (got %d)", chunk_len);
     if (nseq == 0 || total_tokens == 0) return ok();
     if (cu_seqlens == nullptr) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: cu_seqlens is required");
     if (slot_idx == nullptr && pool_slots < nseq)
@@ -124,8 +152,11 @@ extern "C" int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t tot
     if (nseq * H > kMaxInt || total_tokens > kMaxInt || pool_slots > kMaxInt)
         return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: too large");
     if (any_null(state_pool, r, w, k, v, a, b, y)) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: null pointer");
-    return seq_dispatch(dtype, (int)nseq, (int)H, 0, cu_seqlens, slot_idx, (int)pool_slots, (int)total_tokens,
-                        state_pool, r, w, k, v, a, b, y, (hipStream_t)stream);
+    if (chunk_len == 1)
+        return seq_dispatch(dtype, (int)nseq, (int)H, 0, cu_seqlens, slot_idx, (int)pool_slots, (int)total_tokens,
+                            state_pool, r, w, k, v, a, b, y, (hipStream_t)stream);
+    return chunk_dispatch(dtype, (int)nseq, (int)H, 0, cu_seqlens, slot_idx, (int)pool_slots, (int)total_tokens,
+                          state_pool, r, w, k, v, a, b, y, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------

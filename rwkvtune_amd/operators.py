@@ -170,7 +170,9 @@ def wkv7_prefill(state_pool, slot_idx, cu_seqlens, r, w, k, v, a, b, y=None, chu
 
     ``cu_seqlens`` and ``slot_idx`` are int32 device tensors (``slot_idx`` may be
     None for identity).  Each sequence starts from its pool slot's state and leaves
-    its final state there.  Returns ``y`` (``[total, C]``).
+    its final state there.  Returns ``y`` (``[total, C]``).  ``chunk_len`` 0, 16,
+    32 or 64 runs the chunked matrix-core kernel, 1 the token-serial one; both
+    compute the same recurrence.
     """
     _check_inputs("wkv7_prefill", r, w, k, v, a, b)
     total, C = r.shape[0], r.shape[-1]

@@ -148,11 +148,14 @@ def test_cfg2_1000_steps_linearity(gpu_device):
     assert torch.equal(ya * 0.125, yb)
 
 
+@pytest.mark.parametrize("chunk_len", [1, 0])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_ragged_prefill_token_serial(gpu_device, dtype):
+def test_ragged_prefill(gpu_device, dtype, chunk_len):
+    """Ragged prompts (empty, single-token, partial and whole 32-token chunks)
+    into chosen slots: token-serial (chunk_len=1) and chunked (chunk_len=0)."""
     H = 4
     lens = [1, 0, 37, 5, 64, 130]
-    print(f"[case] ragged prefill {lens} dtype={dtype}", flush=True)
+    print(f"[case] ragged prefill {lens} dtype={dtype} chunk_len={chunk_len}", flush=True)
     cu = cu_seqlens_of(lens)
     inp = wkv_inputs((cu[-1],), H, N, seed=108, dtype=dtype)
     pool0 = wkv_state(8, H, N, seed=109)
@@ -161,11 +164,113 @@ def test_ragged_prefill_token_serial(gpu_device, dtype):
     pool = pool0.to(gpu_device)
     y = ops.wkv7_prefill(pool, torch.tensor(slots, dtype=torch.int32, device=gpu_device),
                          torch.tensor(cu, dtype=torch.int32, device=gpu_device),
-                         *inp.to(gpu_device).as_tuple())
+                         *inp.to(gpu_device).as_tuple(), chunk_len=chunk_len)
     torch.cuda.synchronize()
     check_y(y, y_ref, H, dtype)
     assert state_rel(pool.cpu()[slots], fin) <= S_TOL
     assert torch.equal(pool.cpu()[[3, 4]], pool0[[3, 4]])
+
+
+def decay_regime_inputs(seed):
+    """fp32 inputs of 4 sequences x 4 heads whose decays cover the chunked
+    kernel's regimes: per-token log-decay -exp(w) of
+      head 0: ~-1e-9 (no decay: D = 1 to fp32),
+      head 1: -1.2 (just above the matrix form's floor of -1.25: operands span e^+-38),
+      head 2: -2.7 (below the floor: the exact serial fallback),
+      head 3: alternating by 32-token chunk between -0.3 and -2.7 (both paths
+              in one sequence, state carried between them),
+    plus the trained-model range (w <= -0.5) on sequence 3."""
+    H = 4
+    lens = [100, 64, 33, 96]
+    cu = cu_seqlens_of(lens)
+    inp = wkv_inputs((cu[-1],), H, N, seed=seed, dtype=torch.float32)
+    w = inp.w.view(-1, H, N)
+    w[:, 0] = -20.0
+    w[:, 1] = float(torch.log(torch.tensor(1.2)))
+    w[:, 2] = 1.0
+    for si, (tb, te) in enumerate(zip(cu[:-1], cu[1:])):
+        for t in range(tb, te):
+            w[t, 3] = -1.2 if ((t - tb) // 32) % 2 == 0 else 1.0
+    tb, te = cu[3], cu[4]
+    w[tb:te] = w[tb:te].clamp_max(-0.5)
+    return inp, lens, cu
+
+
+def test_chunked_prefill_decay_regimes(gpu_device):
+    H = 4
+    print("[case] chunked prefill decay regimes", flush=True)
+    inp, lens, cu = decay_regime_inputs(112)
+    pool0 = wkv_state(len(lens), H, N, seed=113)
+    y_ref, fin = wkv7_ragged(*inp.as_tuple(), cu, states=pool0)
+    pool = pool0.to(gpu_device)
+    y = ops.wkv7_prefill(pool, None, torch.tensor(cu, dtype=torch.int32, device=gpu_device),
+                         *inp.to(gpu_device).as_tuple(), chunk_len=32)
+    torch.cuda.synchronize()
+    check_y(y, y_ref, H, torch.float32)
+    assert state_rel(pool.cpu(), fin) <= S_TOL
+
+
+@pytest.mark.parametrize("chunk_len", [16, 32, 64])
+def test_chunk_len_values_same_result(gpu_device, chunk_len):
+    """chunk_len 16/32/64 name the caller's chunking; the result is the recurrence's."""
+    H = 2
+    lens = [70, 3]
+    cu = cu_seqlens_of(lens)
+    print(f"[case] chunk_len={chunk_len}", flush=True)
+    inp = wkv_inputs((cu[-1],), H, N, seed=114, dtype=torch.float32).to(gpu_device)
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=gpu_device)
+    p0 = torch.zeros(2, H, N, N, device=gpu_device)
+    p1 = p0.clone()
+    y0 = ops.wkv7_prefill(p0, None, cu_d, *inp.as_tuple(), chunk_len=0)
+    y1 = ops.wkv7_prefill(p1, None, cu_d, *inp.as_tuple(), chunk_len=chunk_len)
+    assert torch.equal(y0, y1) and torch.equal(p0, p1)
+    with pytest.raises(ValueError):
+        ops.wkv7_prefill(p1, None, cu_d, *inp.as_tuple(), chunk_len=48)
+
+
+def test_chunked_prefill_cfg3_shape(gpu_device):
+    """cfg3: 64 prompts with lengths ~U(64, 2048), H=32, bf16 inputs drawn as in
+    cfg2, zero initial state.  All 64 sequences: chunked equals the token-serial
+    kernel (y within 1e-3 relative as bf16 outputs, state per (seq, head) within
+    1e-4); the shortest, a middle and the longest sequence against the fp64 C
+    oracle at the stated tolerances."""
+    from oracle import cref
+    H = 32
+    lens = ragged_lengths(64, 64, 2048, seed=3)
+    cu = cu_seqlens_of(lens)
+    print(f"[case] cfg3 chunked prefill total={cu[-1]}", flush=True)
+    inp = wkv_inputs((cu[-1],), H, N, seed=115)
+    g = inp.to(gpu_device)
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=gpu_device)
+    pc = torch.zeros(64, H, N, N, device=gpu_device)
+    ps = torch.zeros(64, H, N, N, device=gpu_device)
+    yc = ops.wkv7_prefill(pc, None, cu_d, *g.as_tuple(), chunk_len=64)
+    ys = ops.wkv7_prefill(ps, None, cu_d, *g.as_tuple(), chunk_len=1)
+    torch.cuda.synchronize()
+    e = float((yc.double() - ys.double()).norm() / ys.double().norm())
+    assert e <= 1e-3, f"chunked vs serial y rel err {e:.3e}"
+    assert state_rel(pc.cpu(), ps.cpu()) <= S_TOL
+    order = sorted(range(64), key=lambda i: lens[i])
+    for si in (order[0], order[32], order[-1]):
+        tb, te = cu[si], cu[si + 1]
+        y_ref, S_ref = cref.wkv7_ref_f64(*(t[tb:te][None] for t in inp.as_tuple()))
+        check_y(yc[tb:te].cpu(), y_ref[0], H, torch.bfloat16)
+        assert state_rel(pc[si:si + 1].cpu(), S_ref) <= S_TOL
+
+
+def test_uniform_batch_prefill_operator(gpu_device):
+    """rwkv7_wkv on [B, T, C] with T > 1 runs the chunked kernel on uniform
+    lengths; each batch row equals its own fp64 recurrence."""
+    B, H, T = 3, 2, 70
+    print("[case] uniform [B,T,C] chunked", flush=True)
+    inp = wkv_inputs((B, T), H, N, seed=116)
+    S0 = wkv_state(B, H, N, seed=117)
+    y_ref, S_ref = wkv7_rowwise(*inp.as_tuple(), N, S0)
+    st = S0.to(gpu_device)
+    y = ops.rwkv7_wkv(*inp.to(gpu_device).as_tuple(), head_size=64, state=st)
+    torch.cuda.synchronize()
+    check_y(y, y_ref, H, torch.bfloat16)
+    assert state_rel(st.cpu(), S_ref) <= S_TOL
 
 
 def test_reference_operator_contract(gpu_device):
