@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of rwkvtune's batched-generation hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|decode|prefill]
 
 Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a message.
 
@@ -17,6 +17,9 @@ rollout (default)  GRPO rollout on RWKV-7 1.5B (L=24, C=2048, H=32, V=65536), bf
     result assembly included).
 decode             isolated WKV7 decode kernel at B=256 slots, H=32 (cfg2); a step is
     one launch; value = algorithmic GB/s.
+prefill            chunked WKV7 prefill of cfg3 (64 ragged prompts ~U(64, 2048), H=32)
+    in one launch; value = prompt tokens/s; roofline = bf16 MFMA rate executed
+    (three part products per contraction) against the 2.5 PFLOP/s dense peak.
 
 Both workloads also time the dominant rollout kernel - the fused single-token
 time-mix (``tmix_decode_kernel``: WKV step + decay/LoRA element-wise + GroupNorm /
@@ -142,6 +145,83 @@ def wkv_decode_leg(dev, iters=800, pools_n=8):
             "pools": pools_n, "launches": iters}
 
 
+# chunked prefill (L = 32 tokens, N = 64): contraction flops per (chunk, head) of the
+# matrix form - A_ab, A_ak, B_rb, B_rk (4 x L*L*N), S a~^T and S r~^T (2 x N*L*N),
+# V^T A_ak (N*L*L), SA B_rb + V^T B_rk (2 x N*L*L), SA bbar + V^T kbar (2 x N*L*N);
+# executed as 3 bf16 MFMA products each for bf16/fp16 I/O (hi/lo operand split)
+CHUNK_L = 32
+PREFILL_FLOPS_PER_CHUNK_HEAD = 2 * (4 * CHUNK_L * CHUNK_L * N + 2 * N * CHUNK_L * N + N * CHUNK_L * CHUNK_L
+                                    + 2 * N * CHUNK_L * CHUNK_L + 2 * N * CHUNK_L * N)
+MFMA_PARTS = 3
+PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
+PREFILL_BYTES_PER_HEAD_TOKEN = 7 * N * 2        # r, w, k, v, a, b in, y out (bf16)
+STATE_BYTES_PER_SEQ_HEAD = 2 * N * N * 4        # fp32 state read + write
+
+
+def cfg3_lengths():
+    from rwkvtune_amd.workloads import ragged_lengths
+    return ragged_lengths(64, 64, 2048, seed=3)
+
+
+def prefill_leg(dev, iters=20, chunk_len=64):
+    """cfg3: ragged chunked prefill, 64 prompts ~U(64, 2048), H=32, bf16 inputs drawn
+    as in cfg2, zero initial state; one launch covers the whole batch."""
+    from rwkvtune_amd import operators as ops
+    from rwkvtune_amd.workloads import cu_seqlens_of, wkv_inputs
+    H = 32
+    lens = cfg3_lengths()
+    cu = cu_seqlens_of(lens)
+    total = cu[-1]
+    inp = wkv_inputs((total,), H, N, seed=115).to(dev)
+    cu_d = torch.tensor(cu, dtype=torch.int32, device=dev)
+    pool = torch.zeros(len(lens), H, N, N, device=dev)
+    y = torch.empty_like(inp.r)
+    args = inp.as_tuple()
+    st = torch.cuda.current_stream(dev)
+
+    def launch(i, cl=chunk_len):
+        pool.zero_()
+        ops.wkv7_prefill(pool, None, cu_d, *args, y=y, chunk_len=cl)
+    # the zero fill is timed separately and taken out
+    for i in range(3):
+        launch(i)
+    us_total = time_launches(launch, iters, st)
+    us_fill = time_launches(lambda i: pool.zero_(), iters, st)
+    us = us_total - us_fill
+    us_serial = time_launches(lambda i: launch(i, 1), 3, st) - us_fill
+    chunks = sum((n + CHUNK_L - 1) // CHUNK_L for n in lens) * H
+    flops = chunks * PREFILL_FLOPS_PER_CHUNK_HEAD
+    nbytes = total * H * PREFILL_BYTES_PER_HEAD_TOKEN + len(lens) * H * STATE_BYTES_PER_SEQ_HEAD
+    alg_tf = flops / (us * 1e-6) / 1e12
+    mfma_tf = alg_tf * MFMA_PARTS
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"kernel": "wkv7_chunk_kernel<bf16>", "tokens": total, "seqs": len(lens), "H": H,
+            "us_per_launch": us, "tokens_per_s": total / (us * 1e-6), "algorithmic_TFLOPs": alg_tf,
+            "mfma_bf16_TFLOPs": mfma_tf, "mfma_frac": mfma_tf / PEAK_BF16_TFLOPS,
+            "flops_per_launch": flops, "bytes_per_launch": nbytes, "GBs": gbs, "hbm_frac": gbs / PEAK_HBM_GBS,
+            "token_serial_us": us_serial, "speedup_vs_token_serial": us_serial / us, "launches": iters}
+
+
+def cpu_baseline_prefill(max_tokens=2048):
+    """The reference CPU operator (restated in oracle/) over the first cfg3 prompts."""
+    from oracle.wkv7 import wkv7_cpu
+    from rwkvtune_amd.workloads import wkv_inputs
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    H = 32
+    lens = cfg3_lengths()
+    n = lens[0]
+    n = min(n, max_tokens)
+    inp = wkv_inputs((1, n), H, N, seed=115)
+    S0 = torch.zeros(1, H, N, N)
+    t0 = time.perf_counter()
+    wkv7_cpu(*(t.float() for t in inp.as_tuple()), N, S0)
+    dt = time.perf_counter() - t0
+    return {"value": n / dt, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"first cfg3 prompt ({n} tokens, H=32) through the restated wkv_cpu.py path, fp32; "
+                      f"{dt:.2f} s"}
+
+
 def rollout(steps, warmup, dev):
     from rwkvtune_amd.grpo_batch_generator import GRPOBatchGenerator
     from rwkvtune_amd.model import build_model, config_from_preset
@@ -234,7 +314,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="rollout", choices=["rollout", "decode"])
+    ap.add_argument("--workload", default="rollout", choices=["rollout", "decode", "prefill"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -259,6 +339,9 @@ def main():
         log(f"[bench] tmix_decode: {tm['us_per_launch']:.2f} us/launch, {tm['GBs']:.0f} GB/s")
         wk = wkv_decode_leg(dev)
         log(f"[bench] wkv7 decode cfg2: {wk['us_per_step']:.2f} us/step, {wk['GBs']:.0f} GB/s")
+        pf = prefill_leg(dev)
+        log(f"[bench] wkv7 chunked prefill cfg3: {pf['us_per_launch']:.0f} us, {pf['mfma_bf16_TFLOPs']:.0f} "
+            f"bf16 MFMA TFLOP/s, {pf['speedup_vs_token_serial']:.2f}x token-serial")
         cpu = None
         if not a.no_cpu_baseline:
             log("[bench] cpu baseline (restated reference rollout, bounded sample) ...")
@@ -279,6 +362,27 @@ def main():
                          "frac": tm["frac"], "traffic": None, "kernel": tm["kernel"],
                          "us_per_launch": tm["us_per_launch"]},
             "wkv7_decode_cfg2": {"GBs": wk["GBs"], "frac": wk["frac"], "us_per_step": wk["us_per_step"]},
+            "wkv7_prefill_cfg3": {k: pf[k] for k in ("us_per_launch", "tokens_per_s", "mfma_bf16_TFLOPs",
+                                                     "mfma_frac", "GBs", "hbm_frac", "speedup_vs_token_serial")},
+            "cpu_baseline": cpu,
+        }
+    elif a.workload == "prefill":
+        steps = 20 if a.steps is None else a.steps
+        warmup = 3 if a.warmup is None else a.warmup
+        pf = prefill_leg(dev, iters=steps)
+        cpu = None if a.no_cpu_baseline else cpu_baseline_prefill()
+        out = {
+            "metric": METRIC, "value": pf["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": pf["us_per_launch"] / 1e3, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16 I/O, bf16 MFMA (hi/lo operand split), fp32 state",
+            "data": "synthetic",
+            "config": {"workload": f"cfg3 WKV7 ragged chunked prefill: 64 prompts U(64,2048) = {pf['tokens']} "
+                                   "tokens, H=32, N=64, zero initial state"},
+            "roofline": {"bound": "mfma", "achieved": pf["mfma_bf16_TFLOPs"], "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": pf["mfma_frac"], "traffic": None, "kernel": pf["kernel"],
+                         "algorithmic_TFLOPs": pf["algorithmic_TFLOPs"], "hbm_GBs": pf["GBs"],
+                         "hbm_frac": pf["hbm_frac"]},
+            "token_serial_us": pf["token_serial_us"], "speedup_vs_token_serial": pf["speedup_vs_token_serial"],
             "cpu_baseline": cpu,
         }
     else:

@@ -13,6 +13,10 @@
  * [slots][H][64][64], row = value index, column = key index
  * (rwkvtune/models/rwkv7/operators/cuda/wkv7s.cu:13).  Head size is 64.
  * `w` is the raw decay input: the kernels apply exp(-exp(w)) (wkv7s.cu:27).
+ * Alignment: the WKV entry points (rwkv7s_forward, rwkv7_wkv_decode,
+ * rwkv7_wkv_prefill) need r, w, k, v, a, b aligned to 4 elements (8 bytes for
+ * 16-bit types, 16 for float32) and the state to 16 bytes; other pointers
+ * return RWKV7_ERR_INVALID.  Fresh allocations always qualify.
  */
 #ifndef RWKV7_HIP_H
 #define RWKV7_HIP_H

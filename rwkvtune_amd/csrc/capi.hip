@@ -94,6 +94,15 @@ bool any_null(const void* p0, const void* p1, const void* p2, const void* p3, co
     return !p0 || !p1 || !p2 || !p3 || !p4 || !p5 || !p6 || !p7;
 }
 
+// The WKV kernels read 4 consecutive input elements per access (8 bytes for
+// 16-bit types, 16 for float32) and the state 16 bytes at a time.
+bool misaligned(int dtype, const void* state, const void* r, const void* w, const void* k, const void* v,
+                const void* a, const void* b) {
+    const uintptr_t m = dtype == RWKV7_DTYPE_F32 ? 15 : 7;
+    return (((uintptr_t)r | (uintptr_t)w | (uintptr_t)k | (uintptr_t)v | (uintptr_t)a | (uintptr_t)b) & m) != 0 ||
+           ((uintptr_t)state & 15) != 0;
+}
+
 }  // namespace
 
 extern "C" int rwkv7_abi_version(void) { return 1; }
@@ -112,6 +121,8 @@ extern "C" int rwkv7s_forward(int dtype, int64_t B, int64_t T, int64_t C, int64_
     if (B * T > kMaxInt || B * H > kMaxInt || B * T * C > (int64_t)1 << 40)
         return fail(RWKV7_ERR_INVALID, "rwkv7s_forward: problem too large");
     if (any_null(state, r, w, k, v, a, b, y)) return fail(RWKV7_ERR_INVALID, "rwkv7s_forward: null pointer");
+    if (misaligned(dtype, state, r, w, k, v, a, b))
+        return fail(RWKV7_ERR_INVALID, "rwkv7s_forward: inputs must be aligned to 4 elements, the state to 16 bytes");
     hipStream_t st = (hipStream_t)stream;
     if (T == 1)
         return seq_dispatch(dtype, (int)B, (int)H, 1, nullptr, nullptr, (int)B, (int)B, state, r, w, k, v, a, b, y, st);
@@ -131,6 +142,8 @@ extern "C" int rwkv7_wkv_decode(int dtype, int64_t B, int64_t H, float* state_po
         return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_decode: identity slots need pool_slots >= B");
     if (B * H > kMaxInt || pool_slots > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_decode: too large");
     if (any_null(state_pool, r, w, k, v, a, b, y)) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_decode: null pointer");
+    if (misaligned(dtype, state_pool, r, w, k, v, a, b))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_decode: inputs must be aligned to 4 elements, the state to 16 bytes");
     return seq_dispatch(dtype, (int)B, (int)H, 1, nullptr, slot_idx, (int)pool_slots, (int)B, state_pool, r, w,
                         k, v, a, b, y, (hipStream_t)stream);
 }
@@ -152,6 +165,8 @@ extern "C" int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t tot
     if (nseq * H > kMaxInt || total_tokens > kMaxInt || pool_slots > kMaxInt)
         return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: too large");
     if (any_null(state_pool, r, w, k, v, a, b, y)) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: null pointer");
+    if (misaligned(dtype, state_pool, r, w, k, v, a, b))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: inputs must be aligned to 4 elements, the state to 16 bytes");
     if (chunk_len == 1)
         return seq_dispatch(dtype, (int)nseq, (int)H, 0, cu_seqlens, slot_idx, (int)pool_slots, (int)total_tokens,
                             state_pool, r, w, k, v, a, b, y, (hipStream_t)stream);

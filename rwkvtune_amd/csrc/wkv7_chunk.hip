@@ -323,6 +323,486 @@ __global__ __launch_bounds__(256) void wkv7_chunk_kernel(
     for (int e = tid; e < NH * NH; e += 256) gS[e] = sm.S[e >> 6][e & 63];
 }
 
+// ===========================================================================
+// bf16 / fp16 I/O: the same chunk algebra with every MFMA operand stored once,
+// at production, as bf16 hi + lo planes in LDS (x = hi + lo + e, |e| <= 2^-17 |x|),
+// and three v_mfma_f32_32x32x16_bf16 per product step (hi.hi + hi.lo + lo.hi).
+// The per-product error (~2^-16) leaves y ~5e-5 of its rms from the exact
+// recurrence and the state ~5e-6 relative, well inside the bf16 / fp16 output
+// rounding; the float32 kernel above keeps the three-part split instead.
+//
+// 32x32x16 operand layout: lane l supplies row (l % 32) of A (and of B^T) at
+// k = 8*(l/32) .. +7; accumulator q of lane l is C[8*(q/4) + 4*(l/32) + q%4][l%32].
+// Products whose result is stored are computed transposed where that gives each
+// lane 4 consecutive elements of a stored row.
+// ===========================================================================
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int KP = 72;  // bf16 row stride of planes whose K is 64 (144 B)
+constexpr int TQ = 40;  // bf16 row stride of planes whose K is 32 (80 B)
+constexpr int LWS = 72; // float row stride of the log-decay table
+
+struct __attribute__((aligned(16))) ChunkLds2 {
+    uint16_t Rt[2][L][KP], At[2][L][KP], Kh[2][L][KP], Bh[2][L][KP];  // rows t, K = key j
+    uint16_t Sp[2][NH][KP];                                           // rows i, K = j
+    uint16_t VT[2][NH][TQ], BbT[2][NH][TQ], KbT[2][NH][TQ];           // rows i (VT) / j, K = t
+    uint16_t AakT[2][L][TQ], BrbT[2][L][TQ], BrkT[2][L][TQ];          // rows t, K = s
+    uint16_t SA[2][NH][TQ];                                           // rows i, K = t
+    float Sf[NH][SP];   // float32 state [i][j]
+    float X[NH][TP];    // S a~^T + V^T A_ak  [i][t]
+    float Aab[L][TP];   // [s][t], zero for s >= t
+    float LW[L][LWS];   // per-token log-decay, then its inclusive prefix  [t][j]
+    float tot[4][NH];
+    float DL[NH];
+};
+
+__device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
+    const f32x2 v = {x0, x1};
+    hi = __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+    const f32x2 r = {x0 - __uint_as_float(hi << 16), x1 - __uint_as_float(hi & 0xffff0000u)};
+    lo = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, bf16x2_t));
+}
+
+// hi / lo planes of 4 consecutive values, as two 8-byte words
+__device__ __forceinline__ void split4(float x0, float x1, float x2, float x3, uint2& hi, uint2& lo) {
+    split2(x0, x1, hi.x, lo.x);
+    split2(x2, x3, hi.y, lo.y);
+}
+
+template <typename IO> __device__ __forceinline__ f32x4 unpack4(uint2 u);
+template <> __device__ __forceinline__ f32x4 unpack4<bf16_t>(uint2 u) {
+    f32x4 o;
+    o.x = __uint_as_float(u.x << 16);
+    o.y = __uint_as_float(u.x & 0xffff0000u);
+    o.z = __uint_as_float(u.y << 16);
+    o.w = __uint_as_float(u.y & 0xffff0000u);
+    return o;
+}
+template <> __device__ __forceinline__ f32x4 unpack4<f16_t>(uint2 u) {
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    const h4 h = __builtin_bit_cast(h4, u);
+    f32x4 o;
+    o.x = (float)h.x; o.y = (float)h.y; o.z = (float)h.z; o.w = (float)h.w;
+    return o;
+}
+
+// 8 bf16 of plane row (row0 + l%32) at k0 + 8*(l/32)
+__device__ __forceinline__ bf16x8_t frag(const uint16_t* plane, int stride, int row0, int k0, int lane) {
+    return *reinterpret_cast<const bf16x8_t*>(plane + (row0 + (lane & 31)) * stride + k0 + 8 * (lane >> 5));
+}
+
+__device__ __forceinline__ f32x16 mfma3(f32x16 acc, bf16x8_t a0, bf16x8_t a1, bf16x8_t b0, bf16x8_t b1) {
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc, 0, 0, 0);
+}
+
+// acc += A[rows a0..a0+31][K] . B[rows b0..b0+31][K]^T on hi/lo planes
+__device__ __forceinline__ f32x16 mma32(f32x16 acc, const uint16_t* A, int as, int aplane, int ar0,
+                                        const uint16_t* B, int bs, int bplane, int br0, int K, int lane) {
+    for (int k0 = 0; k0 < K; k0 += 16) {
+        const bf16x8_t a0 = frag(A, as, ar0, k0, lane), a1 = frag(A + aplane, as, ar0, k0, lane);
+        const bf16x8_t b0 = frag(B, bs, br0, k0, lane), b1 = frag(B + bplane, bs, br0, k0, lane);
+        acc = mfma3(acc, a0, a1, b0, b1);
+    }
+    return acc;
+}
+
+// Store accumulator C (= M^T of the stored matrix M) as hi/lo planes of M:
+// lane l holds M[l%32][8g + 4*(l/32) + 0..3] in acc[4g .. 4g+3].
+__device__ __forceinline__ void store_planes_T(uint16_t* P, int stride, int plane, int row0, int col0,
+                                               const f32x16& acc, int lane) {
+    const int row = row0 + (lane & 31);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        uint2 hi, lo;
+        split4(acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3], hi, lo);
+        const int col = col0 + 8 * g + 4 * (lane >> 5);
+        *reinterpret_cast<uint2*>(P + row * stride + col) = hi;
+        *reinterpret_cast<uint2*>(P + plane + row * stride + col) = lo;
+    }
+}
+
+constexpr int RT_PLANE = L * KP, S_PLANE = NH * KP, T64_PLANE = NH * TQ, T32_PLANE = L * TQ;
+
+// The 16-bit kernel keeps log-decays in base 2, so every exponential is one
+// v_exp_f32 (about 1 ulp for the arguments here, all >= -58).  Their accuracy is
+// bounded anyway by the float32 prefix sum of up to 32 log-decays.
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLog2DecayFloor = kLogDecayFloor * kLog2e;
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// hi / lo bf16 parts of one value (hardware round-to-nearest-even)
+__device__ __forceinline__ void split1(float x, uint16_t& hi, uint16_t& lo) {
+    uint32_t h, l;
+    split2(x, 0.f, h, l);
+    hi = (uint16_t)h;
+    lo = (uint16_t)l;
+}
+
+template <typename IO>
+__global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
+    int H, int T_uniform, const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_idx, int pool_slots,
+    int total_tokens, float* __restrict__ state, const IO* __restrict__ r, const IO* __restrict__ w,
+    const IO* __restrict__ k, const IO* __restrict__ v, const IO* __restrict__ a, const IO* __restrict__ b,
+    IO* __restrict__ y)
+{
+    typedef io_traits<IO> tr;
+    __shared__ ChunkLds2 sm;
+    const int unit = blockIdx.x;
+    const int s = unit / H;
+    const int h = unit - s * H;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+
+    const int tb = cu_seqlens != nullptr ? cu_seqlens[s] : s * T_uniform;
+    const int te = cu_seqlens != nullptr ? cu_seqlens[s + 1] : tb + T_uniform;
+    if (tb < 0 || te < tb || te > total_tokens || te == tb) return;  // malformed or empty: untouched
+    const int slot = slot_idx != nullptr ? slot_idx[s] : s;
+    if (slot < 0 || slot >= pool_slots) return;
+
+    const int C = H * NH;
+    float* gS = state + ((size_t)slot * H + h) * (NH * NH);
+
+    // state -> float32 master and hi/lo planes; thread: row i, 16 columns
+    {
+        const int i = tid >> 2, c0 = (tid & 3) * 16;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(gS + i * NH + c0 + 4 * q);
+            *reinterpret_cast<f32x4*>(&sm.Sf[i][c0 + 4 * q]) = x;
+            uint2 hi, lo;
+            split4(x.x, x.y, x.z, x.w, hi, lo);
+            *reinterpret_cast<uint2*>(&sm.Sp[0][i][c0 + 4 * q]) = hi;
+            *reinterpret_cast<uint2*>(&sm.Sp[1][i][c0 + 4 * q]) = lo;
+        }
+    }
+
+    // phase-A mapping: tokens 2*tp, 2*tp+1 of the chunk, channels 4*c4 .. +3
+    const int tp = tid >> 4, c4 = tid & 15, j0 = 4 * c4;
+    uint2 raw[6][2];  // r, w, k, v, a, b of this thread's two tokens (zero past the end)
+    auto fetch = [&](int t0c) {
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int t = t0c + 2 * tp + e;
+            const bool ok = t < te;
+            const size_t off = (size_t)(ok ? t : tb) * C + h * NH + j0;  // clamped to a valid row
+            const IO* src[6] = {r, w, k, v, a, b};
+#pragma unroll
+            for (int q = 0; q < 6; ++q) {
+                const uint2 u = *reinterpret_cast<const uint2*>(src[q] + off);
+                raw[q][e] = ok ? u : make_uint2(0u, 0u);
+            }
+        }
+    };
+    fetch(tb);
+
+    for (int t0 = tb; t0 < te; t0 += L) {
+        const int n = min(L, te - t0);
+        // ---- A1: log-decay of the chunk, strong-decay test ----------------------
+        bool slow = false;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int t = 2 * tp + e;
+            const f32x4 wv = unpack4<IO>(raw[1][e]);
+            f32x4 lw;  // log2 of the decay exp(-exp(w))
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const float x = t < n ? -ex2(wv[c] * kLog2e) * kLog2e : 0.f;
+                slow |= !(x >= kLog2DecayFloor);
+                lw[c] = x;
+            }
+            *reinterpret_cast<f32x4*>(&sm.LW[t][j0]) = lw;
+        }
+        const bool any_slow = __syncthreads_or(slow) != 0;
+
+        if (!any_slow) {
+            // ---- A2: inclusive prefix over the chunk per key (4 segments of 8) ----
+            {
+                const int seg = tid >> 6, j = lane;
+                float pre[8], acc = 0.f;
+#pragma unroll
+                for (int u = 0; u < 8; ++u) {
+                    acc += sm.LW[8 * seg + u][j];
+                    pre[u] = acc;
+                }
+                sm.tot[seg][j] = acc;
+                __syncthreads();
+                float off = 0.f, all = 0.f;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const float tq = sm.tot[q][j];
+                    off += q < seg ? tq : 0.f;
+                    all += tq;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) sm.LW[8 * seg + u][j] = pre[u] + off;
+                if (seg == 0) sm.DL[j] = ex2(all);
+                __syncthreads();
+            }
+            // ---- A3: scaled operands as hi/lo planes ------------------------------
+            {
+                f32x4 vv[2], kb[2], bb[2];
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    const int t = 2 * tp + e;
+                    const f32x4 ld = *reinterpret_cast<const f32x4*>(&sm.LW[t][j0]);
+                    const f32x4 ldm = t > 0 ? *reinterpret_cast<const f32x4*>(&sm.LW[t > 0 ? t - 1 : 0][j0])
+                                            : f32x4{0.f, 0.f, 0.f, 0.f};
+                    const f32x4 ldl = *reinterpret_cast<const f32x4*>(&sm.LW[L - 1][j0]);
+                    const f32x4 rv = unpack4<IO>(raw[0][e]), kv = unpack4<IO>(raw[2][e]);
+                    const f32x4 av = unpack4<IO>(raw[4][e]), bv = unpack4<IO>(raw[5][e]);
+                    vv[e] = unpack4<IO>(raw[3][e]);
+                    f32x4 rt, at, kh, bh;
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        const float iD = ex2(-ld[c]);
+                        const float ratio = ex2(ldl[c] - ld[c]);
+                        rt[c] = rv[c] * ex2(ld[c]);
+                        at[c] = av[c] * ex2(ldm[c]);
+                        kh[c] = kv[c] * iD;
+                        bh[c] = bv[c] * iD;
+                        kb[e][c] = kv[c] * ratio;
+                        bb[e][c] = bv[c] * ratio;
+                    }
+                    uint2 hi, lo;
+                    split4(rt.x, rt.y, rt.z, rt.w, hi, lo);
+                    *reinterpret_cast<uint2*>(&sm.Rt[0][t][j0]) = hi;
+                    *reinterpret_cast<uint2*>(&sm.Rt[1][t][j0]) = lo;
+                    split4(at.x, at.y, at.z, at.w, hi, lo);
+                    *reinterpret_cast<uint2*>(&sm.At[0][t][j0]) = hi;
+                    *reinterpret_cast<uint2*>(&sm.At[1][t][j0]) = lo;
+                    split4(kh.x, kh.y, kh.z, kh.w, hi, lo);
+                    *reinterpret_cast<uint2*>(&sm.Kh[0][t][j0]) = hi;
+                    *reinterpret_cast<uint2*>(&sm.Kh[1][t][j0]) = lo;
+                    split4(bh.x, bh.y, bh.z, bh.w, hi, lo);
+                    *reinterpret_cast<uint2*>(&sm.Bh[0][t][j0]) = hi;
+                    *reinterpret_cast<uint2*>(&sm.Bh[1][t][j0]) = lo;
+                }
+                // transposed planes: key / value j, tokens 2tp and 2tp+1 in one word
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const int j = j0 + c;
+                    uint32_t hi, lo;
+                    split2(vv[0][c], vv[1][c], hi, lo);
+                    *reinterpret_cast<uint32_t*>(&sm.VT[0][j][2 * tp]) = hi;
+                    *reinterpret_cast<uint32_t*>(&sm.VT[1][j][2 * tp]) = lo;
+                    split2(kb[0][c], kb[1][c], hi, lo);
+                    *reinterpret_cast<uint32_t*>(&sm.KbT[0][j][2 * tp]) = hi;
+                    *reinterpret_cast<uint32_t*>(&sm.KbT[1][j][2 * tp]) = lo;
+                    split2(bb[0][c], bb[1][c], hi, lo);
+                    *reinterpret_cast<uint32_t*>(&sm.BbT[0][j][2 * tp]) = hi;
+                    *reinterpret_cast<uint32_t*>(&sm.BbT[1][j][2 * tp]) = lo;
+                }
+            }
+        }
+        // the raw registers are free: fetch the next chunk while this one computes
+        if (t0 + L < te) fetch(t0 + L);
+        __syncthreads();
+
+        if (any_slow) {
+            // ---- exact token-serial update on the float32 master -----------------
+            const int i = tid >> 2, q = tid & 3;
+            for (int t = 0; t < n; ++t) {
+                const size_t off = (size_t)(t0 + t) * C + h * NH;
+                float sa = 0.f;
+#pragma unroll
+                for (int c = 0; c < 16; ++c) sa += tr::to_f32(a[off + q * 16 + c]) * sm.Sf[i][q * 16 + c];
+                sa += __shfl_xor(sa, 1, 64);
+                sa += __shfl_xor(sa, 2, 64);
+                const float vi = tr::to_f32(v[off + i]);
+                float yi = 0.f;
+#pragma unroll
+                for (int c = 0; c < 16; ++c) {
+                    const int jj = q * 16 + c;
+                    const float wd = expf(-expf(tr::to_f32(w[off + jj])));
+                    const float sv = sm.Sf[i][jj] * wd + tr::to_f32(k[off + jj]) * vi + sa * tr::to_f32(b[off + jj]);
+                    sm.Sf[i][jj] = sv;
+                    yi += sv * tr::to_f32(r[off + jj]);
+                }
+                yi += __shfl_xor(yi, 1, 64);
+                yi += __shfl_xor(yi, 2, 64);
+                if (q == 0) y[off + i] = tr::from_f32(yi);
+            }
+            // refresh the hi/lo planes of the state (same thread owns the same row)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int jj = q * 16 + 4 * c;
+                const f32x4 x = *reinterpret_cast<const f32x4*>(&sm.Sf[i][jj]);
+                uint2 hi, lo;
+                split4(x.x, x.y, x.z, x.w, hi, lo);
+                *reinterpret_cast<uint2*>(&sm.Sp[0][i][jj]) = hi;
+                *reinterpret_cast<uint2*>(&sm.Sp[1][i][jj]) = lo;
+            }
+            __syncthreads();
+            continue;
+        }
+
+        // ---- B: two 32x32 tiles per wave, K = 64 over keys -------------------------
+        const f32x16 zero16 = {0.f};
+        f32x16 accX = zero16, accY = zero16;  // waves 0/1: X^T, Y^T of value rows 32*wave..
+        if (wave < 2) {
+            // X^T[t][i] = a~_t . S_i,  Y^T[t][i] = r~_t . S_i   (i in tile `wave`)
+            for (int k0 = 0; k0 < NH; k0 += 16) {
+                const bf16x8_t s0 = frag(&sm.Sp[0][0][0], KP, 32 * wave, k0, lane);
+                const bf16x8_t s1 = frag(&sm.Sp[1][0][0], KP, 32 * wave, k0, lane);
+                const bf16x8_t a0 = frag(&sm.At[0][0][0], KP, 0, k0, lane), a1 = frag(&sm.At[1][0][0], KP, 0, k0, lane);
+                const bf16x8_t r0 = frag(&sm.Rt[0][0][0], KP, 0, k0, lane), r1 = frag(&sm.Rt[1][0][0], KP, 0, k0, lane);
+                accX = mfma3(accX, a0, a1, s0, s1);
+                accY = mfma3(accY, r0, r1, s0, s1);
+            }
+        } else {
+            // wave 2: A_ab[s][t] = b^_s . a~_t and B_rb[s][t] = b^_s . r~_t  (shared b^)
+            // wave 3: A_ak[s][t] = k^_s . a~_t and B_rk[s][t] = k^_s . r~_t  (shared k^)
+            const uint16_t* Pq = wave == 2 ? &sm.Bh[0][0][0] : &sm.Kh[0][0][0];
+            f32x16 c1 = zero16, c2 = zero16;
+            for (int k0 = 0; k0 < NH; k0 += 16) {
+                const bf16x8_t p0 = frag(Pq, KP, 0, k0, lane), p1 = frag(Pq + RT_PLANE, KP, 0, k0, lane);
+                const bf16x8_t a0 = frag(&sm.At[0][0][0], KP, 0, k0, lane), a1 = frag(&sm.At[1][0][0], KP, 0, k0, lane);
+                const bf16x8_t r0 = frag(&sm.Rt[0][0][0], KP, 0, k0, lane), r1 = frag(&sm.Rt[1][0][0], KP, 0, k0, lane);
+                c1 = mfma3(c1, p0, p1, a0, a1);
+                c2 = mfma3(c2, p0, p1, r0, r1);
+            }
+            // masks: lane holds [s = 8g + 4(l/32) + e][t = l%32]
+            const int tcol = lane & 31;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int srow = 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+                c1[q] = srow < tcol ? c1[q] : 0.f;   // A_ab / A_ak: s < t
+                c2[q] = srow <= tcol ? c2[q] : 0.f;  // B_rb / B_rk: s <= t
+            }
+            if (wave == 2) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    sm.Aab[8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)][tcol] = c1[q];
+                store_planes_T(&sm.BrbT[0][0][0], TQ, T32_PLANE, 0, 0, c2, lane);
+            } else {
+                store_planes_T(&sm.AakT[0][0][0], TQ, T32_PLANE, 0, 0, c1, lane);
+                store_planes_T(&sm.BrkT[0][0][0], TQ, T32_PLANE, 0, 0, c2, lane);
+            }
+        }
+        __syncthreads();
+
+        // ---- C: X^T += A_ak^T V (waves 0/1); state tiles start (waves 2/3) --------
+        f32x16 accS0 = zero16, accS1 = zero16;  // waves 2/3: S^T tiles (j tile 0 / 1, i tile wave-2)
+        if (wave < 2) {
+            accX = mma32(accX, &sm.AakT[0][0][0], TQ, T32_PLANE, 0, &sm.VT[0][0][0], TQ, T64_PLANE, 32 * wave, L,
+                         lane);
+            // X[i][t]: lane holds i = 32*wave + l%32, t = 8g + 4(l/32) + 0..3
+            const int i = 32 * wave + (lane & 31);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<f32x4*>(&sm.X[i][8 * g + 4 * (lane >> 5)]) =
+                    f32x4{accX[4 * g], accX[4 * g + 1], accX[4 * g + 2], accX[4 * g + 3]};
+        } else {
+            const int ir = wave - 2;               // value-row tile
+            const int i = 32 * ir + (lane & 31);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int jo = 8 * g + 4 * (lane >> 5);
+                const f32x4 s0 = *reinterpret_cast<const f32x4*>(&sm.Sf[i][jo]);
+                const f32x4 s1 = *reinterpret_cast<const f32x4*>(&sm.Sf[i][32 + jo]);
+                const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sm.DL[jo]);
+                const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sm.DL[32 + jo]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    accS0[4 * g + e] = s0[e] * d0[e];
+                    accS1[4 * g + e] = s1[e] * d1[e];
+                }
+            }
+            // S^T[j][i] += kbar_j . v_i over the chunk's tokens
+            for (int k0 = 0; k0 < L; k0 += 16) {
+                const bf16x8_t v0 = frag(&sm.VT[0][0][0], TQ, 32 * ir, k0, lane);
+                const bf16x8_t v1 = frag(&sm.VT[1][0][0], TQ, 32 * ir, k0, lane);
+                const bf16x8_t k00 = frag(&sm.KbT[0][0][0], TQ, 0, k0, lane), k01 = frag(&sm.KbT[1][0][0], TQ, 0, k0, lane);
+                const bf16x8_t k10 = frag(&sm.KbT[0][0][0], TQ, 32, k0, lane), k11 = frag(&sm.KbT[1][0][0], TQ, 32, k0, lane);
+                accS0 = mfma3(accS0, k00, k01, v0, v1);
+                accS1 = mfma3(accS1, k10, k11, v0, v1);
+            }
+        }
+        __syncthreads();
+
+        // ---- triangular solve: SA[i][t] = X[i][t] + sum_{u<t} SA[i][u] A_ab[u][t] -----
+        {
+            const int i = tid >> 2, q = tid & 3;
+            float sq[8];  // SA[i][4m + q]
+#pragma unroll
+            for (int m = 0; m < 8; ++m) sq[m] = 0.f;
+#pragma unroll
+            for (int t = 0; t < L; ++t) {
+                float part = 0.f;
+#pragma unroll
+                for (int m = 0; m < (t + 3) / 4; ++m) part = fmaf(sq[m], sm.Aab[4 * m + q][t], part);
+                part += dpp_xor1(part);
+                part += dpp_xor2(part);
+                const float sat = sm.X[i][t] + part;
+                sq[t >> 2] = q == (t & 3) ? sat : sq[t >> 2];
+            }
+#pragma unroll
+            for (int m = 0; m < 8; ++m) split1(sq[m], sm.SA[0][i][4 * m + q], sm.SA[1][i][4 * m + q]);
+        }
+        __syncthreads();
+
+        // ---- D: Y^T += B_rb^T SA + B_rk^T V (waves 0/1); S^T += bbar SA (waves 2/3) --
+        if (wave < 2) {
+            for (int k0 = 0; k0 < L; k0 += 16) {
+                const bf16x8_t p0 = frag(&sm.BrbT[0][0][0], TQ, 0, k0, lane), p1 = frag(&sm.BrbT[1][0][0], TQ, 0, k0, lane);
+                const bf16x8_t q0 = frag(&sm.BrkT[0][0][0], TQ, 0, k0, lane), q1 = frag(&sm.BrkT[1][0][0], TQ, 0, k0, lane);
+                const bf16x8_t s0 = frag(&sm.SA[0][0][0], TQ, 32 * wave, k0, lane);
+                const bf16x8_t s1 = frag(&sm.SA[1][0][0], TQ, 32 * wave, k0, lane);
+                const bf16x8_t v0 = frag(&sm.VT[0][0][0], TQ, 32 * wave, k0, lane);
+                const bf16x8_t v1 = frag(&sm.VT[1][0][0], TQ, 32 * wave, k0, lane);
+                accY = mfma3(accY, p0, p1, s0, s1);
+                accY = mfma3(accY, q0, q1, v0, v1);
+            }
+            // y[t0 + t][32*wave + l%32], t = 8g + 4(l/32) + e
+            IO* yb = y + (size_t)t0 * C + h * NH + 32 * wave + (lane & 31);
+            if (n == L) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    yb[(8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * C] = tr::from_f32(accY[q]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int t = 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+                    if (t < n) yb[t * C] = tr::from_f32(accY[q]);
+                }
+            }
+        } else {
+            const int ir = wave - 2;
+            for (int k0 = 0; k0 < L; k0 += 16) {
+                const bf16x8_t s0 = frag(&sm.SA[0][0][0], TQ, 32 * ir, k0, lane);
+                const bf16x8_t s1 = frag(&sm.SA[1][0][0], TQ, 32 * ir, k0, lane);
+                const bf16x8_t b00 = frag(&sm.BbT[0][0][0], TQ, 0, k0, lane), b01 = frag(&sm.BbT[1][0][0], TQ, 0, k0, lane);
+                const bf16x8_t b10 = frag(&sm.BbT[0][0][0], TQ, 32, k0, lane), b11 = frag(&sm.BbT[1][0][0], TQ, 32, k0, lane);
+                accS0 = mfma3(accS0, b00, b01, s0, s1);
+                accS1 = mfma3(accS1, b10, b11, s0, s1);
+            }
+            // lane holds S[i = 32*ir + l%32][j = 32*jt + 8g + 4(l/32) + 0..3]
+            const int i = 32 * ir + (lane & 31);
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int jo = 8 * g + 4 * (lane >> 5);
+                *reinterpret_cast<f32x4*>(&sm.Sf[i][jo]) =
+                    f32x4{accS0[4 * g], accS0[4 * g + 1], accS0[4 * g + 2], accS0[4 * g + 3]};
+                *reinterpret_cast<f32x4*>(&sm.Sf[i][32 + jo]) =
+                    f32x4{accS1[4 * g], accS1[4 * g + 1], accS1[4 * g + 2], accS1[4 * g + 3]};
+            }
+            store_planes_T(&sm.Sp[0][0][0], KP, S_PLANE, 32 * ir, 0, accS0, lane);
+            store_planes_T(&sm.Sp[0][0][0], KP, S_PLANE, 32 * ir, 32, accS1, lane);
+        }
+        // No barrier here: the next chunk's first LDS writes (LW) touch nothing
+        // read in phase D, and its barriers precede every other write.
+    }
+    __syncthreads();
+    for (int e = tid; e < NH * NH / 4; e += 256) {
+        const int i = e >> 4, c = (e & 15) * 4;
+        *reinterpret_cast<f32x4*>(gS + i * NH + c) = *reinterpret_cast<const f32x4*>(&sm.Sf[i][c]);
+    }
+}
+
 }  // namespace
 
 template <typename IO>
@@ -330,9 +810,15 @@ hipError_t launch_wkv7_chunk(int nseq, int H, int T_uniform, const int32_t* cu_s
                              int pool_slots, int total_tokens, float* state, const void* r, const void* w,
                              const void* k, const void* v, const void* a, const void* b, void* y, hipStream_t stream)
 {
-    hipLaunchKernelGGL(wkv7_chunk_kernel<IO>, dim3((unsigned)nseq * (unsigned)H), dim3(256), 0, stream, H,
-                       T_uniform, cu_seqlens, slot_idx, pool_slots, total_tokens, state, (const IO*)r, (const IO*)w,
-                       (const IO*)k, (const IO*)v, (const IO*)a, (const IO*)b, (IO*)y);
+    if constexpr (sizeof(IO) == 4) {
+        hipLaunchKernelGGL(wkv7_chunk_kernel<IO>, dim3((unsigned)nseq * (unsigned)H), dim3(256), 0, stream, H,
+                           T_uniform, cu_seqlens, slot_idx, pool_slots, total_tokens, state, (const IO*)r,
+                           (const IO*)w, (const IO*)k, (const IO*)v, (const IO*)a, (const IO*)b, (IO*)y);
+    } else {
+        hipLaunchKernelGGL(wkv7_chunk2_kernel<IO>, dim3((unsigned)nseq * (unsigned)H), dim3(256), 0, stream, H,
+                           T_uniform, cu_seqlens, slot_idx, pool_slots, total_tokens, state, (const IO*)r,
+                           (const IO*)w, (const IO*)k, (const IO*)v, (const IO*)a, (const IO*)b, (IO*)y);
+    }
     return hipGetLastError();
 }
 

@@ -54,7 +54,15 @@ def _check_inputs(fn, r, w, k, v, a, b):
 
 
 def _contig(*ts):
-    return [t.contiguous() for t in ts]
+    """Contiguous copies where needed, plus a fresh copy of any tensor whose data
+    pointer is not aligned to 4 elements (the kernels read 4 elements at once)."""
+    out = []
+    for t in ts:
+        t = t.contiguous()
+        if t.data_ptr() % (4 * t.element_size()):
+            t = t.clone()
+        out.append(t)
+    return out
 
 
 def _check_out(y, r):

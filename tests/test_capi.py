@@ -66,11 +66,19 @@ def test_host_side_errors(lib):
     # identity slots need a pool at least as large as the batch
     rc = lib.rwkv7_wkv_decode(2, 4, 1, fake, 2, None, *[fake] * 6, fake, None)
     assert rc == 1 and b"pool_slots" in lib.rwkv7_last_error()
-    # prefill: chunk length outside {0,16,32,64}; missing cu_seqlens
+    # prefill: chunk length outside {0,1,16,32,64}; missing cu_seqlens
     rc = lib.rwkv7_wkv_prefill(2, 1, 1, 4, fake, None, fake, 1, *[fake] * 6, fake, 48, None)
     assert rc == 1 and b"chunk_len" in lib.rwkv7_last_error()
     rc = lib.rwkv7_wkv_prefill(2, 1, 1, 4, None, None, fake, 1, *[fake] * 6, fake, 0, None)
     assert rc == 1 and b"cu_seqlens" in lib.rwkv7_last_error()
+    # inputs must be aligned to 4 elements (8 bytes for bf16, 16 for fp32), the state to 16 bytes
+    odd = P(16 + 2)
+    rc = lib.rwkv7_wkv_prefill(2, 1, 1, 4, fake, None, fake, 1, odd, *[fake] * 5, fake, 0, None)
+    assert rc == 1 and b"aligned" in lib.rwkv7_last_error()
+    rc = lib.rwkv7_wkv_decode(0, 1, 1, fake, 1, None, *[fake] * 5, P(16 + 8), fake, None)
+    assert rc == 1 and b"aligned" in lib.rwkv7_last_error()
+    rc = lib.rwkv7s_forward(2, 1, 2, 64, 1, P(16 + 8), *[fake] * 6, fake, None)
+    assert rc == 1 and b"aligned" in lib.rwkv7_last_error()
 
 
 def test_python_wrapper_raises_library_message(lib):
