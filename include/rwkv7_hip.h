@@ -145,20 +145,21 @@ int rwkv7_activation(int dtype, int kind, int64_t n, void *x, void *stream);
  *
  * rwkv7_tmix_prep: from the projection outputs r, k, v and the LoRA outputs
  * (w_lora = tanh(xw@w1)@w2, a_lora = (xa@a1)@a2, v_lora = (xv@v1)@v2), write the
- * six float32 WKV operands wkv_ops = {r, w_raw, k', v', -kk, kk*a} ([M, C] each)
- * and, on layer 0, v_first = v (float32 [M, C]; read on later layers).
+ * six WKV operands wkv_ops = {r, w_raw, k', v', -kk, kk*a} ([M, C] each, in the
+ * I/O dtype: the reference hands its WKV kernel tensors of the model dtype) and,
+ * on layer 0, v_first = v (float32 [M, C]; read on later layers).
  * Replaces model.py:215-227 and the operand construction of model.py:233-247.
  */
 int rwkv7_tmix_prep(int dtype, int64_t M, int64_t H, int layer0, const void *r, const void *k,
                     const void *v, const void *w_lora, const void *a_lora, const void *v_lora,
-                    float *v_first, const float *const *params, float *const *wkv_ops,
+                    float *v_first, const float *const *params, void *const *wkv_ops,
                     void *stream);
 
 /* out = (GroupNorm_H(y; ln_x, eps 64e-5) + sum_head(r*k'*r_k) * v') * g, from the
- * float32 WKV output y and the operands written by rwkv7_tmix_prep.
+ * WKV output y and the operands written by rwkv7_tmix_prep (all in the I/O dtype).
  * Replaces model.py:258-269 (before the output projection). */
-int rwkv7_tmix_post(int dtype, int64_t M, int64_t H, const float *y, const float *r_op,
-                    const float *k_op, const float *v_op, const void *g,
+int rwkv7_tmix_post(int dtype, int64_t M, int64_t H, const void *y, const void *r_op,
+                    const void *k_op, const void *v_op, const void *g,
                     const float *const *params, void *out, void *stream);
 
 /* Single-token fused path: rwkv7_tmix_prep + one WKV step on

@@ -192,10 +192,10 @@ hipError_t launch_activation(int kind, int64_t n, void* x, hipStream_t st);
 template <typename IO>
 hipError_t launch_tmix_prep(int M, int H, int layer0, const void* r, const void* k, const void* v,
                             const void* wl, const void* al, const void* vl, float* vfirst,
-                            const float* const* params, float* const* ops, hipStream_t st);
+                            const float* const* params, void* const* ops, hipStream_t st);
 template <typename IO>
-hipError_t launch_tmix_post(int M, int H, const float* y, const float* r_op, const float* k_op,
-                            const float* v_op, const void* g, const float* const* params, void* out,
+hipError_t launch_tmix_post(int M, int H, const void* y, const void* r_op, const void* k_op,
+                            const void* v_op, const void* g, const float* const* params, void* out,
                             hipStream_t st);
 template <typename IO>
 hipError_t launch_tmix_decode(int M, int H, int layer0, const void* r, const void* k, const void* v,
@@ -276,7 +276,7 @@ static bool params_ok(const float* const* p) {
 
 extern "C" int rwkv7_tmix_prep(int dtype, int64_t M, int64_t H, int layer0, const void* r, const void* k,
                                const void* v, const void* w_lora, const void* a_lora, const void* v_lora,
-                               float* v_first, const float* const* params, float* const* wkv_ops,
+                               float* v_first, const float* const* params, void* const* wkv_ops,
                                void* stream) {
     if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_prep: bad dtype code %d", dtype);
     if (M < 0 || bad_h(H) || M > kMaxInt)
@@ -293,8 +293,8 @@ extern "C" int rwkv7_tmix_prep(int dtype, int64_t M, int64_t H, int layer0, cons
     return launch_status(e, "tmix_prep_kernel");
 }
 
-extern "C" int rwkv7_tmix_post(int dtype, int64_t M, int64_t H, const float* y, const float* r_op,
-                               const float* k_op, const float* v_op, const void* g,
+extern "C" int rwkv7_tmix_post(int dtype, int64_t M, int64_t H, const void* y, const void* r_op,
+                               const void* k_op, const void* v_op, const void* g,
                                const float* const* params, void* out, void* stream) {
     if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_post: bad dtype code %d", dtype);
     if (M < 0 || bad_h(H) || M > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_post: bad sizes");

@@ -335,15 +335,17 @@ __device__ __forceinline__ PrepOut tmix_prep_elem(
     return o;
 }
 
-// Prefill: write the six fp32 WKV operands (r, w_raw, k, v, -kk, kk*a) of every
-// (row, head).  One wave per (row, head); grid (M, H/4), 256 threads.
+// Prefill: write the six WKV operands (r, w_raw, k, v, -kk, kk*a) of every
+// (row, head) in the I/O type, as the reference's model hands its WKV kernel
+// tensors of the model dtype (model.py:233-247).  One wave per (row, head);
+// grid (M, H/4), 256 threads.
 template <typename IO>
 __global__ __launch_bounds__(kThreads) void tmix_prep_kernel(
     int M, int H, int layer0, const IO* __restrict__ r, const IO* __restrict__ k,
     const IO* __restrict__ v, const IO* __restrict__ wl, const IO* __restrict__ al,
     const IO* __restrict__ vl, float* __restrict__ vfirst, TmixParams P,
-    float* __restrict__ r_op, float* __restrict__ w_op, float* __restrict__ k_op,
-    float* __restrict__ v_op, float* __restrict__ a_op, float* __restrict__ b_op)
+    IO* __restrict__ r_op, IO* __restrict__ w_op, IO* __restrict__ k_op,
+    IO* __restrict__ v_op, IO* __restrict__ a_op, IO* __restrict__ b_op)
 {
     typedef io_traits<IO> tr;
     const int m = blockIdx.x;
@@ -354,19 +356,19 @@ __global__ __launch_bounds__(kThreads) void tmix_prep_kernel(
     const int ch = h * RWKV7_HEAD + j;
     const size_t off = (size_t)m * C + ch;
     const PrepOut o = tmix_prep_elem(layer0, off, ch, r, k, v, wl, al, vl, vfirst, P);
-    r_op[off] = tr::to_f32(r[off]);
-    w_op[off] = o.w_raw;
-    k_op[off] = o.k;
-    v_op[off] = o.v;
-    a_op[off] = o.a_op;
-    b_op[off] = o.b_op;
+    r_op[off] = r[off];
+    w_op[off] = tr::from_f32(o.w_raw);
+    k_op[off] = tr::from_f32(o.k);
+    v_op[off] = tr::from_f32(o.v);
+    a_op[off] = tr::from_f32(o.a_op);
+    b_op[off] = tr::from_f32(o.b_op);
 }
 
 // Prefill: out = (GroupNorm_H(y) + (sum_j r_j k_j r_k_j) v) * g   (model.py:258-269)
 template <typename IO>
 __global__ __launch_bounds__(kThreads) void tmix_post_kernel(
-    int M, int H, const float* __restrict__ y, const float* __restrict__ r_op,
-    const float* __restrict__ k_op, const float* __restrict__ v_op, const IO* __restrict__ g,
+    int M, int H, const IO* __restrict__ y, const IO* __restrict__ r_op,
+    const IO* __restrict__ k_op, const IO* __restrict__ v_op, const IO* __restrict__ g,
     TmixParams P, IO* __restrict__ out)
 {
     typedef io_traits<IO> tr;
@@ -377,13 +379,13 @@ __global__ __launch_bounds__(kThreads) void tmix_post_kernel(
     const int C = H * RWKV7_HEAD;
     const int ch = h * RWKV7_HEAD + j;
     const size_t off = (size_t)m * C + ch;
-    const float yj = y[off];
+    const float yj = tr::to_f32(y[off]);
     const float mean = wave_sum(yj) * (1.0f / 64.0f);
     const float d = yj - mean;
     const float var = wave_sum(d * d) * (1.0f / 64.0f);
     const float yn = d / sqrtf(var + 64e-5f) * P.lnx_w[ch] + P.lnx_b[ch];
-    const float bonus = wave_sum(r_op[off] * k_op[off] * P.r_k[ch]);
-    out[off] = tr::from_f32((yn + bonus * v_op[off]) * tr::to_f32(g[off]));
+    const float bonus = wave_sum(tr::to_f32(r_op[off]) * tr::to_f32(k_op[off]) * P.r_k[ch]);
+    out[off] = tr::from_f32((yn + bonus * tr::to_f32(v_op[off])) * tr::to_f32(g[off]));
 }
 
 // Decode: one token per row, fused prep + WKV step + post.  One 64-lane wave
@@ -569,24 +571,24 @@ static TmixParams make_params(const float* const* p) {
 template <typename IO>
 hipError_t launch_tmix_prep(int M, int H, int layer0, const void* r, const void* k, const void* v,
                             const void* wl, const void* al, const void* vl, float* vfirst,
-                            const float* const* params, float* const* ops, hipStream_t st)
+                            const float* const* params, void* const* ops, hipStream_t st)
 {
     dim3 grid(M, (H + kWaves - 1) / kWaves);
     hipLaunchKernelGGL(tmix_prep_kernel<IO>, grid, dim3(kThreads), 0, st, M, H, layer0,
                        (const IO*)r, (const IO*)k, (const IO*)v, (const IO*)wl, (const IO*)al,
-                       (const IO*)vl, vfirst, make_params(params), ops[0], ops[1], ops[2], ops[3],
-                       ops[4], ops[5]);
+                       (const IO*)vl, vfirst, make_params(params), (IO*)ops[0], (IO*)ops[1], (IO*)ops[2],
+                       (IO*)ops[3], (IO*)ops[4], (IO*)ops[5]);
     return hipGetLastError();
 }
 
 template <typename IO>
-hipError_t launch_tmix_post(int M, int H, const float* y, const float* r_op, const float* k_op,
-                            const float* v_op, const void* g, const float* const* params, void* out,
+hipError_t launch_tmix_post(int M, int H, const void* y, const void* r_op, const void* k_op,
+                            const void* v_op, const void* g, const float* const* params, void* out,
                             hipStream_t st)
 {
     dim3 grid(M, (H + kWaves - 1) / kWaves);
-    hipLaunchKernelGGL(tmix_post_kernel<IO>, grid, dim3(kThreads), 0, st, M, H, y, r_op, k_op, v_op,
-                       (const IO*)g, make_params(params), (IO*)out);
+    hipLaunchKernelGGL(tmix_post_kernel<IO>, grid, dim3(kThreads), 0, st, M, H, (const IO*)y, (const IO*)r_op,
+                       (const IO*)k_op, (const IO*)v_op, (const IO*)g, make_params(params), (IO*)out);
     return hipGetLastError();
 }
 
@@ -615,9 +617,9 @@ hipError_t launch_tmix_decode(int M, int H, int layer0, const void* r, const voi
     template hipError_t launch_activation<IO>(int, int64_t, void*, hipStream_t);                   \
     template hipError_t launch_tmix_prep<IO>(int, int, int, const void*, const void*, const void*, \
                                              const void*, const void*, const void*, float*,        \
-                                             const float* const*, float* const*, hipStream_t);     \
-    template hipError_t launch_tmix_post<IO>(int, int, const float*, const float*, const float*,   \
-                                             const float*, const void*, const float* const*,       \
+                                             const float* const*, void* const*, hipStream_t);      \
+    template hipError_t launch_tmix_post<IO>(int, int, const void*, const void*, const void*,      \
+                                             const void*, const void*, const float* const*,        \
                                              void*, hipStream_t);                                  \
     template hipError_t launch_tmix_decode<IO>(int, int, int, const void*, const void*,            \
                                                const void*, const void*, const void*, const void*, \

@@ -465,9 +465,12 @@ class RWKV7Model(nn.Module):
         xk_ffn = torch.empty((1, M, C), dtype=dt, device=dev)
         v_first = torch.empty((M, C), dtype=torch.float32, device=dev)
         if not decode:
-            ops = torch.empty((6, M, C), dtype=torch.float32, device=dev)
+            # prefill WKV operands and output in the model dtype, as the reference
+            # passes them to its WKV kernel (model.py:233-250); bf16 / fp16 models
+            # then take the 16-bit chunked matrix-core kernel
+            ops = torch.empty((6, M, C), dtype=dt, device=dev)
             ops_ptrs = (ctypes.c_void_p * 6)(*[ops[i].data_ptr() for i in range(6)])
-            y = torch.empty((M, C), dtype=torch.float32, device=dev)
+            y = torch.empty((M, C), dtype=dt, device=dev)
         ffn_out = None
         S = pool.n_slots
         # decode rows of a bf16 model use the grouped MFMA GEMM (small M, many
