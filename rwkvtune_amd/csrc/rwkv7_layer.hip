@@ -440,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void tmix_decode_kernel(
     f32x4* sp = reinterpret_cast<f32x4*>(state + ((size_t)slot * H + h) * (RWKV7_HEAD * RWKV7_HEAD));
     f32x4 S[16];
 #pragma unroll
-    for (int mm = 0; mm < 16; ++mm) S[mm] = sp[64 * mm + l];
+    for (int mm = 0; mm < 16; ++mm) S[mm] = stream_load(sp + 64 * mm + l);
 
     float p[16];
 #pragma unroll
@@ -469,7 +469,7 @@ __global__ __launch_bounds__(kThreads) void tmix_decode_kernel(
         }
     }
 #pragma unroll
-    for (int mm = 0; mm < 16; ++mm) sp[64 * mm + l] = S[mm];
+    for (int mm = 0; mm < 16; ++mm) stream_store(sp + 64 * mm + l, S[mm]);
 
     // y of row i = 4c + gq, then GroupNorm over the head, bonus and gate
     const int i = 4 * c + gq;

@@ -4,7 +4,7 @@
 // exp(-exp(w_raw)), sa = S a, S <- S diag(w) + v k^T + sa b^T, y = S r), with
 // these design differences:
 //   * one 64-lane wave per (sequence, head) unit, state streamed with
-//     fully coalesced 128-bit accesses: lane l = 16g + c holds
+//     fully coalesced, non-temporal 128-bit accesses: lane l = 16g + c holds
 //     S[4m+g][4c..4c+3] for m = 0..15, so state access m of a wave covers
 //     the contiguous kilobyte [1024m, 1024m+1024) of the unit's 16 KB state;
 //   * row reductions (S a and S r) are DPP butterflies inside 16-lane rows
@@ -51,7 +51,7 @@ __global__ __launch_bounds__(64, 4) void wkv7_seq_kernel(
     f32x4* sp = reinterpret_cast<f32x4*>(state + ((size_t)slot * H + h) * (RWKV7_HEAD * RWKV7_HEAD));
     f32x4 S[16];
 #pragma unroll
-    for (int m = 0; m < 16; ++m) S[m] = sp[64 * m + l];
+    for (int m = 0; m < 16; ++m) S[m] = stream_load(sp + 64 * m + l);
 
     __shared__ float vsh[64];   // vsh[gg*16 + mm] = v[4mm + gg]
     __shared__ float sash[64];  // sash[gg*16 + cc] = sa[4cc + gg]
@@ -104,7 +104,7 @@ __global__ __launch_bounds__(64, 4) void wkv7_seq_kernel(
     }
 
 #pragma unroll
-    for (int m = 0; m < 16; ++m) sp[64 * m + l] = S[m];
+    for (int m = 0; m < 16; ++m) stream_store(sp + 64 * m + l, S[m]);
 }
 
 }  // namespace
