@@ -312,12 +312,14 @@ extern "C" int rwkv7_tmix_decode(int dtype, int64_t M, int64_t H, int layer0, co
                                  const void* g, float* v_first, const float* const* params, float* state_pool,
                                  int64_t pool_slots, const int32_t* row_slot, void* out, void* stream) {
     if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_decode: bad dtype code %d", dtype);
-    if (M < 0 || bad_h(H) || pool_slots < 0 || M > kMaxInt || pool_slots > kMaxInt)
+    if (M < 0 || bad_h(H) || pool_slots < 0 || M > kMaxInt || pool_slots > kMaxInt || M * H > kMaxInt)
         return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_decode: bad sizes (H must be a positive multiple of 4)");
     if (M == 0) return ok();
     if (!params || !params_ok(params) || !r || !k || !v || !w_lora || !a_lora || !g || !v_first ||
         !state_pool || !row_slot || !out)
         return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_decode: null pointer");
+    if (((uintptr_t)state_pool & 15) != 0)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_decode: state_pool must be aligned to 16 bytes");
     if (!layer0 && (!v_lora || !params[2]))
         return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_decode: layer > 0 needs v_lora and v0");
     hipError_t e;

@@ -33,6 +33,15 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
 __device__ __forceinline__ f32x4 stream_load(const f32x4* p) { return __builtin_nontemporal_load(p); }
 __device__ __forceinline__ void stream_store(f32x4* p, f32x4 v) { __builtin_nontemporal_store(v, p); }
 
+// Orders LDS writes before LDS reads of other lanes of the same wave (wave-scope
+// release / acquire around a wave barrier); enough where a wave only exchanges
+// data through its own LDS slice.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 template <typename IO> struct io_traits;
 
 template <> struct io_traits<float> {

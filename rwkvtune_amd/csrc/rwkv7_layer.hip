@@ -28,10 +28,19 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 
+// Sum over the 64 lanes of a wave, returned in every lane (all lanes active).
+// DPP butterflies inside each 16-lane row (lane ^1, ^2, ^7, ^15), then the four
+// row sums read from lanes 0, 16, 32, 48: no LDS round trips.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_xor1(v);
+    v += dpp_xor2(v);
+    v += dpp_xor7(v);
+    v += dpp_xor15(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
 }
 
 // Sum over the 256-thread block; `red` is kWaves floats of LDS.  Safe to call
@@ -389,11 +398,14 @@ __global__ __launch_bounds__(kThreads) void tmix_post_kernel(
 }
 
 // Decode: one token per row, fused prep + WKV step + post.  One 64-lane wave
-// per (row, head), four per block; the state of (slot, head) is streamed with
-// the same coalesced layout as the stand-alone decode kernel: lane l = 16g + c
-// holds S[4m+g][4c..4c+3] for m = 0..15.
+// per block and per (row, head), block index = row * H + head, so consecutive
+// blocks stream consecutive 16 KB states of the pool, and single-wave blocks
+// fill every free wave slot (measured on MI355X: 75% of HBM peak at 256 rows x
+// 32 heads, against 69% for four-wave blocks).  The state of (slot, head) is
+// streamed with the same coalesced layout as the stand-alone decode kernel:
+// lane l = 16g + c holds S[4m+g][4c..4c+3] for m = 0..15.
 template <typename IO>
-__global__ __launch_bounds__(kThreads) void tmix_decode_kernel(
+__global__ __launch_bounds__(64) void tmix_decode_kernel(
     int M, int H, int layer0, const IO* __restrict__ r, const IO* __restrict__ k,
     const IO* __restrict__ v, const IO* __restrict__ wl, const IO* __restrict__ al,
     const IO* __restrict__ vl, const IO* __restrict__ g, float* __restrict__ vfirst, TmixParams P,
@@ -401,12 +413,10 @@ __global__ __launch_bounds__(kThreads) void tmix_decode_kernel(
     IO* __restrict__ out)
 {
     typedef io_traits<IO> tr;
-    __shared__ float lds[kWaves][7][64];
-    const int wv = threadIdx.x >> 6;
-    const int m = blockIdx.x;
-    const int h = blockIdx.y * kWaves + wv;
-    if (h >= H) return;
-    const int l = threadIdx.x & 63;
+    __shared__ float sh[7][64];
+    const int m = blockIdx.x / H;
+    const int h = blockIdx.x - m * H;
+    const int l = threadIdx.x;
     const int C = H * RWKV7_HEAD;
     const size_t base = (size_t)m * C + (size_t)h * RWKV7_HEAD;
     int slot = row_slot[m];
@@ -415,19 +425,23 @@ __global__ __launch_bounds__(kThreads) void tmix_decode_kernel(
         out[base + l] = tr::from_f32(0.f);
         return;
     }
+    // state loads first, so their latency overlaps the element-wise prep
+    f32x4* sp = reinterpret_cast<f32x4*>(state + ((size_t)slot * H + h) * (RWKV7_HEAD * RWKV7_HEAD));
+    f32x4 S[16];
+#pragma unroll
+    for (int mm = 0; mm < 16; ++mm) S[mm] = stream_load(sp + 64 * mm + l);
 
     // element-wise prep, lane l = element l of the head
     const int chl = h * RWKV7_HEAD + l;
     const PrepOut o = tmix_prep_elem(layer0, base + l, chl, r, k, v, wl, al, vl, vfirst, P);
     const float bonus = wave_sum(o.rkr);
-    float (*sh)[64] = lds[wv];
     sh[0][l] = tr::to_f32(r[base + l]);
     sh[1][l] = expf(-expf(o.w_raw));  // decay (wkv7s.cu:27)
     sh[2][l] = o.k;
     sh[3][l] = o.a_op;
     sh[4][l] = o.b_op;
     sh[5][(l & 3) * 16 + (l >> 2)] = o.v;  // sh[5][gg*16+mm] = v[4mm+gg]
-    __syncthreads();
+    wave_sync();  // single-wave block: a wave barrier orders the LDS exchange
 
     const int gq = l >> 4;
     const int c = l & 15;
@@ -437,16 +451,11 @@ __global__ __launch_bounds__(kThreads) void tmix_decode_kernel(
     const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sh[3][4 * c]);
     const f32x4 b4 = *reinterpret_cast<const f32x4*>(&sh[4][4 * c]);
 
-    f32x4* sp = reinterpret_cast<f32x4*>(state + ((size_t)slot * H + h) * (RWKV7_HEAD * RWKV7_HEAD));
-    f32x4 S[16];
-#pragma unroll
-    for (int mm = 0; mm < 16; ++mm) S[mm] = stream_load(sp + 64 * mm + l);
-
     float p[16];
 #pragma unroll
     for (int mm = 0; mm < 16; ++mm) p[mm] = fast_dot4(a4, S[mm]);
     sh[6][gq * 16 + c] = row16_reduce_scatter(p, c);  // sa[4c+gq]
-    __syncthreads();
+    wave_sync();
 
     const f32x4* vq = reinterpret_cast<const f32x4*>(&sh[5][gq * 16]);
     const f32x4* sq = reinterpret_cast<const f32x4*>(&sh[6][gq * 16]);
@@ -598,8 +607,7 @@ hipError_t launch_tmix_decode(int M, int H, int layer0, const void* r, const voi
                               float* vfirst, const float* const* params, float* state, int pool_slots,
                               const int32_t* row_slot, void* out, hipStream_t st)
 {
-    dim3 grid(M, (H + kWaves - 1) / kWaves);
-    hipLaunchKernelGGL(tmix_decode_kernel<IO>, grid, dim3(kThreads), 0, st, M, H, layer0,
+    hipLaunchKernelGGL(tmix_decode_kernel<IO>, dim3((unsigned)M * (unsigned)H), dim3(64), 0, st, M, H, layer0,
                        (const IO*)r, (const IO*)k, (const IO*)v, (const IO*)wl, (const IO*)al,
                        (const IO*)vl, (const IO*)g, vfirst, make_params(params), state, pool_slots,
                        row_slot, (IO*)out);
