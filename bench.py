@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of rwkvtune's batched-generation hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|decode|prefill]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|decode|prefill|tmix]
 
 Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a message.
 
@@ -17,6 +17,9 @@ rollout (default)  GRPO rollout on RWKV-7 1.5B (L=24, C=2048, H=32, V=65536), bf
     result assembly included).
 decode             isolated WKV7 decode kernel at B=256 slots, H=32 (cfg2); a step is
     one launch; value = algorithmic GB/s.
+tmix               the fused decode time-mix kernel alone at the rollout shape (the
+    roofline kernel of the default line), plus a plain copy of known size; for
+    kernel-trace and PMC runs.
 prefill            chunked WKV7 prefill of cfg3 (64 ragged prompts ~U(64, 2048), H=32)
     in one launch; value = prompt tokens/s; roofline = bf16 MFMA rate executed
     (three part products per contraction) against the 2.5 PFLOP/s dense peak.
@@ -92,6 +95,26 @@ def time_launches(fn, n_iter, stream):
     e1.record(stream)
     e1.synchronize()
     return e0.elapsed_time(e1) * 1e3 / n_iter  # us
+
+
+# HBM traffic of one tmix_decode launch at the leg's shape, from rocprofv3 --pmc runs of
+# `bench.py --workload tmix` (profiles/tmix_decode_rollout_shape_pmc.md): FETCH_SIZE and
+# WRITE_SIZE means in KiB per dispatch, each scaled by the same counter's reading for a
+# plain copy of known size in the same run (FETCH reads 0.5x, WRITE 1.0x of the true bytes)
+TMIX_PMC_FETCH_KIB, TMIX_PMC_WRITE_KIB = 70238.7, 132118.2
+PMC_FETCH_SCALE, PMC_WRITE_SCALE = 131072.0 / 65547.6, 131072.0 / 131072.0
+TMIX_TRAFFIC_BYTES = (TMIX_PMC_FETCH_KIB * PMC_FETCH_SCALE + TMIX_PMC_WRITE_KIB * PMC_WRITE_SCALE) * 1024
+
+
+def copy_reference(dev, n_bytes=256 * 32 * 64 * 64 * 4, reps=8):
+    """Plain device copy of a known size (the PMC counters' scale reference)."""
+    n = n_bytes // 4
+    src = torch.ones(n, device=dev)
+    dst = torch.zeros(n, device=dev)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return n_bytes
 
 
 def tmix_decode_leg(dev, iters=480):
@@ -314,7 +337,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="rollout", choices=["rollout", "decode", "prefill"])
+    ap.add_argument("--workload", default="rollout", choices=["rollout", "decode", "prefill", "tmix"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -359,12 +382,30 @@ def main():
                        "decode_steps": ro["runs"][-1]["decode_steps"],
                        "prefill_s": ro["runs"][-1]["prefill_s"], "decode_s": ro["runs"][-1]["decode_s"]},
             "roofline": {"bound": "hbm", "achieved": tm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": tm["frac"], "traffic": None, "kernel": tm["kernel"],
-                         "us_per_launch": tm["us_per_launch"]},
+                         "frac": tm["frac"], "traffic": TMIX_TRAFFIC_BYTES, "kernel": tm["kernel"],
+                         "us_per_launch": tm["us_per_launch"], "algorithmic_bytes": tm["bytes_per_launch"]},
             "wkv7_decode_cfg2": {"GBs": wk["GBs"], "frac": wk["frac"], "us_per_step": wk["us_per_step"]},
             "wkv7_prefill_cfg3": {k: pf[k] for k in ("us_per_launch", "tokens_per_s", "mfma_bf16_TFLOPs",
                                                      "mfma_frac", "GBs", "hbm_frac", "speedup_vs_token_serial")},
             "cpu_baseline": cpu,
+        }
+    elif a.workload == "tmix":
+        # the roofline kernel alone (for kernel-trace / PMC runs), then a plain copy of
+        # known size that scales the PMC byte counters
+        steps = 480 if a.steps is None else a.steps
+        warmup = 48 if a.warmup is None else a.warmup
+        tm = tmix_decode_leg(dev, iters=steps)
+        ref = copy_reference(dev)
+        out = {
+            "metric": METRIC, "value": tm["GBs"], "unit": "GB/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+            "ms_per_step": tm["us_per_launch"] / 1e3, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16 I/O, fp32 state and element-wise", "data": "synthetic",
+            "config": {"workload": "fused decode time-mix (tmix_decode_kernel) at the cfg4 decode shape: 256 rows, "
+                                   "H=32, 24 rotating layer pools", "copy_reference_bytes": ref},
+            "roofline": {"bound": "hbm", "achieved": tm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": tm["frac"], "traffic": TMIX_TRAFFIC_BYTES, "kernel": tm["kernel"],
+                         "us_per_launch": tm["us_per_launch"], "algorithmic_bytes": tm["bytes_per_launch"]},
+            "cpu_baseline": None,
         }
     elif a.workload == "prefill":
         steps = 20 if a.steps is None else a.steps
