@@ -179,7 +179,7 @@ int rwkv7_tmix_decode(int dtype, int64_t M, int64_t H, int layer0, const void *r
  *   C_i[M, N_i] = act_in_i(A_i[M, K_i]) . B_i[N_i, K_i]^T,  then epi_i on C_i,
  * with A_i, B_i, C_i bf16 row-major with row strides lda_i, ldb_i, ldc_i
  * (B in nn.Linear [out][in] layout), float32 accumulation.  act_in: 0 none,
- * 1 tanh, 2 sigmoid; epi: 0 none, 1 relu(x)^2.  K_i % 32 == 0, lda/ldb
+ * 1 tanh, 2 sigmoid; epi: 0 none, 1 relu(x)^2, 2 tanh, 3 sigmoid.  K_i % 32 == 0, lda/ldb
  * multiples of 8 and >= K_i, A/B 16-byte aligned.  The pointer and size
  * arrays are host arrays of `count` entries.  Problems whose K is split across
  * blocks write float32 partial tiles to `workspace` (contents need no

@@ -537,8 +537,8 @@ extern "C" int rwkv7_gemm_decode(int64_t M, int count, const void* const* A, con
                         "rwkv7_gemm_decode: problem %d: lda/ldb >= K and %% 8 == 0, ldc >= N required", i);
         if ((((uintptr_t)A[i]) | ((uintptr_t)B[i])) & 15)
             return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: A and B must be 16-byte aligned", i);
-        if (act_in[i] < 0 || act_in[i] > 2 || epi[i] < 0 || epi[i] > 1)
-            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: act_in in 0..2, epi in 0..1", i);
+        if (act_in[i] < 0 || act_in[i] > 2 || epi[i] < 0 || epi[i] > 3)
+            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: act_in in 0..2, epi in 0..3", i);
         tiles += ((M + 63) / 64) * (int64_t)((N[i] + 63) / 64) * 16;
     }
     if (tiles > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: too many tiles");

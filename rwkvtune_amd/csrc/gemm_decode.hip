@@ -1,38 +1,44 @@
 // Grouped bf16 GEMM for the decode step's projections on gfx950 MFMA.
 //
 // At decode the model's dense projections have M = live slots (<= 256) rows:
-// r / k / v / output (C x C), the LoRA pairs (C x 64..256 and back), the FFN
-// (C x 4C, 4C x C) and the head (C x V).  A library GEMM call costs ~10 us at
-// these sizes whatever the work, and a layer needs 14 of them; here one launch
-// runs up to 8 independent problems
-//     C_p[M, N_p] = act_in_p(A_p[M, K_p]) . B_p[N_p, K_p]^T      (epi_p applied to C_p)
+// r / k / v / output (C x C), the LoRA pairs (C x 64..480 and back), the FFN
+// (C x 4C, 4C x C).  One launch runs up to 8 independent problems
+//     C_p[M, N_p] = epi_p( act_in_p(A_p[M, K_p]) . B_p[N_p, K_p]^T )
 // with B in nn.Linear layout [out][in] (row-major N x K), bf16 in, fp32
 // accumulate, bf16 out.  act_in: 0 none, 1 tanh, 2 sigmoid (the activations
 // between the LoRA down and up projections, model.py:211, 221); epi: 0 none,
-// 1 relu(x)^2 (FFN key, model.py:337).
+// 1 relu(x)^2 (FFN key, model.py:337), 2 tanh, 3 sigmoid (the same LoRA
+// activations applied to a down projection's output instead).
 //
-// Tiling: a 256-thread block computes a 64 x 64 tile of one problem over one
-// K range; its four waves own 32 x 32 quadrants as 2 x 2 blocks of
-// v_mfma_f32_16x16x32_bf16.  K is staged through LDS 128 at a time,
-// double-buffered (the global loads of stage s+1 are in flight during stage s).
-// MFMA operand layout (gfx950, checked on the device): lane l holds row l%16 of
-// the A block and row l%16 of the B block, k = 8*(l/16) .. +7; accumulator i
-// of lane l is C[4*(l/16) + i][l%16].
-//
-// Split-K: with M <= 256 a C x C projection has only 128 tiles, too few blocks
-// to keep HBM busy, so each problem's K is cut into `splits` ranges.  Each range
-// writes its float32 partial tile to the caller's workspace and a second kernel
-// sums the ranges in split order (deterministic) and applies the epilogue.
+// At M = 256 the weights are read once per 64-row block of A and every block
+// is short, so memory latency, not bandwidth or the matrix cores, bounds a
+// naive tiling.  Here:
+//   * a 256-thread block computes a 64 x 64 tile; each wave owns a 32 x 32
+//     quadrant (v_mfma_f32_32x32x16_bf16);
+//   * K is staged through LDS 64 at a time, and the global loads of the next
+//     four stages are in flight in registers while one stage computes (a ring
+//     of named registers: arrays indexed in loops would be placed in scratch);
+//   * blocks are ordered so that the row tiles and K ranges of one column tile
+//     run back to back on one XCD (blocks are dealt to the 8 XCDs round-robin),
+//     where they share the weight rows through that XCD's L2;
+//   * problems with too few tiles to fill the GPU split K; each range writes a
+//     float32 partial tile to the caller's workspace and gemm_reduce_kernel sums
+//     the ranges in order (deterministic) and applies the epilogue.
+// MFMA operand layout (gfx950): lane l supplies row l%32 of A and of B, k =
+// 8*(l/32) .. +7; accumulator q of lane l is C[8*(q/4) + 4*(l/32) + q%4][l%32].
 #include "common.hpp"
 
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMaxProblems = 8;
-constexpr int TM = 64, TN = 64, TK = 128, NCH = TK / 32;
-constexpr int LDS_STRIDE = TK + 8;  // bf16 elements per LDS row (padding against bank conflicts)
+constexpr int TM = 64, TN = 64, BK = 64;
+constexpr int LS = BK + 8;             // LDS row stride (bf16), padded against bank conflicts
+constexpr int RING = 4;                // stages of global loads in flight
 constexpr int TILE_ELEMS = TM * TN;
+constexpr int kThreads = 256;
 
 struct GemmProblem {
     const bf16_t* A;
@@ -42,10 +48,11 @@ struct GemmProblem {
     int64_t ws_off;   // float offset of this problem's partials in the workspace
     int N, K;
     int act_in, epi;
-    int tile_begin;   // first block index of this problem
-    int n_tiles_n;    // tiles along N
+    int block_begin;  // first block of this problem (a multiple of 8)
+    int n_tiles;      // tiles along N
+    int n_groups;     // ceil(n_tiles / 8)
     int splits;       // K ranges
-    int k_per;        // K per range (multiple of 32)
+    int k_per;        // K per range (multiple of BK)
     int red_begin;    // first block of this problem in gemm_reduce_kernel
 };
 
@@ -54,8 +61,6 @@ struct GemmBatch {
     int count;
     int M;
 };
-
-__device__ __forceinline__ uint4 sel(uint4 v, bool ok) { return ok ? v : make_uint4(0, 0, 0, 0); }
 
 __device__ __forceinline__ float act_fn(int act, float x) {
     if (act == 1) return tanhf(x);
@@ -80,12 +85,16 @@ __device__ __forceinline__ float epi_fn(int epi, float v) {
         v = v > 0.f ? v : 0.f;
         return v * v;
     }
+    if (epi == 2) return tanhf(v);
+    if (epi == 3) return 1.0f / (1.0f + expf(-v));
     return v;
 }
 
-__global__ __launch_bounds__(256) void gemm_decode_kernel(GemmBatch batch, float* __restrict__ ws) {
-    __shared__ __align__(16) bf16_t As[2][TM * LDS_STRIDE];
-    __shared__ __align__(16) bf16_t Bs[2][TN * LDS_STRIDE];
+__device__ __forceinline__ uint4 sel(uint4 v, bool ok) { return ok ? v : make_uint4(0u, 0u, 0u, 0u); }
+
+__global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmBatch batch, float* __restrict__ ws) {
+    __shared__ __attribute__((aligned(16))) bf16_t As[2][TM * LS];
+    __shared__ __attribute__((aligned(16))) bf16_t Bs[2][TN * LS];
 
     // select the block's problem with constant indices only (a dynamic index
     // into the kernel-argument struct would copy it to scratch memory)
@@ -93,123 +102,99 @@ __global__ __launch_bounds__(256) void gemm_decode_kernel(GemmBatch batch, float
     GemmProblem P = batch.p[0];
 #pragma unroll
     for (int i = 1; i < kMaxProblems; ++i)
-        if (i < batch.count && bid >= batch.p[i].tile_begin) P = batch.p[i];
-    const int local = bid - P.tile_begin;
-    const int split = local % P.splits;
-    const int tile = local / P.splits;
-    const int tn = tile % P.n_tiles_n;
-    const int tm = tile / P.n_tiles_n;
+        if (i < batch.count && bid >= batch.p[i].block_begin) P = batch.p[i];
     const int M = batch.M;
-    const int m0 = tm * TM, n0 = tn * TN;
-    const int k_beg = split * P.k_per;
-    const int k_end = min(P.K, k_beg + P.k_per);
-    const int nstage = (k_end - k_beg + TK - 1) / TK;
+    const int mt = (M + TM - 1) / TM;
+    const int local = bid - P.block_begin;
+    const int xcd = local & 7, j = local >> 3;  // block_begin is a multiple of 8: same XCD as bid
+    const int per = mt * P.splits;
+    const int ntile = (j / per) * 8 + xcd;
+    if (ntile >= P.n_tiles) return;  // padding block of the last column group
+    const int rem = j % per;
+    const int mtile = rem % mt, split = rem / mt;
+    const int m0 = mtile * TM, n0 = ntile * TN;
+    const int kb = split * P.k_per;
+    const int ke = min(P.K, kb + P.k_per);
+    const int nst = (ke - kb + BK - 1) / BK;
 
-    const int t = threadIdx.x;
-    const int lane = t & 63;
-    const int wave = t >> 6;
-    const int wm = (wave >> 1) * 32;  // wave quadrant
-    const int wn = (wave & 1) * 32;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
 
-    // global -> LDS: thread t moves row t/4 of the A and B tiles, k chunk
-    // (t%4)*8 of each 32-wide slice of a stage (NCH slices per stage).  Rows
-    // past M / N and slices past k_end are loaded from a valid address and
-    // zeroed, so every load is an unconditional 16-byte global load.
-    const int lr = t >> 2;
-    const int lk = (t & 3) * 8;
-    const bool a_ok = (m0 + lr) < M;
-    const bool b_ok = (n0 + lr) < P.N;
-    const bf16_t* a_row = P.A + (int64_t)(a_ok ? m0 + lr : M - 1) * P.lda + lk;
-    const bf16_t* b_row = P.B + (int64_t)(b_ok ? n0 + lr : P.N - 1) * P.ldb + lk;
+    // global -> LDS: thread t moves 16-byte chunks t and t + 256 of the A tile and
+    // of the B tile per stage (64 rows x 8 chunks).  Rows past M / N read a valid
+    // row (their results are not stored); chunks past the K range are zeroed.
+    const int r0 = t >> 3, kq = (t & 7) * 8;     // chunk t: row r0, k offset kq; chunk t+256: row r0 + 32
+    const bf16_t* a0 = P.A + (int64_t)min(m0 + r0, M - 1) * P.lda + kb + kq;
+    const bf16_t* a1 = P.A + (int64_t)min(m0 + r0 + 32, M - 1) * P.lda + kb + kq;
+    const bf16_t* b0 = P.B + (int64_t)min(n0 + r0, P.N - 1) * P.ldb + kb + kq;
+    const bf16_t* b1 = P.B + (int64_t)min(n0 + r0 + 32, P.N - 1) * P.ldb + kb + kq;
+    const int l0 = r0 * LS + kq, l1 = (r0 + 32) * LS + kq;
+    const int kspan = ke - kb;
 
-    f32x4 acc[2][2];
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    uint4 ra[NCH], rb[NCH];
-    auto load_stage = [&](int s) {
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            const int k = k_beg + s * TK + 32 * c;  // start of the 32-wide slice
-            const bool kv = k < k_end;
-            const int ko = kv ? k : k_beg;
-            ra[c] = sel(*reinterpret_cast<const uint4*>(a_row + ko), a_ok && kv);
-            rb[c] = sel(*reinterpret_cast<const uint4*>(b_row + ko), b_ok && kv);
-        }
-    };
-    auto store_stage = [&](int buf) {
-#pragma unroll
-        for (int c = 0; c < NCH; ++c) {
-            *reinterpret_cast<uint4*>(&As[buf][lr * LDS_STRIDE + lk + 32 * c]) = apply_act8(ra[c], P.act_in);
-            *reinterpret_cast<uint4*>(&Bs[buf][lr * LDS_STRIDE + lk + 32 * c]) = rb[c];
-        }
-    };
-
-    if (nstage > 0) {
-        load_stage(0);
-        store_stage(0);
+    uint4 ga0_0, ga1_0, gb0_0, gb1_0, ga0_1, ga1_1, gb0_1, gb1_1;
+    uint4 ga0_2, ga1_2, gb0_2, gb1_2, ga0_3, ga1_3, gb0_3, gb1_3;
+#define GD_LOAD(p, st)                                                                   \
+    {                                                                                    \
+        const int ko = (st) * BK;                                                        \
+        const bool ok = ko + kq < kspan;                                                 \
+        const int kc = ok ? ko : -kq;  /* past the range: re-read the range's first chunk */ \
+        ga0_##p = sel(*reinterpret_cast<const uint4*>(a0 + kc), ok);                     \
+        ga1_##p = sel(*reinterpret_cast<const uint4*>(a1 + kc), ok);                     \
+        gb0_##p = sel(*reinterpret_cast<const uint4*>(b0 + kc), ok);                     \
+        gb1_##p = sel(*reinterpret_cast<const uint4*>(b1 + kc), ok);                     \
     }
-    __syncthreads();
-    for (int s = 0; s < nstage; ++s) {
-        const int cur = s & 1;
-        if (s + 1 < nstage) load_stage(s + 1);
-#pragma unroll
-        for (int ks = 0; ks < NCH; ++ks) {
-            bf16x8_t af[2], bf[2];
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int row = wm + i * 16 + (lane & 15);
-                af[i] = *reinterpret_cast<const bf16x8_t*>(&As[cur][row * LDS_STRIDE + 32 * ks + (lane >> 4) * 8]);
-            }
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int col = wn + j * 16 + (lane & 15);
-                bf[j] = *reinterpret_cast<const bf16x8_t*>(&Bs[cur][col * LDS_STRIDE + 32 * ks + (lane >> 4) * 8]);
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (s + 1 < nstage) store_stage(cur ^ 1);
-        __syncthreads();
-    }
+    GD_LOAD(0, 0)
+    GD_LOAD(1, min(1, nst - 1))
+    GD_LOAD(2, min(2, nst - 1))
+    GD_LOAD(3, min(3, nst - 1))
 
-    // accumulator i of lane l is C[4*(l/16)+i][l%16] of its 16x16 block
+    f32x16 acc = {0.f};
+    const int r = lane & 31, kg = (lane >> 5) * 8;
+    const int act = P.act_in;
+#define GD_STEP(p)                                                                       \
+    if (s0 + (p) < nst) {                                                                \
+        const int s = s0 + (p);                                                          \
+        const int buf = s & 1;                                                           \
+        *reinterpret_cast<uint4*>(&As[buf][l0]) = apply_act8(ga0_##p, act);              \
+        *reinterpret_cast<uint4*>(&As[buf][l1]) = apply_act8(ga1_##p, act);              \
+        *reinterpret_cast<uint4*>(&Bs[buf][l0]) = gb0_##p;                               \
+        *reinterpret_cast<uint4*>(&Bs[buf][l1]) = gb1_##p;                               \
+        __syncthreads();                                                                 \
+        GD_LOAD(p, min(s + RING, nst - 1))                                               \
+        _Pragma("unroll") for (int kk = 0; kk < BK; kk += 16) {                          \
+            const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(&As[buf][(wm + r) * LS + kk + kg]); \
+            const bf16x8_t bf = *reinterpret_cast<const bf16x8_t*>(&Bs[buf][(wn + r) * LS + kk + kg]); \
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc, 0, 0, 0);         \
+        }                                                                                \
+    }
+    // One barrier per stage: stage s writes LDS buffer s&1, which every wave
+    // finished reading (stage s-2) before it reached stage s-1's barrier.
+    for (int s0 = 0; s0 < nst; s0 += RING) {
+        GD_STEP(0) GD_STEP(1) GD_STEP(2) GD_STEP(3)
+    }
+#undef GD_STEP
+#undef GD_LOAD
+
     if (P.splits == 1) {
+        const int col = n0 + wn + (lane & 31);
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int col = n0 + wn + j * 16 + (lane & 15);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int row = m0 + wm + i * 16 + 4 * (lane >> 4) + e;
-                    if (row < M && col < P.N)
-                        P.C[(int64_t)row * P.ldc + col] = f32_to_bf16(epi_fn(P.epi, acc[i][j][e]));
-                }
-            }
+        for (int q = 0; q < 16; ++q) {
+            const int row = m0 + wm + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+            if (row < M && col < P.N) P.C[(int64_t)row * P.ldc + col] = f32_to_bf16(epi_fn(P.epi, acc[q]));
+        }
         return;
     }
-
     // split-K: publish this range's partial tile; gemm_reduce_kernel, launched
     // next on the same stream, sums the ranges (a kernel boundary is what makes
     // another block's writes visible: the L2 of each XCD is private)
-    const int ntile = ((M + TM - 1) / TM) * P.n_tiles_n;
-    float* part = ws + P.ws_off + ((int64_t)split * ntile + tile) * TILE_ELEMS;
+    const int tile = mtile * P.n_tiles + ntile;
+    const int ntiles = mt * P.n_tiles;
+    float* part = ws + P.ws_off + ((int64_t)split * ntiles + tile) * TILE_ELEMS;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int r = wm + i * 16 + 4 * (lane >> 4) + e;
-                const int c = wn + j * 16 + (lane & 15);
-                part[r * TN + c] = acc[i][j][e];
-            }
+    for (int q = 0; q < 16; ++q) {
+        const int rr = wm + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+        part[rr * TN + wn + (lane & 31)] = acc[q];
+    }
 }
 
 // Sum the split-K partial tiles in split order (deterministic), apply the
@@ -223,11 +208,12 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmBatch batch, const
         if (i < batch.count && bid >= batch.p[i].red_begin) P = batch.p[i];
     const int tile = bid - P.red_begin;
     const int M = batch.M;
-    const int ntile = ((M + TM - 1) / TM) * P.n_tiles_n;
-    if (P.splits <= 1 || tile >= ntile) return;
-    const int m0 = (tile / P.n_tiles_n) * TM, n0 = (tile % P.n_tiles_n) * TN;
+    const int mt = (M + TM - 1) / TM;
+    const int ntiles = mt * P.n_tiles;
+    if (P.splits <= 1 || tile >= ntiles) return;
+    const int m0 = (tile / P.n_tiles) * TM, n0 = (tile % P.n_tiles) * TN;
     const float* base = ws + P.ws_off + (int64_t)tile * TILE_ELEMS;
-    const int64_t stride = (int64_t)ntile * TILE_ELEMS;
+    const int64_t stride = (int64_t)ntiles * TILE_ELEMS;
     for (int e = threadIdx.x; e < TILE_ELEMS; e += 256) {
         float v = 0.f;
         for (int s = 0; s < P.splits; ++s) v += base[s * stride + e];
@@ -236,30 +222,29 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmBatch batch, const
     }
 }
 
-// Split counts per problem so that the launch has about 640 blocks, each K
-// range a multiple of 32 and at least 256 wide; also the workspace floats and
-// the tiles the reduction pass covers.
+// Split counts: when the launch's tiles alone would not reach ~384 blocks
+// (1.5 per CU), every problem splits K into equal ranges of at least 1024 (a
+// multiple of BK), at most 8; also the workspace floats and the tiles the
+// reduction pass covers.
 void plan(int M, int count, const int* N, const int* K, int* splits, int* k_per, int64_t* ws_floats,
           int64_t* red_tiles) {
     const int mt = (M + TM - 1) / TM;
-    int64_t tiles = 0;
-    for (int i = 0; i < count; ++i) tiles += (int64_t)mt * ((N[i] + TN - 1) / TN);
-    const int64_t target = 640;
-    int s = (int)((target + tiles - 1) / tiles);
-    if (s < 1) s = 1;
-    if (s > 16) s = 16;
+    int64_t total = 0;
+    for (int i = 0; i < count; ++i) total += (int64_t)mt * ((N[i] + TN - 1) / TN);
+    const int want = (int)((384 + total - 1) / total);
     *ws_floats = 0;
     *red_tiles = 0;
     for (int i = 0; i < count; ++i) {
-        int si = s;
-        const int max_by_k = K[i] / 256;
+        const int64_t nt = (int64_t)mt * ((N[i] + TN - 1) / TN);
+        int si = want;
+        const int max_by_k = K[i] / 1024;
         if (si > max_by_k) si = max_by_k < 1 ? 1 : max_by_k;
+        if (si > 8) si = 8;
         int kp = (K[i] + si - 1) / si;
-        kp = (kp + 31) / 32 * 32;
+        kp = (kp + BK - 1) / BK * BK;
         si = (K[i] + kp - 1) / kp;
         splits[i] = si;
         k_per[i] = kp;
-        const int64_t nt = (int64_t)mt * ((N[i] + TN - 1) / TN);
         if (si > 1) {
             *ws_floats += (int64_t)si * nt * TILE_ELEMS;
             *red_tiles += nt;
@@ -290,7 +275,7 @@ hipError_t launch_gemm_decode(int M, int count, const void* const* A, const void
     int64_t wsf = 0, red = 0;
     plan(M, count, N, K, splits, k_per, &wsf, &red);
     const int mt = (M + TM - 1) / TM;
-    int tiles = 0, red_tiles = 0;
+    int blocks = 0, red_tiles = 0;
     int64_t ws_off = 0;
     for (int i = 0; i < count; ++i) {
         GemmProblem& p = b.p[i];
@@ -304,20 +289,21 @@ hipError_t launch_gemm_decode(int M, int count, const void* const* A, const void
         p.K = K[i];
         p.act_in = act_in[i];
         p.epi = epi[i];
-        p.n_tiles_n = (N[i] + TN - 1) / TN;
+        p.n_tiles = (N[i] + TN - 1) / TN;
+        p.n_groups = (p.n_tiles + 7) / 8;
         p.splits = splits[i];
         p.k_per = k_per[i];
-        p.tile_begin = tiles;
+        p.block_begin = blocks;
         p.ws_off = ws_off;
         p.red_begin = red_tiles;
-        const int nt = mt * p.n_tiles_n;
-        tiles += nt * p.splits;
+        blocks += 8 * p.n_groups * mt * p.splits;
+        const int nt = mt * p.n_tiles;
         if (p.splits > 1) {
             ws_off += (int64_t)p.splits * nt * TILE_ELEMS;
             red_tiles += nt;
         }
     }
-    hipLaunchKernelGGL(gemm_decode_kernel, dim3(tiles), dim3(256), 0, st, b, ws);
+    hipLaunchKernelGGL(gemm_decode_kernel, dim3(blocks), dim3(kThreads), 0, st, b, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || red_tiles == 0) return e;
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3(red_tiles), dim3(256), 0, st, b, (const float*)ws);

@@ -324,9 +324,13 @@ class RWKV7Model(nn.Module):
         self.ln_out = nn.LayerNorm(config.n_embd)
         self.head = nn.Linear(config.n_embd, config.vocab_size, bias=False)
         self._packs = None
-        # the library's grouped MFMA GEMM for decode projections; off by default:
-        # hipBLASLt's batched GEMMs are faster at these shapes on this stack
-        self.use_grouped_gemm = False
+        # decode rows of a bf16 model run the seven projections of the token-shift
+        # mixes (r, k, v and the LoRA downs, with tanh / sigmoid fused) as one launch
+        # of the library's grouped MFMA GEMM; measured in HIP graphs at 256 rows it
+        # beats the batched library calls plus their activation launches, while the
+        # remaining projections stay library GEMMs (faster there)
+        self.use_grouped_gemm = True
+        self._lora_h = {}
 
     # -- bookkeeping ---------------------------------------------------------
 
@@ -492,27 +496,27 @@ class RWKV7Model(nn.Module):
                           P(pk.mix7), P(mixes), st)
             xr, xk, xv, xw, xa, xg, _ = mixes.unbind(0)
             if grouped:
-                # two grouped launches: the seven projections of the six mixes, then
-                # the four LoRA up-projections with tanh / sigmoid on their inputs
+                # one grouped launch: r, k, v and the LoRA downs of the six mixes, tanh
+                # (w) and sigmoid (g) as epilogues; the downs land in a zero-padded
+                # [n][M][D] buffer (padding columns are never written) for the batched
+                # LoRA-up product
                 lt = pk.lora_t
-                r, k, v = (torch.empty((M, C), dtype=dt, device=dev) for _ in range(3))
-                hw = torch.empty((M, lt["w1"].shape[0]), dtype=dt, device=dev)
-                ha = torch.empty((M, lt["a1"].shape[0]), dtype=dt, device=dev)
-                hg = torch.empty((M, lt["g1"].shape[0]), dtype=dt, device=dev)
+                nl, D = pk.lora_down.shape[0], pk.lora_down.shape[2]
+                key = (dev, M, nl, D)
+                hbuf = self._lora_h.get(key)
+                if hbuf is None:
+                    hbuf = self._lora_h[key] = torch.zeros((nl, M, D), dtype=dt, device=dev)
+                rkv = torch.empty((3, M, C), dtype=dt, device=dev)
+                r, k, v = rkv.unbind(0)
+                dn = [("w1", 0, 2), ("a1", 1, 0), ("g1", 2, 3)] + ([] if l == 0 else [("v1", 3, 0)])
+                src = {"w1": xw, "a1": xa, "g1": xg, "v1": xv}
                 probs = [(xr, att.receptance.weight, r, 0, 0), (xk, att.key.weight, k, 0, 0),
-                         (xv, att.value.weight, v, 0, 0), (xw, lt["w1"], hw, 0, 0), (xa, lt["a1"], ha, 0, 0),
-                         (xg, lt["g1"], hg, 0, 0)]
-                if l > 0:
-                    hv = torch.empty((M, lt["v1"].shape[0]), dtype=dt, device=dev)
-                    probs.append((xv, lt["v1"], hv, 0, 0))
+                         (xv, att.value.weight, v, 0, 0)]
+                probs += [(src[n], lt[n], hbuf[i, :, :lt[n].shape[0]], 0, e) for n, i, e in dn]
                 self._gemm_group(M, probs, st)
-                wl, al, g = (torch.empty((M, C), dtype=dt, device=dev) for _ in range(3))
-                probs = [(hw, lt["w2"], wl, 1, 0), (ha, lt["a2"], al, 0, 0), (hg, lt["g2"], g, 2, 0)]
-                vl = None
-                if l > 0:
-                    vl = torch.empty((M, C), dtype=dt, device=dev)
-                    probs.append((hv, lt["v2"], vl, 0, 0))
-                self._gemm_group(M, probs, st)
+                up = torch.bmm(hbuf, pk.lora_up)
+                wl, al, g = up[0], up[1], up[2]
+                vl = up[3] if l > 0 else None
             else:
                 # batched library GEMMs: r/k/v in one, the LoRA downs in one (with
                 # tanh on w and sigmoid on g between), the LoRA ups in one
@@ -535,24 +539,14 @@ class RWKV7Model(nn.Module):
                 wkv_ops.wkv7_prefill(kv, seq_slot, cu_seqlens, *ops.unbind(0), y=y)
                 _lib.call("rwkv7_tmix_post", code, M, H, P(y), P(ops[0]), P(ops[2]), P(ops[3]), P(g),
                           pk.tparams, P(o), st)
-            if grouped:
-                att_out = torch.empty((M, C), dtype=dt, device=dev)
-                self._gemm_group(M, [(o, att.output.weight, att_out, 0, 0)], st)
-            else:
-                att_out = self._lin(o, att.output.weight)
+            att_out = self._lin(o, att.output.weight)
             # residual + attention -> ln2 -> FFN shift/lerp
             _lib.call("rwkv7_shift_mix", code, M, C, P(x_res), P(att_out), None, None, 0, None, None,
                       P(x_mid), P(pk.ln2[0]), P(pk.ln2[1]), P(fx), S, P(row_slot), P(row_last), 1,
                       P(pk.mixk), P(xk_ffn), st)
-            if grouped:
-                hk = torch.empty((M, ffn.key.weight.shape[0]), dtype=dt, device=dev)
-                self._gemm_group(M, [(xk_ffn[0], ffn.key.weight, hk, 0, 1)], st)  # relu^2 epilogue
-                ffn_out = torch.empty((M, C), dtype=dt, device=dev)
-                self._gemm_group(M, [(hk, ffn.value.weight, ffn_out, 0, 0)], st)
-            else:
-                hk = self._lin(xk_ffn[0], ffn.key.weight)
-                _lib.call("rwkv7_activation", code, 2, hk.numel(), P(hk), st)
-                ffn_out = self._lin(hk, ffn.value.weight)
+            hk = self._lin(xk_ffn[0], ffn.key.weight)
+            _lib.call("rwkv7_activation", code, 2, hk.numel(), P(hk), st)
+            ffn_out = self._lin(hk, ffn.value.weight)
         n_out = M if logit_rows is None else (n_logit_rows if n_logit_rows is not None else logit_rows.numel())
         if n_out == 0:
             return None
@@ -561,10 +555,6 @@ class RWKV7Model(nn.Module):
                   P(self._ln_out[0]), P(self._ln_out[1]), P(xo), st)
         if return_hidden:
             return xo
-        if grouped:
-            logits = torch.empty((n_out, self.config.vocab_size), dtype=dt, device=dev)
-            self._gemm_group(n_out, [(xo, self.head.weight, logits, 0, 0)], st)
-            return logits
         return self._lin(xo, self.head.weight)
 
     # -- reference-compatible entry points ------------------------------------
