@@ -174,15 +174,15 @@ int rwkv7_tmix_decode(int dtype, int64_t M, int64_t H, int layer0, const void *r
                       void *out, void *stream);
 
 /*
- * Grouped bf16 GEMM for decode-sized projections: `count` (1..8) independent
- * problems in one launch, problem i computing
- *   C_i[M, N_i] = act_in_i(A_i[M, K_i]) . B_i[N_i, K_i]^T,  then epi_i on C_i,
- * with A_i, B_i, C_i bf16 row-major with row strides lda_i, ldb_i, ldc_i
- * (B in nn.Linear [out][in] layout), float32 accumulation.  act_in: 0 none,
- * 1 tanh, 2 sigmoid; epi: 0 none, 1 relu(x)^2, 2 tanh, 3 sigmoid.  K_i % 32 == 0, lda/ldb
- * multiples of 8 and >= K_i, A/B 16-byte aligned.  The pointer and size
- * arrays are host arrays of `count` entries.  Problems whose K is split across
- * blocks write float32 partial tiles to `workspace` (contents need no
+ * Grouped bf16 GEMM for decode-sized projections (M up to a few hundred rows):
+ * `count` (1..8) independent problems in one launch, problem i computing
+ *   C_i[M, N_i] = epi_i(A_i[M, K_i] . B_i^T)
+ * with A_i, C_i bf16 row-major (row strides lda_i, ldc_i) and B_i the
+ * nn.Linear weight [N_i][K_i] in the packed layout of rwkv7_gemm_pack, float32
+ * accumulation.  epi: 0 none, 1 relu(x)^2, 2 tanh, 3 sigmoid.  K_i % 8 == 0,
+ * lda_i % 8 == 0 and >= K_i, A_i and B_i 16-byte aligned.  The pointer and
+ * size arrays are host arrays of `count` entries.  Problems whose K is split
+ * across blocks write float32 partial tiles to `workspace` (contents need no
  * initialisation) and a second launch on `stream` reduces them;
  * rwkv7_gemm_decode_workspace gives the floats a problem set needs (-1 on
  * invalid sizes).  Calls that share a workspace must not overlap.  Replaces
@@ -191,9 +191,21 @@ int rwkv7_tmix_decode(int dtype, int64_t M, int64_t H, int layer0, const void *r
  */
 int64_t rwkv7_gemm_decode_workspace(int64_t M, int count, const int *N, const int *K);
 int rwkv7_gemm_decode(int64_t M, int count, const void *const *A, const void *const *B,
-                      void *const *C, const int64_t *lda, const int64_t *ldb, const int64_t *ldc,
-                      const int *N, const int *K, const int *act_in, const int *epi,
+                      void *const *C, const int64_t *lda, const int64_t *ldc,
+                      const int *N, const int *K, const int *epi,
                       float *workspace, int64_t workspace_floats, void *stream);
+
+/*
+ * Weight packing for rwkv7_gemm_decode: B [N][K] bf16 (row stride ldb, a
+ * multiple of 8, K % 8 == 0) into rwkv7_gemm_packed_elems(N, K) bf16 elements
+ * at `out`: 64 x 64 tiles of 8 KB, tile (nt, kt) at element
+ * (nt * ceil(K/64) + kt) * 4096, rows past N and columns past K zero, the 16-byte
+ * chunks of a tile row in the order the GEMM's LDS stage uses.  Run once per
+ * weight (no counterpart in the reference: its weights are read in place).
+ * rwkv7_gemm_packed_elems returns -1 on invalid sizes.
+ */
+int64_t rwkv7_gemm_packed_elems(int N, int K);
+int rwkv7_gemm_pack(const void *B, int64_t ldb, int N, int K, void *out, void *stream);
 
 /* ------------------------------------------------------------------------
  * Sampling

@@ -47,7 +47,9 @@ SIGNATURES = {
     "rwkv7_rollout_prepare": (_I32, [_I64, _I64] + [_P] * 18 + [_P]),
     "rwkv7_admit_copy": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64] + [_P] * 6 + [_P]),
     "rwkv7_gemm_decode_workspace": (_I64, [_I64, _I32, _P, _P]),
-    "rwkv7_gemm_decode": (_I32, [_I64, _I32] + [_P] * 10 + [_P, _I64, _P]),
+    "rwkv7_gemm_decode": (_I32, [_I64, _I32] + [_P] * 8 + [_P, _I64, _P]),
+    "rwkv7_gemm_packed_elems": (_I64, [_I32, _I32]),
+    "rwkv7_gemm_pack": (_I32, [_P, _I64, _I32, _I32, _P, _P]),
 }
 
 _lock = threading.Lock()

@@ -497,11 +497,12 @@ extern "C" int rwkv7_admit_copy(const int32_t* counters, const int32_t* admit_sl
 // ---------------------------------------------------------------------------
 
 hipError_t launch_gemm_decode(int M, int count, const void* const* A, const void* const* B, void* const* C,
-                              const int64_t* lda, const int64_t* ldb, const int64_t* ldc, const int* N,
-                              const int* K, const int* act_in, const int* epi, float* ws, hipStream_t st);
+                              const int64_t* lda, const int64_t* ldc, const int* N, const int* K,
+                              const int* epi, float* ws, hipStream_t st);
 int gemm_decode_max_problems();
 int64_t gemm_decode_workspace(int M, int count, const int* N, const int* K);
-
+int64_t gemm_packed_elems(int N, int K);
+hipError_t launch_gemm_pack(const void* B, int64_t ldb, int N, int K, void* out, hipStream_t st);
 namespace {
 int check_gemm_problems(const char* fn, int64_t M, int count, const int* N, const int* K) {
     if (count < 1 || count > gemm_decode_max_problems())
@@ -509,8 +510,8 @@ int check_gemm_problems(const char* fn, int64_t M, int count, const int* N, cons
     if (M < 0 || M > (1 << 20)) return fail(RWKV7_ERR_INVALID, "%s: bad M=%lld", fn, (long long)M);
     if (!N || !K) return fail(RWKV7_ERR_INVALID, "%s: null array", fn);
     for (int i = 0; i < count; ++i)
-        if (N[i] <= 0 || K[i] <= 0 || (K[i] % 32) != 0)
-            return fail(RWKV7_ERR_INVALID, "%s: problem %d: N > 0, K > 0 and K %% 32 == 0 required", fn, i);
+        if (N[i] <= 0 || K[i] <= 0 || (K[i] % 8) != 0)
+            return fail(RWKV7_ERR_INVALID, "%s: problem %d: N > 0, K > 0 and K %% 8 == 0 required", fn, i);
     return RWKV7_OK;
 }
 }  // namespace
@@ -522,31 +523,45 @@ extern "C" int64_t rwkv7_gemm_decode_workspace(int64_t M, int count, const int* 
 }
 
 extern "C" int rwkv7_gemm_decode(int64_t M, int count, const void* const* A, const void* const* B, void* const* C,
-                                 const int64_t* lda, const int64_t* ldb, const int64_t* ldc, const int* N,
-                                 const int* K, const int* act_in, const int* epi, float* workspace,
-                                 int64_t workspace_floats, void* stream) {
+                                 const int64_t* lda, const int64_t* ldc, const int* N, const int* K, const int* epi,
+                                 float* workspace, int64_t workspace_floats, void* stream) {
     if (check_gemm_problems("rwkv7_gemm_decode", M, count, N, K) != RWKV7_OK) return RWKV7_ERR_INVALID;
     if (M == 0) return ok();
-    if (!A || !B || !C || !lda || !ldb || !ldc || !act_in || !epi)
-        return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: null array");
-    int64_t tiles = 0;
+    if (!A || !B || !C || !lda || !ldc || !epi) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: null array");
+    int64_t blocks = 0;
     for (int i = 0; i < count; ++i) {
         if (!A[i] || !B[i] || !C[i]) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: null pointer in problem %d", i);
-        if (lda[i] < K[i] || ldb[i] < K[i] || ldc[i] < N[i] || (lda[i] % 8) != 0 || (ldb[i] % 8) != 0)
-            return fail(RWKV7_ERR_INVALID,
-                        "rwkv7_gemm_decode: problem %d: lda/ldb >= K and %% 8 == 0, ldc >= N required", i);
+        if (lda[i] < K[i] || ldc[i] < N[i] || (lda[i] % 8) != 0)
+            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: lda >= K and %% 8 == 0, ldc >= N required", i);
         if ((((uintptr_t)A[i]) | ((uintptr_t)B[i])) & 15)
-            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: A and B must be 16-byte aligned", i);
-        if (act_in[i] < 0 || act_in[i] > 2 || epi[i] < 0 || epi[i] > 3)
-            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: act_in in 0..2, epi in 0..3", i);
-        tiles += ((M + 63) / 64) * (int64_t)((N[i] + 63) / 64) * 16;
+            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: A and packed B must be 16-byte aligned", i);
+        if (epi[i] < 0 || epi[i] > 3)
+            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: epi in 0..3", i);
+        blocks += ((M + 31) / 32) * (int64_t)((N[i] + 63) / 64 + 7) * 8;
     }
-    if (tiles > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: too many tiles");
+    if (blocks > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: too many tiles");
     const int64_t need_ws = gemm_decode_workspace((int)M, count, N, K);
     if (need_ws > 0 && (workspace == nullptr || workspace_floats < need_ws))
         return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: needs a workspace of %lld floats (have %lld)",
                     (long long)need_ws, (long long)workspace_floats);
-    return launch_status(launch_gemm_decode((int)M, count, A, B, C, lda, ldb, ldc, N, K, act_in, epi, workspace,
+    return launch_status(launch_gemm_decode((int)M, count, A, B, C, lda, ldc, N, K, epi, workspace,
                                             (hipStream_t)stream),
                          "gemm_decode_kernel");
+}
+
+extern "C" int64_t rwkv7_gemm_packed_elems(int N, int K) {
+    if (N <= 0 || K <= 0 || (K % 8) != 0 || N > (1 << 24) || K > (1 << 24)) {
+        fail(RWKV7_ERR_INVALID, "rwkv7_gemm_packed_elems: N > 0, K > 0, K %% 8 == 0 required");
+        return -1;
+    }
+    ok();
+    return gemm_packed_elems(N, K);
+}
+
+extern "C" int rwkv7_gemm_pack(const void* B, int64_t ldb, int N, int K, void* out, void* stream) {
+    if (rwkv7_gemm_packed_elems(N, K) < 0) return RWKV7_ERR_INVALID;
+    if (!B || !out) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_pack: null pointer");
+    if (ldb < K || (ldb % 8) != 0 || ((((uintptr_t)B) | ((uintptr_t)out)) & 15))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_pack: ldb >= K, ldb %% 8 == 0 and 16-byte aligned buffers required");
+    return launch_status(launch_gemm_pack(B, ldb, N, K, out, (hipStream_t)stream), "gemm_pack_kernel");
 }

@@ -1,23 +1,41 @@
 // Grouped bf16 GEMM for the decode step's projections on gfx950 MFMA.
 //
 // At decode the model's dense projections have M = live slots (<= 256) rows:
-// r / k / v / output (C x C), the LoRA pairs (C x 64..480 and back), the FFN
-// (C x 4C, 4C x C).  One launch runs up to 8 independent problems
-//     C_p[M, N_p] = epi_p( act_in_p(A_p[M, K_p]) . B_p[N_p, K_p]^T )
-// with B in nn.Linear layout [out][in] (row-major N x K), bf16 in, fp32
-// accumulate, bf16 out.  act_in: 0 none, 1 tanh, 2 sigmoid (the activations
-// between the LoRA down and up projections, model.py:211, 221); epi: 0 none,
-// 1 relu(x)^2 (FFN key, model.py:337), 2 tanh, 3 sigmoid (the same LoRA
-// activations applied to a down projection's output instead).
+// r / k / v / output (C x C), the LoRA downs (C x 64..480), the FFN
+// (C x 4C, 4C x C) and the head (C x V).  One launch runs up to 8 independent
+// problems
+//     C_p[M, N_p] = epi_p( A_p[M, K_p] . B_p[N_p, K_p]^T )
+// with A row-major, B an nn.Linear weight [out][in] (N x K) stored in the
+// packed layout below, bf16 in, fp32 accumulate, bf16 out.  epi: 0 none,
+// 1 relu(x)^2 (FFN key, model.py:337), 2 tanh, 3 sigmoid (the LoRA activations
+// of model.py:211, 221, applied to a down projection's output).
 //
-// At M = 256 the weights are read once per 64-row block of A and every block
-// is short, so memory latency, not bandwidth or the matrix cores, bounds a
-// naive tiling.  Here:
-//   * a 256-thread block computes a 64 x 64 tile; each wave owns a 32 x 32
-//     quadrant (v_mfma_f32_32x32x16_bf16);
-//   * K is staged through LDS 64 at a time, and the global loads of the next
-//     four stages are in flight in registers while one stage computes (a ring
-//     of named registers: arrays indexed in loops would be placed in scratch);
+// At M <= 256 every weight byte is used by at most 256 rows, so a projection
+// is bound by streaming its weights (close to the MFMA / HBM ridge at M = 256,
+// far below it for fewer rows).  The kernel is built for that:
+//   * weights are packed once (gemm_pack_kernel) into 64 x 64 tiles, each a
+//     contiguous 8 KB block already in the block's LDS order, tiles of one
+//     64-row group consecutive along K: a stage's weight load is one linear
+//     8 KB copy.  Read in place, an [out][in] matrix gives 64 separate 128-byte
+//     segments per stage, and HBM streams such a pattern at ~1.7 TB/s against
+//     ~5 TB/s for long contiguous runs (measured on MI355X);
+//   * a block of 4 or 8 waves computes a BM x BN tile (a template: waves in a
+//     WM x WN grid, each MS x NS tiles of v_mfma_f32_32x32x16_bf16; BN a
+//     multiple of 64).  A CU moves roughly 30-40 GB/s of vector loads whether
+//     they hit L2 or not (measured), so at M = 256 the activation re-reads,
+//     not the weights, dominate a small tile; large tiles cut them, and split
+//     K restores the block count;
+//   * K advances 64 at a time through a ring of R LDS stages filled by direct
+//     global -> LDS loads (global_load_lds_dwordx4: no registers, no LDS store
+//     instructions), R - 1 stages in flight.  Each stage costs one barrier; the
+//     wait before it names its own count of outstanding loads (s_waitcnt
+//     vmcnt(n)), so the loads of later stages stay in flight;
+//   * a stage row is 64 bf16 = 8 chunks of 16 bytes; chunk c of stage row r
+//     sits at position c ^ swz(r), which keeps the MFMA operand reads (32 rows,
+//     one chunk each) free of LDS bank conflicts;
+//   * A chunks past a problem's K read a 16-byte zero page instead (direct
+//     loads cannot be masked; packed weights are zero-padded to whole tiles),
+//     rows past M read a valid row whose results are not stored;
 //   * blocks are ordered so that the row tiles and K ranges of one column tile
 //     run back to back on one XCD (blocks are dealt to the 8 XCDs round-robin),
 //     where they share the weight rows through that XCD's L2;
@@ -28,29 +46,29 @@
 // 8*(l/32) .. +7; accumulator q of lane l is C[8*(q/4) + 4*(l/32) + q%4][l%32].
 #include "common.hpp"
 
+// source of the chunks past a K range
+__device__ __attribute__((aligned(16))) uint32_t g_gemm_zero_chunk[4];
+
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMaxProblems = 8;
-constexpr int TM = 64, TN = 64, BK = 64;
-constexpr int LS = BK + 8;             // LDS row stride (bf16), padded against bank conflicts
-constexpr int RING = 4;                // stages of global loads in flight
-constexpr int TILE_ELEMS = TM * TN;
-constexpr int kThreads = 256;
+constexpr int BK = 64;                 // k per stage: one 128-byte row segment
 
 struct GemmProblem {
     const bf16_t* A;
-    const bf16_t* B;
+    const bf16_t* B;  // packed
     bf16_t* C;
-    int64_t lda, ldb, ldc;
+    int64_t lda, ldc;
     int64_t ws_off;   // float offset of this problem's partials in the workspace
     int N, K;
-    int act_in, epi;
+    int epi;
     int block_begin;  // first block of this problem (a multiple of 8)
     int n_tiles;      // tiles along N
-    int n_groups;     // ceil(n_tiles / 8)
+    int k_tiles;      // 64-wide K tiles of the packed weight
+    int n64;          // 64-row tiles of the packed weight
     int splits;       // K ranges
     int k_per;        // K per range (multiple of BK)
     int red_begin;    // first block of this problem in gemm_reduce_kernel
@@ -60,24 +78,34 @@ struct GemmBatch {
     GemmProblem p[kMaxProblems];
     int count;
     int M;
+    int bm, bn;       // tile of the launch (read by gemm_reduce_kernel)
 };
 
-__device__ __forceinline__ float act_fn(int act, float x) {
-    if (act == 1) return tanhf(x);
-    if (act == 2) return 1.0f / (1.0f + expf(-x));
-    return x;
-}
+// Block tile: WM x WN waves, each wave MS x NS MFMA tiles of 32 x 32; a ring
+// of R LDS stages.
+template <int WM_, int WN_, int MS_, int NS_, int R_>
+struct Tile {
+    static constexpr int WM = WM_, WN = WN_, MS = MS_, NS = NS_, R = R_;
+    static constexpr int NWAVE = WM * WN, THREADS = 64 * NWAVE;
+    static constexpr int BM = 32 * MS * WM, BN = 32 * NS * WN;
+    static constexpr int ROWS = BM + BN;          // stage rows: A rows, then B rows
+    static constexpr int IPW = ROWS / 8 / NWAVE;  // direct loads per wave per stage (8 rows each)
+    static constexpr int STAGE = ROWS * 128;      // bytes
+    static_assert(NWAVE == 4 || NWAVE == 8, "4 or 8 waves per block");
+    static_assert(BN % 64 == 0, "packed weights come in 64-row tiles");
+    static_assert(IPW * 8 * NWAVE == ROWS, "loads split evenly over the waves");
+    static_assert(R >= 2 && (R - 2) * IPW < 64, "vmcnt holds at most 63 outstanding loads");
+    static_assert(R * STAGE <= 160 * 1024, "LDS");
+};
 
-__device__ __forceinline__ uint4 apply_act8(uint4 v, int act) {
-    if (act == 0) return v;
-    uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float lo = act_fn(act, __uint_as_float(w[i] << 16));
-        const float hi = act_fn(act, __uint_as_float(w[i] & 0xffff0000u));
-        w[i] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
-    }
-    return make_uint4(w[0], w[1], w[2], w[3]);
+// LDS position of logical chunk c in stage row r (conflict-free for 32 and 64 banks)
+__device__ __forceinline__ int swz(int r) { return (r ^ (r >> 3)) & 7; }
+
+// s_waitcnt vmcnt(N) lgkmcnt(0)
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | ((N >> 4) << 14));
 }
 
 __device__ __forceinline__ float epi_fn(int epi, float v) {
@@ -90,98 +118,142 @@ __device__ __forceinline__ float epi_fn(int epi, float v) {
     return v;
 }
 
-__device__ __forceinline__ uint4 sel(uint4 v, bool ok) { return ok ? v : make_uint4(0u, 0u, 0u, 0u); }
-
-__global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmBatch batch, float* __restrict__ ws) {
-    __shared__ __attribute__((aligned(16))) bf16_t As[2][TM * LS];
-    __shared__ __attribute__((aligned(16))) bf16_t Bs[2][TN * LS];
-
-    // select the block's problem with constant indices only (a dynamic index
-    // into the kernel-argument struct would copy it to scratch memory)
-    const int bid = blockIdx.x;
+__device__ __forceinline__ GemmProblem select_problem(const GemmBatch& batch, int bid, bool reduce) {
+    // constant indices only: a dynamic index into the kernel-argument struct
+    // would copy it to scratch memory
     GemmProblem P = batch.p[0];
 #pragma unroll
     for (int i = 1; i < kMaxProblems; ++i)
-        if (i < batch.count && bid >= batch.p[i].block_begin) P = batch.p[i];
+        if (i < batch.count && bid >= (reduce ? batch.p[i].red_begin : batch.p[i].block_begin)) P = batch.p[i];
+    return P;
+}
+
+template <class T>
+__global__ __launch_bounds__(T::THREADS) void gemm_decode_kernel(GemmBatch batch, float* __restrict__ ws) {
+    __shared__ __attribute__((aligned(16))) uint8_t ring[T::R * T::STAGE];
+
+    const GemmProblem P = select_problem(batch, blockIdx.x, false);
     const int M = batch.M;
-    const int mt = (M + TM - 1) / TM;
-    const int local = bid - P.block_begin;
-    const int xcd = local & 7, j = local >> 3;  // block_begin is a multiple of 8: same XCD as bid
+    const int mt = (M + T::BM - 1) / T::BM;
+    const int local = blockIdx.x - P.block_begin;
+    const int xcd = local & 7, j = local >> 3;  // block_begin is a multiple of 8: same XCD as blockIdx.x
     const int per = mt * P.splits;
     const int ntile = (j / per) * 8 + xcd;
-    if (ntile >= P.n_tiles) return;  // padding block of the last column group
+    if (ntile >= P.n_tiles) return;             // padding block of the last column group
     const int rem = j % per;
     const int mtile = rem % mt, split = rem / mt;
-    const int m0 = mtile * TM, n0 = ntile * TN;
+    const int m0 = mtile * T::BM, n0 = ntile * T::BN;
     const int kb = split * P.k_per;
-    const int ke = min(P.K, kb + P.k_per);
-    const int nst = (ke - kb + BK - 1) / BK;
+    const int kspan = min(P.K, kb + P.k_per) - kb;
+    const int nst = (kspan + BK - 1) / BK;
 
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
-
-    // global -> LDS: thread t moves 16-byte chunks t and t + 256 of the A tile and
-    // of the B tile per stage (64 rows x 8 chunks).  Rows past M / N read a valid
-    // row (their results are not stored); chunks past the K range are zeroed.
-    const int r0 = t >> 3, kq = (t & 7) * 8;     // chunk t: row r0, k offset kq; chunk t+256: row r0 + 32
-    const bf16_t* a0 = P.A + (int64_t)min(m0 + r0, M - 1) * P.lda + kb + kq;
-    const bf16_t* a1 = P.A + (int64_t)min(m0 + r0 + 32, M - 1) * P.lda + kb + kq;
-    const bf16_t* b0 = P.B + (int64_t)min(n0 + r0, P.N - 1) * P.ldb + kb + kq;
-    const bf16_t* b1 = P.B + (int64_t)min(n0 + r0 + 32, P.N - 1) * P.ldb + kb + kq;
-    const int l0 = r0 * LS + kq, l1 = (r0 + 32) * LS + kq;
-    const int kspan = ke - kb;
-
-    uint4 ga0_0, ga1_0, gb0_0, gb1_0, ga0_1, ga1_1, gb0_1, gb1_1;
-    uint4 ga0_2, ga1_2, gb0_2, gb1_2, ga0_3, ga1_3, gb0_3, gb1_3;
-#define GD_LOAD(p, st)                                                                   \
-    {                                                                                    \
-        const int ko = (st) * BK;                                                        \
-        const bool ok = ko + kq < kspan;                                                 \
-        const int kc = ok ? ko : -kq;  /* past the range: re-read the range's first chunk */ \
-        ga0_##p = sel(*reinterpret_cast<const uint4*>(a0 + kc), ok);                     \
-        ga1_##p = sel(*reinterpret_cast<const uint4*>(a1 + kc), ok);                     \
-        gb0_##p = sel(*reinterpret_cast<const uint4*>(b0 + kc), ok);                     \
-        gb1_##p = sel(*reinterpret_cast<const uint4*>(b1 + kc), ok);                     \
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    // Direct loads: load i of wave w fills stage rows 8 (w IPW + i) .. +7, A rows
+    // first.  For an A row, lane L brings logical chunk (L%8) ^ swz(row) of row
+    // 8 (w IPW + i) + L/8 to LDS position L%8 of that row; a B load is a linear
+    // 1 KB piece of the packed tile, which holds the same arrangement.
+    const bf16_t* src[T::IPW];
+    int kc[T::IPW];  // k offset of the lane's A chunk within a stage (-1: B load)
+    const int kt0 = kb / BK;
+#pragma unroll
+    for (int i = 0; i < T::IPW; ++i) {
+        const int row0 = 8 * (wave * T::IPW + i);
+        if (row0 < T::BM) {
+            const int row = row0 + (lane >> 3);
+            const int c = (lane & 7) ^ swz(row);
+            kc[i] = 8 * c;
+            src[i] = P.A + (int64_t)min(m0 + row, M - 1) * P.lda + kb + 8 * c;
+        } else {
+            // B rows rr0 .. rr0 + 7 lie in one 64-row packed tile; tiles past
+            // the weight (N not a multiple of BN) re-read its last tile
+            const int rr0 = row0 - T::BM;
+            const int t64 = min(ntile * (T::BN / 64) + rr0 / 64, P.n64 - 1);
+            kc[i] = -1;
+            src[i] = P.B + ((int64_t)t64 * P.k_tiles + kt0) * (64 * BK) + (rr0 % 64) * BK + lane * 8;
+        }
     }
-    GD_LOAD(0, 0)
-    GD_LOAD(1, min(1, nst - 1))
-    GD_LOAD(2, min(2, nst - 1))
-    GD_LOAD(3, min(3, nst - 1))
+    const bf16_t* zero = reinterpret_cast<const bf16_t*>(g_gemm_zero_chunk);
+    auto issue = [&](int s) {
+        uint8_t* dst = ring + (s % T::R) * T::STAGE + wave * T::IPW * 8 * 128;
+#pragma unroll
+        for (int i = 0; i < T::IPW; ++i) {
+            const bf16_t* g;
+            if (8 * (wave * T::IPW + i) >= T::BM)  // wave-uniform
+                g = src[i] + s * (64 * BK);
+            else
+                g = (s * BK + kc[i] < kspan) ? src[i] + s * BK : zero;
+            __builtin_amdgcn_global_load_lds(g, dst + i * 8 * 128, 16, 0, 0);
+        }
+    };
 
-    f32x16 acc = {0.f};
-    const int r = lane & 31, kg = (lane >> 5) * 8;
-    const int act = P.act_in;
-#define GD_STEP(p)                                                                       \
-    if (s0 + (p) < nst) {                                                                \
-        const int s = s0 + (p);                                                          \
-        const int buf = s & 1;                                                           \
-        *reinterpret_cast<uint4*>(&As[buf][l0]) = apply_act8(ga0_##p, act);              \
-        *reinterpret_cast<uint4*>(&As[buf][l1]) = apply_act8(ga1_##p, act);              \
-        *reinterpret_cast<uint4*>(&Bs[buf][l0]) = gb0_##p;                               \
-        *reinterpret_cast<uint4*>(&Bs[buf][l1]) = gb1_##p;                               \
-        __syncthreads();                                                                 \
-        GD_LOAD(p, min(s + RING, nst - 1))                                               \
-        _Pragma("unroll") for (int kk = 0; kk < BK; kk += 16) {                          \
-            const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(&As[buf][(wm + r) * LS + kk + kg]); \
-            const bf16x8_t bf = *reinterpret_cast<const bf16x8_t*>(&Bs[buf][(wn + r) * LS + kk + kg]); \
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc, 0, 0, 0);         \
-        }                                                                                \
+    f32x16 acc[T::MS][T::NS];
+#pragma unroll
+    for (int a = 0; a < T::MS; ++a)
+#pragma unroll
+        for (int b = 0; b < T::NS; ++b) acc[a][b] = f32x16{0.f};
+    const int lr = lane & 31, hi = lane >> 5;
+    const int wm = (wave / T::WN) * (32 * T::MS), wn = (wave % T::WN) * (32 * T::NS);
+    auto mma = [&](int s) {
+        const uint8_t* st = ring + (s % T::R) * T::STAGE;
+        // every operand of the stage is read before the first product, so the
+        // LDS latency is paid once per stage rather than once per k step
+        bf16x8_t af[4][T::MS], bfr[4][T::NS];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int c = 2 * kk + hi;
+#pragma unroll
+            for (int a = 0; a < T::MS; ++a) {
+                const int row = wm + 32 * a + lr;
+                af[kk][a] = *reinterpret_cast<const bf16x8_t*>(st + row * 128 + ((c ^ swz(row)) << 4));
+            }
+#pragma unroll
+            for (int b = 0; b < T::NS; ++b) {
+                const int row = wn + 32 * b + lr;  // row of the B part
+                bfr[kk][b] = *reinterpret_cast<const bf16x8_t*>(st + (T::BM + row) * 128 + ((c ^ swz(row)) << 4));
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the products
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int a = 0; a < T::MS; ++a)
+#pragma unroll
+                for (int b = 0; b < T::NS; ++b)
+                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[kk][a], bfr[kk][b], acc[a][b], 0, 0, 0);
+    };
+
+    // Stage s lives in slot s % R.  Iteration s: wait until this wave's loads of
+    // stage s have landed (the R - 2 later stages may still be in flight) and
+    // its LDS reads of stage s - 1 are done; the barrier then makes every
+    // wave's share of stage s visible, and tells every wave that slot
+    // (s - 1) % R is no longer read, so stage s + R - 1 is issued into it.
+#pragma unroll
+    for (int s = 0; s < T::R - 1; ++s)
+        if (s < nst) issue(s);
+    for (int s = 0; s < nst; ++s) {
+        if (s + T::R - 2 < nst)
+            wait_vm_lgkm<(T::R - 2) * T::IPW>();
+        else
+            wait_vm_lgkm<0>();
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");  // no LDS read moves above the barrier
+        if (s + T::R - 1 < nst) issue(s + T::R - 1);
+        mma(s);
     }
-    // One barrier per stage: stage s writes LDS buffer s&1, which every wave
-    // finished reading (stage s-2) before it reached stage s-1's barrier.
-    for (int s0 = 0; s0 < nst; s0 += RING) {
-        GD_STEP(0) GD_STEP(1) GD_STEP(2) GD_STEP(3)
-    }
-#undef GD_STEP
-#undef GD_LOAD
 
     if (P.splits == 1) {
-        const int col = n0 + wn + (lane & 31);
 #pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int row = m0 + wm + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
-            if (row < M && col < P.N) P.C[(int64_t)row * P.ldc + col] = f32_to_bf16(epi_fn(P.epi, acc[q]));
-        }
+        for (int a = 0; a < T::MS; ++a)
+#pragma unroll
+            for (int b = 0; b < T::NS; ++b) {
+                const int col = n0 + wn + 32 * b + lr;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int row = m0 + wm + 32 * a + 8 * (q >> 2) + 4 * hi + (q & 3);
+                    if (row < M && col < P.N)
+                        P.C[(int64_t)row * P.ldc + col] = f32_to_bf16(epi_fn(P.epi, acc[a][b][q]));
+                }
+            }
         return;
     }
     // split-K: publish this range's partial tile; gemm_reduce_kernel, launched
@@ -189,93 +261,110 @@ __global__ __launch_bounds__(kThreads) void gemm_decode_kernel(GemmBatch batch, 
     // another block's writes visible: the L2 of each XCD is private)
     const int tile = mtile * P.n_tiles + ntile;
     const int ntiles = mt * P.n_tiles;
-    float* part = ws + P.ws_off + ((int64_t)split * ntiles + tile) * TILE_ELEMS;
+    float* part = ws + P.ws_off + ((int64_t)split * ntiles + tile) * (T::BM * T::BN);
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-        const int rr = wm + 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
-        part[rr * TN + wn + (lane & 31)] = acc[q];
-    }
+    for (int a = 0; a < T::MS; ++a)
+#pragma unroll
+        for (int b = 0; b < T::NS; ++b)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int rr = wm + 32 * a + 8 * (q >> 2) + 4 * hi + (q & 3);
+                part[rr * T::BN + wn + 32 * b + lr] = acc[a][b][q];
+            }
 }
 
 // Sum the split-K partial tiles in split order (deterministic), apply the
-// epilogue and write bf16.  One block per tile of the problems with splits > 1;
-// red_begin is the problem's first block here.
+// epilogue and write bf16.  Thread e of problem p covers 4 consecutive
+// elements of one partial tile; red_begin is the problem's first block here.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmBatch batch, const float* __restrict__ ws) {
-    const int bid = blockIdx.x;
-    GemmProblem P = batch.p[0];
-#pragma unroll
-    for (int i = 1; i < kMaxProblems; ++i)
-        if (i < batch.count && bid >= batch.p[i].red_begin) P = batch.p[i];
-    const int tile = bid - P.red_begin;
-    const int M = batch.M;
-    const int mt = (M + TM - 1) / TM;
+    const GemmProblem P = select_problem(batch, blockIdx.x, true);
+    const int M = batch.M, BM = batch.bm, BN = batch.bn;
+    const int mt = (M + BM - 1) / BM;
     const int ntiles = mt * P.n_tiles;
-    if (P.splits <= 1 || tile >= ntiles) return;
-    const int m0 = (tile / P.n_tiles) * TM, n0 = (tile % P.n_tiles) * TN;
-    const float* base = ws + P.ws_off + (int64_t)tile * TILE_ELEMS;
-    const int64_t stride = (int64_t)ntiles * TILE_ELEMS;
-    for (int e = threadIdx.x; e < TILE_ELEMS; e += 256) {
-        float v = 0.f;
-        for (int s = 0; s < P.splits; ++s) v += base[s * stride + e];
-        const int row = m0 + e / TN, col = n0 + e % TN;
-        if (row < M && col < P.N) P.C[(int64_t)row * P.ldc + col] = f32_to_bf16(epi_fn(P.epi, v));
-    }
+    const int elems = BM * BN;
+    const int64_t e = ((int64_t)(blockIdx.x - P.red_begin) * 256 + threadIdx.x) * 4;
+    if (P.splits <= 1 || e >= (int64_t)ntiles * elems) return;
+    const int tile = (int)(e / elems), te = (int)(e % elems);
+    const int row = (tile / P.n_tiles) * BM + te / BN, col = (tile % P.n_tiles) * BN + te % BN;
+    if (row >= M) return;
+    const float* base = ws + P.ws_off + e;
+    const int64_t stride = (int64_t)ntiles * elems;
+    f32x4 v = *reinterpret_cast<const f32x4*>(base);
+    for (int s = 1; s < P.splits; ++s) v += *reinterpret_cast<const f32x4*>(base + s * stride);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        if (col + c < P.N) P.C[(int64_t)row * P.ldc + col + c] = f32_to_bf16(epi_fn(P.epi, v[c]));
 }
 
-// Split counts: when the launch's tiles alone would not reach ~384 blocks
-// (1.5 per CU), every problem splits K into equal ranges of at least 1024 (a
-// multiple of BK), at most 8; also the workspace floats and the tiles the
-// reduction pass covers.
-void plan(int M, int count, const int* N, const int* K, int* splits, int* k_per, int64_t* ws_floats,
-          int64_t* red_tiles) {
-    const int mt = (M + TM - 1) / TM;
+// Pack an nn.Linear weight B [N][K] (row stride ldb) into 64 x 64 tiles: tile
+// (nt, kt) is the 8 KB block at ((nt * KT) + kt) * 4096 elements, row r of it
+// holds B[64 nt + r][64 kt .. +63] as 8 chunks of 16 bytes with logical chunk
+// c at position c ^ swz(r); rows past N and columns past K are zero.
+__global__ __launch_bounds__(256) void gemm_pack_kernel(const bf16_t* __restrict__ B, int64_t ldb, int N, int K,
+                                                        int KT, int64_t chunks, bf16_t* __restrict__ out) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (q >= chunks) return;
+    const int p = (int)(q & 7), r = (int)((q >> 3) & 63);
+    const int64_t tile = q >> 9;
+    const int kt = (int)(tile % KT), nt = (int)(tile / KT);
+    const int n = nt * 64 + r, k = kt * 64 + 8 * (p ^ swz(r));
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (n < N && k < K) v = *reinterpret_cast<const uint4*>(B + (int64_t)n * ldb + k);
+    reinterpret_cast<uint4*>(out)[q] = v;
+}
+
+// Launch plan of a problem set on a bm x bn tile: split counts (when the tiles
+// alone would not reach `target` blocks, K splits into equal ranges of at least
+// min_k, a multiple of BK, at most 8), block offsets, workspace floats and the
+// tiles the reduction pass covers.  force_splits > 0 overrides the split rule.
+struct Plan {
+    int splits[kMaxProblems], k_per[kMaxProblems];
+    int blocks, red_tiles;  // blocks of the GEMM and of the reduction pass
+    int64_t ws_floats;
+};
+
+Plan make_plan(int bm, int bn, int M, int count, const int* N, const int* K, int target, int min_k,
+               int force_splits) {
+    Plan pl{};
+    const int mt = (M + bm - 1) / bm;
     int64_t total = 0;
-    for (int i = 0; i < count; ++i) total += (int64_t)mt * ((N[i] + TN - 1) / TN);
-    const int want = (int)((384 + total - 1) / total);
-    *ws_floats = 0;
-    *red_tiles = 0;
+    for (int i = 0; i < count; ++i) total += (int64_t)mt * ((N[i] + bn - 1) / bn);
+    const int want = (int)((target + total - 1) / total);
     for (int i = 0; i < count; ++i) {
-        const int64_t nt = (int64_t)mt * ((N[i] + TN - 1) / TN);
-        int si = want;
-        const int max_by_k = K[i] / 1024;
-        if (si > max_by_k) si = max_by_k < 1 ? 1 : max_by_k;
-        if (si > 8) si = 8;
+        const int n_tiles = (N[i] + bn - 1) / bn;
+        const int64_t nt = (int64_t)mt * n_tiles;
+        int si = force_splits > 0 ? force_splits : want;
+        if (force_splits <= 0) {
+            const int max_by_k = K[i] / min_k;
+            if (si > max_by_k) si = max_by_k < 1 ? 1 : max_by_k;
+            if (si > 8) si = 8;
+        }
+        if (si < 1) si = 1;
         int kp = (K[i] + si - 1) / si;
         kp = (kp + BK - 1) / BK * BK;
         si = (K[i] + kp - 1) / kp;
-        splits[i] = si;
-        k_per[i] = kp;
+        pl.splits[i] = si;
+        pl.k_per[i] = kp;
+        pl.blocks += 8 * ((n_tiles + 7) / 8) * mt * si;
         if (si > 1) {
-            *ws_floats += (int64_t)si * nt * TILE_ELEMS;
-            *red_tiles += nt;
+            pl.ws_floats += (int64_t)si * nt * bm * bn;
+            pl.red_tiles += (int)((nt * bm * bn / 4 + 255) / 256);
         }
     }
+    return pl;
 }
 
-}  // namespace
-
-int gemm_decode_max_problems() { return kMaxProblems; }
-
-int64_t gemm_decode_workspace(int M, int count, const int* N, const int* K) {
-    int splits[kMaxProblems], k_per[kMaxProblems];
-    int64_t wsf = 0, red = 0;
-    plan(M, count, N, K, splits, k_per, &wsf, &red);
-    return wsf;
-}
-
-// problems: count entries of {A, B, C, lda, ldb, ldc, N, K, act_in, epi}
-hipError_t launch_gemm_decode(int M, int count, const void* const* A, const void* const* B, void* const* C,
-                              const int64_t* lda, const int64_t* ldb, const int64_t* ldc, const int* N,
-                              const int* K, const int* act_in, const int* epi, float* ws, hipStream_t st)
-{
+template <class T>
+hipError_t launch_tile(int M, int count, const void* const* A, const void* const* B, void* const* C,
+                       const int64_t* lda, const int64_t* ldc, const int* N, const int* K,
+                       const int* epi, float* ws, hipStream_t st, const Plan& pl) {
     GemmBatch b{};
     b.count = count;
     b.M = M;
-    int splits[kMaxProblems], k_per[kMaxProblems];
-    int64_t wsf = 0, red = 0;
-    plan(M, count, N, K, splits, k_per, &wsf, &red);
-    const int mt = (M + TM - 1) / TM;
-    int blocks = 0, red_tiles = 0;
+    b.bm = T::BM;
+    b.bn = T::BN;
+    const int mt = (M + T::BM - 1) / T::BM;
+    int blocks = 0, red = 0;
     int64_t ws_off = 0;
     for (int i = 0; i < count; ++i) {
         GemmProblem& p = b.p[i];
@@ -283,29 +372,68 @@ hipError_t launch_gemm_decode(int M, int count, const void* const* A, const void
         p.B = (const bf16_t*)B[i];
         p.C = (bf16_t*)C[i];
         p.lda = lda[i];
-        p.ldb = ldb[i];
         p.ldc = ldc[i];
         p.N = N[i];
         p.K = K[i];
-        p.act_in = act_in[i];
         p.epi = epi[i];
-        p.n_tiles = (N[i] + TN - 1) / TN;
-        p.n_groups = (p.n_tiles + 7) / 8;
-        p.splits = splits[i];
-        p.k_per = k_per[i];
+        p.n_tiles = (N[i] + T::BN - 1) / T::BN;
+        p.k_tiles = (K[i] + BK - 1) / BK;
+        p.n64 = (N[i] + 63) / 64;
+        p.splits = pl.splits[i];
+        p.k_per = pl.k_per[i];
         p.block_begin = blocks;
         p.ws_off = ws_off;
-        p.red_begin = red_tiles;
-        blocks += 8 * p.n_groups * mt * p.splits;
+        p.red_begin = red;
+        blocks += 8 * ((p.n_tiles + 7) / 8) * mt * p.splits;
         const int nt = mt * p.n_tiles;
         if (p.splits > 1) {
-            ws_off += (int64_t)p.splits * nt * TILE_ELEMS;
-            red_tiles += nt;
+            ws_off += (int64_t)p.splits * nt * T::BM * T::BN;
+            red += (nt * T::BM * T::BN / 4 + 255) / 256;
         }
     }
-    hipLaunchKernelGGL(gemm_decode_kernel, dim3(blocks), dim3(kThreads), 0, st, b, ws);
+    hipLaunchKernelGGL((gemm_decode_kernel<T>), dim3(blocks), dim3(T::THREADS), 0, st, b, ws);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || red_tiles == 0) return e;
-    hipLaunchKernelGGL(gemm_reduce_kernel, dim3(red_tiles), dim3(256), 0, st, b, (const float*)ws);
+    if (e != hipSuccess || red == 0) return e;
+    hipLaunchKernelGGL(gemm_reduce_kernel, dim3(red), dim3(256), 0, st, b, (const float*)ws);
+    return hipGetLastError();
+}
+
+// The library's tile: 64 x 64, 4 waves, 4 stages.  Sweeps over 64..256 x
+// 64..256 tiles, 4 or 8 waves, 2..8 stages and 1..8 K splits at the 1.5B
+// decode shapes (M = 32..256) put it first or within a few percent of the
+// best everywhere: a CU's load path, not the tile, bounds these launches.
+// Launches aim at 384 blocks (1.5 per CU) by splitting K into ranges of at
+// least 512.
+using TileDecode = Tile<2, 2, 1, 1, 4>;
+constexpr int kTarget = 384, kMinK = 512;
+
+Plan plan_for(int M, int count, const int* N, const int* K) {
+    return make_plan(TileDecode::BM, TileDecode::BN, M, count, N, K, kTarget, kMinK, 0);
+}
+
+}  // namespace
+
+int gemm_decode_max_problems() { return kMaxProblems; }
+
+int64_t gemm_decode_workspace(int M, int count, const int* N, const int* K) {
+    return plan_for(M, count, N, K).ws_floats;
+}
+
+// problems: count entries of {A, packed B, C, lda, ldc, N, K, epi}
+hipError_t launch_gemm_decode(int M, int count, const void* const* A, const void* const* B, void* const* C,
+                              const int64_t* lda, const int64_t* ldc, const int* N, const int* K,
+                              const int* epi, float* ws, hipStream_t st)
+{
+    const Plan pl = plan_for(M, count, N, K);
+    return launch_tile<TileDecode>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl);
+}
+
+int64_t gemm_packed_elems(int N, int K) { return (int64_t)((N + 63) / 64) * 64 * ((K + BK - 1) / BK) * BK; }
+
+hipError_t launch_gemm_pack(const void* B, int64_t ldb, int N, int K, void* out, hipStream_t st) {
+    const int KT = (K + BK - 1) / BK;
+    const int64_t chunks = gemm_packed_elems(N, K) / 8;
+    hipLaunchKernelGGL(gemm_pack_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st,
+                       (const bf16_t*)B, ldb, N, K, KT, chunks, (bf16_t*)out);
     return hipGetLastError();
 }

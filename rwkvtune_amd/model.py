@@ -264,6 +264,24 @@ class StatePool:
 # The model
 # ---------------------------------------------------------------------------
 
+class PackedWeight:
+    """An nn.Linear weight [N][K] (bf16) in the tiled layout of the decode GEMM
+    (``rwkv7_gemm_pack``): 64 x 64 tiles, each one contiguous 8 KB block, so a
+    K step of the GEMM reads one linear piece of HBM instead of 64 row segments."""
+
+    def __init__(self, weight: torch.Tensor):
+        if weight.dtype != torch.bfloat16 or weight.ndim != 2 or weight.stride(1) != 1:
+            raise ValueError("PackedWeight needs a bf16 [N][K] weight with unit column stride")
+        self.N, self.K = int(weight.shape[0]), int(weight.shape[1])
+        n = _lib.load().rwkv7_gemm_packed_elems(self.N, self.K)
+        if n < 0:
+            raise ValueError("rwkv7_gemm_packed_elems: " + _lib.load().rwkv7_last_error().decode())
+        w = weight if weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0 else weight.contiguous()
+        self.t = torch.empty(n, dtype=torch.bfloat16, device=weight.device)
+        _lib.call("rwkv7_gemm_pack", _lib.ptr(w), w.stride(0), self.N, self.K, _lib.ptr(self.t),
+                  _lib.stream_of(self.t))
+
+
 class _LayerPack:
     """float32 copies of one layer's per-channel parameters, laid out for the kernels."""
 
@@ -306,11 +324,19 @@ class _LayerPack:
             for i, (dn, up) in enumerate(zip(downs, ups)):
                 self.lora_down[i, :, :dn.shape[1]] = dn.detach()
                 self.lora_up[i, :up.shape[0], :] = up.detach()
-        # LoRA matrices in [out][in] layout for the grouped decode GEMM (bf16 models)
-        self.lora_t = {}
+        # decode-GEMM weights of bf16 models, packed: r / k / v, the LoRA downs
+        # and ups as [out][in] matrices, the FFN key and value
+        self.gp = {}
         if att.w1.dtype == torch.bfloat16:
-            names = ("w1", "a1", "g1", "w2", "a2", "g2") + (() if self.layer0 else ("v1", "v2"))
-            self.lora_t = {n: getattr(att, n).detach().t().contiguous() for n in names}
+            with torch.no_grad():
+                self.gp = {"r": PackedWeight(att.receptance.weight.detach()),
+                           "k": PackedWeight(att.key.weight.detach()),
+                           "v": PackedWeight(att.value.weight.detach()),
+                           "fk": PackedWeight(ffn.key.weight.detach()),
+                           "fv": PackedWeight(ffn.value.weight.detach())}
+                names = ("w1", "a1", "g1", "w2", "a2", "g2") + (() if self.layer0 else ("v1", "v2"))
+                for n in names:
+                    self.gp[n] = PackedWeight(getattr(att, n).detach().t().contiguous())
 
 
 class RWKV7Model(nn.Module):
@@ -324,11 +350,11 @@ class RWKV7Model(nn.Module):
         self.ln_out = nn.LayerNorm(config.n_embd)
         self.head = nn.Linear(config.n_embd, config.vocab_size, bias=False)
         self._packs = None
-        # decode rows of a bf16 model run the seven projections of the token-shift
-        # mixes (r, k, v and the LoRA downs, with tanh / sigmoid fused) as one launch
-        # of the library's grouped MFMA GEMM; measured in HIP graphs at 256 rows it
-        # beats the batched library calls plus their activation launches, while the
-        # remaining projections stay library GEMMs (faster there)
+        # decode rows of a bf16 model run their projections on the library's
+        # grouped MFMA GEMM over packed weights: r, k, v and the LoRA downs (tanh /
+        # sigmoid fused) in one launch, the LoRA ups in one, the FFN key (relu^2
+        # fused) and value; the output projection and the head stay library GEMMs
+        # (faster there at these shapes, measured)
         self.use_grouped_gemm = True
         self._lora_h = {}
 
@@ -413,20 +439,25 @@ class RWKV7Model(nn.Module):
 
     @staticmethod
     def _gemm_group(M: int, probs, stream):
-        """One grouped decode-GEMM launch: probs = [(A, B, C, act_in, epi)], C = act(A) . B^T."""
+        """One grouped decode-GEMM launch: probs = [(A, B, C, epi)] with B a
+        ``PackedWeight``; C = epi(A . B^T), A [M][B.K] and C [M][B.N] bf16 views
+        with unit column stride."""
         n = len(probs)
         P = ctypes.c_void_p
         dev = probs[0][0].device
-        arrA = (P * n)(*[a.data_ptr() for a, _, _, _, _ in probs])
-        arrB = (P * n)(*[b.data_ptr() for _, b, _, _, _ in probs])
-        arrC = (P * n)(*[c.data_ptr() for _, _, c, _, _ in probs])
-        lda = (ctypes.c_int64 * n)(*[a.stride(0) for a, _, _, _, _ in probs])
-        ldb = (ctypes.c_int64 * n)(*[b.stride(0) for _, b, _, _, _ in probs])
-        ldc = (ctypes.c_int64 * n)(*[c.stride(0) for _, _, c, _, _ in probs])
-        N = (ctypes.c_int * n)(*[b.shape[0] for _, b, _, _, _ in probs])
-        K = (ctypes.c_int * n)(*[b.shape[1] for _, b, _, _, _ in probs])
-        act = (ctypes.c_int * n)(*[x for _, _, _, x, _ in probs])
-        epi = (ctypes.c_int * n)(*[x for _, _, _, _, x in probs])
+        for a, b, c, _ in probs:
+            if (a.dtype != torch.bfloat16 or c.dtype != torch.bfloat16 or a.shape != (M, b.K)
+                    or c.shape != (M, b.N) or a.stride(1) != 1 or c.stride(1) != 1):
+                raise ValueError(f"grouped GEMM operands: A {tuple(a.shape)} {a.dtype}, C {tuple(c.shape)} "
+                                 f"{c.dtype} for a {b.N} x {b.K} weight and M = {M}")
+        arrA = (P * n)(*[a.data_ptr() for a, _, _, _ in probs])
+        arrB = (P * n)(*[b.t.data_ptr() for _, b, _, _ in probs])
+        arrC = (P * n)(*[c.data_ptr() for _, _, c, _ in probs])
+        lda = (ctypes.c_int64 * n)(*[a.stride(0) for a, _, _, _ in probs])
+        ldc = (ctypes.c_int64 * n)(*[c.stride(0) for _, _, c, _ in probs])
+        N = (ctypes.c_int * n)(*[b.N for _, b, _, _ in probs])
+        K = (ctypes.c_int * n)(*[b.K for _, b, _, _ in probs])
+        epi = (ctypes.c_int * n)(*[x for _, _, _, x in probs])
         need = _lib.load().rwkv7_gemm_decode_workspace(M, n, N, K)
         if need < 0:
             raise ValueError("rwkv7_gemm_decode_workspace: " + _lib.load().rwkv7_last_error().decode())
@@ -434,7 +465,7 @@ class RWKV7Model(nn.Module):
         if ws is None:
             ws = RWKV7Model._gemm_ws[dev] = RWKV7Model.GemmWorkspace(dev)
         ws.ensure(need)
-        _lib.call("rwkv7_gemm_decode", M, n, arrA, arrB, arrC, lda, ldb, ldc, N, K, act, epi,
+        _lib.call("rwkv7_gemm_decode", M, n, arrA, arrB, arrC, lda, ldc, N, K, epi,
                   P(ws.ws.data_ptr()), ws.ws.numel(), stream)
 
     @torch.no_grad()
@@ -496,11 +527,10 @@ class RWKV7Model(nn.Module):
                           P(pk.mix7), P(mixes), st)
             xr, xk, xv, xw, xa, xg, _ = mixes.unbind(0)
             if grouped:
-                # one grouped launch: r, k, v and the LoRA downs of the six mixes, tanh
-                # (w) and sigmoid (g) as epilogues; the downs land in a zero-padded
-                # [n][M][D] buffer (padding columns are never written) for the batched
-                # LoRA-up product
-                lt = pk.lora_t
+                # two grouped launches: r, k, v and the LoRA downs of the six
+                # mixes (tanh on w, sigmoid on g as epilogues, into a [n][M][D]
+                # buffer), then the four LoRA ups
+                gp = pk.gp
                 nl, D = pk.lora_down.shape[0], pk.lora_down.shape[2]
                 key = (dev, M, nl, D)
                 hbuf = self._lora_h.get(key)
@@ -510,11 +540,12 @@ class RWKV7Model(nn.Module):
                 r, k, v = rkv.unbind(0)
                 dn = [("w1", 0, 2), ("a1", 1, 0), ("g1", 2, 3)] + ([] if l == 0 else [("v1", 3, 0)])
                 src = {"w1": xw, "a1": xa, "g1": xg, "v1": xv}
-                probs = [(xr, att.receptance.weight, r, 0, 0), (xk, att.key.weight, k, 0, 0),
-                         (xv, att.value.weight, v, 0, 0)]
-                probs += [(src[n], lt[n], hbuf[i, :, :lt[n].shape[0]], 0, e) for n, i, e in dn]
+                probs = [(xr, gp["r"], r, 0), (xk, gp["k"], k, 0), (xv, gp["v"], v, 0)]
+                probs += [(src[n], gp[n], hbuf[i, :, :gp[n].N], e) for n, i, e in dn]
                 self._gemm_group(M, probs, st)
-                up = torch.bmm(hbuf, pk.lora_up)
+                up = torch.empty((nl, M, C), dtype=dt, device=dev)
+                ups = [("w2", 0), ("a2", 1), ("g2", 2)] + ([] if l == 0 else [("v2", 3)])
+                self._gemm_group(M, [(hbuf[i, :, :gp[n].K], gp[n], up[i], 0) for n, i in ups], st)
                 wl, al, g = up[0], up[1], up[2]
                 vl = up[3] if l > 0 else None
             else:
@@ -544,9 +575,16 @@ class RWKV7Model(nn.Module):
             _lib.call("rwkv7_shift_mix", code, M, C, P(x_res), P(att_out), None, None, 0, None, None,
                       P(x_mid), P(pk.ln2[0]), P(pk.ln2[1]), P(fx), S, P(row_slot), P(row_last), 1,
                       P(pk.mixk), P(xk_ffn), st)
-            hk = self._lin(xk_ffn[0], ffn.key.weight)
-            _lib.call("rwkv7_activation", code, 2, hk.numel(), P(hk), st)
-            ffn_out = self._lin(hk, ffn.value.weight)
+            if grouped:
+                # FFN key with relu^2 as its epilogue, then the value projection
+                hk = torch.empty((M, pk.gp["fk"].N), dtype=dt, device=dev)
+                self._gemm_group(M, [(xk_ffn[0], pk.gp["fk"], hk, 1)], st)
+                ffn_out = torch.empty((M, C), dtype=dt, device=dev)
+                self._gemm_group(M, [(hk, pk.gp["fv"], ffn_out, 0)], st)
+            else:
+                hk = self._lin(xk_ffn[0], ffn.key.weight)
+                _lib.call("rwkv7_activation", code, 2, hk.numel(), P(hk), st)
+                ffn_out = self._lin(hk, ffn.value.weight)
         n_out = M if logit_rows is None else (n_logit_rows if n_logit_rows is not None else logit_rows.numel())
         if n_out == 0:
             return None

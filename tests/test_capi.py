@@ -85,3 +85,25 @@ def test_python_wrapper_raises_library_message(lib):
     with pytest.raises(ValueError, match="bad dtype"):
         _lib.call("rwkv7s_forward", 9, 1, 1, 64, 1, ctypes.c_void_p(16),
                   *[ctypes.c_void_p(16)] * 7, None)
+
+
+def test_gemm_host_side_errors(lib):
+    P = ctypes.c_void_p
+    fake = P(16)
+    # packed size: 64 x 64 tiles, zero padding; invalid sizes give -1 and a message
+    assert lib.rwkv7_gemm_packed_elems(100, 136) == 128 * 192
+    assert lib.rwkv7_gemm_packed_elems(64, 12) == -1 and b"K % 8" in lib.rwkv7_last_error()
+    # pack: ldb below K, misaligned output
+    assert lib.rwkv7_gemm_pack(fake, 8, 16, 64, fake, None) == 1 and b"ldb" in lib.rwkv7_last_error()
+    assert lib.rwkv7_gemm_pack(fake, 64, 16, 64, P(16 + 2), None) == 1
+    # grouped GEMM: problem count, K % 8, lda below K, epilogue code
+    one = (ctypes.c_int * 1)
+    arr = (P * 1)
+    i64 = (ctypes.c_int64 * 1)
+    args = lambda N, K, lda, epi: (4, 1, arr(fake), arr(fake), arr(fake), i64(lda), i64(N), one(N), one(K),
+                                   one(epi), None, 0, None)
+    assert lib.rwkv7_gemm_decode(4, 0, *args(64, 64, 64, 0)[2:]) == 1
+    assert lib.rwkv7_gemm_decode(*args(64, 60, 64, 0)) == 1 and b"K % 8" in lib.rwkv7_last_error()
+    assert lib.rwkv7_gemm_decode(*args(64, 64, 32, 0)) == 1 and b"lda" in lib.rwkv7_last_error()
+    assert lib.rwkv7_gemm_decode(*args(64, 64, 64, 5)) == 1 and b"epi" in lib.rwkv7_last_error()
+    assert lib.rwkv7_gemm_decode_workspace(256, 1, one(2048), one(60)) == -1
