@@ -150,10 +150,11 @@ __device__ __forceinline__ void load_row(const ResidualSrc<IO>& src, int m, int 
     }
 }
 
-// in-place LayerNorm of register rows a (and b when two) with weight/bias w, bv
+// in-place LayerNorm of register rows a (and b when two) with weight/bias held
+// in registers (ww, bb: the row's chunks of this thread)
 template <int NV>
-__device__ __forceinline__ void ln_regs(f32x4 (&a)[NV], f32x4 (&b)[NV], bool two, int C4, const float* w,
-                                        const float* bv, float* red) {
+__device__ __forceinline__ void ln_regs_pre(f32x4 (&a)[NV], f32x4 (&b)[NV], bool two, int C4, const f32x4 (&ww)[NV],
+                                            const f32x4 (&bb)[NV], float* red) {
     const int t = threadIdx.x;
     const float invC = 1.0f / (float)(C4 * 4);
     f32x2 s = {0.f, 0.f};
@@ -178,19 +179,31 @@ __device__ __forceinline__ void ln_regs(f32x4 (&a)[NV], f32x4 (&b)[NV], bool two
             }
         }
     }
-    q = block_sum2(q, red);
+    q = block_sum2(q, red + 2 * kWaves);
     const float ia = 1.0f / sqrtf(q.x * invC + 1e-5f);
     const float ib = 1.0f / sqrtf(q.y * invC + 1e-5f);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int c = t + j * kThreads;
-        if (c < C4) {
-            const f32x4 ww = *reinterpret_cast<const f32x4*>(w + 4 * c);
-            const f32x4 bb = *reinterpret_cast<const f32x4*>(bv + 4 * c);
-            a[j] = (a[j] - ma) * ia * ww + bb;
-            if (two) b[j] = (b[j] - mb) * ib * ww + bb;
+        if (t + j * kThreads < C4) {
+            a[j] = (a[j] - ma) * ia * ww[j] + bb[j];
+            if (two) b[j] = (b[j] - mb) * ib * ww[j] + bb[j];
         }
     }
+}
+
+// the same with weight/bias read from memory
+template <int NV>
+__device__ __forceinline__ void ln_regs(f32x4 (&a)[NV], f32x4 (&b)[NV], bool two, int C4, const float* w,
+                                        const float* bv, float* red) {
+    f32x4 ww[NV], bb[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        const int c = threadIdx.x + j * kThreads;
+        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+        ww[j] = c < C4 ? *reinterpret_cast<const f32x4*>(w + 4 * c) : z;
+        bb[j] = c < C4 ? *reinterpret_cast<const f32x4*>(bv + 4 * c) : z;
+    }
+    ln_regs_pre<NV>(a, b, two, C4, ww, bb, red);
 }
 
 template <typename IO, int NV, int NMIX>
@@ -200,7 +213,7 @@ __global__ __launch_bounds__(kThreads) void shift_mix_kernel(
     float* __restrict__ prev_pool, int pool_slots, const int32_t* __restrict__ row_slot,
     const int32_t* __restrict__ row_last, const float* __restrict__ mix, IO* __restrict__ out)
 {
-    __shared__ float red[2 * kWaves];
+    __shared__ float red[4 * kWaves];
     const int m = blockIdx.x;
     const int t = threadIdx.x;
     const int C4 = C >> 2;
@@ -208,41 +221,72 @@ __global__ __launch_bounds__(kThreads) void shift_mix_kernel(
     if (slot >= pool_slots) slot = -1;
     const int last = row_last[m];
     const bool first = last >= 0 || m == 0;
+    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
 
-    RowRegs<IO, NV> cur, prv;
-    load_row<IO, NV>(src, m, C4, cur);
-    if (first) {
-        const float* p = prev_pool + (size_t)(slot < 0 ? 0 : slot) * C;
+    // embedding row of a token (null: out of range -> zero row)
+    auto emb_row = [&](int row) -> const IO* {
+        const int64_t tk = src.tokens[row];
+        return (tk >= 0 && tk < src.vocab) ? src.emb + tk * (int64_t)C : nullptr;
+    };
+    const IO* e_cur = src.tokens != nullptr ? emb_row(m) : nullptr;
+    const IO* e_prv = (src.tokens != nullptr && !first) ? emb_row(m - 1) : nullptr;
+    // chunk c of the residual of `row` (embedding lookup, or x_in + add)
+    auto resid = [&](int row, const IO* e, int c) -> f32x4 {
+        if (c >= C4) return z;
+        if (src.tokens != nullptr) return e != nullptr ? vec4io<IO>::load(e + 4 * c) : z;
+        f32x4 a = *reinterpret_cast<const f32x4*>(src.x_in + (size_t)row * C + 4 * c);
+        if (src.add != nullptr) a += vec4io<IO>::load(src.add + (size_t)row * C + 4 * c);
+        return a;
+    };
+
+    // Every operand is loaded up front - the row, the previous row (or the
+    // slot's x_prev), the LayerNorm parameters and the mix coefficients - into
+    // plain register arrays, so their latencies overlap.
+    // (wide rows, NV > 4, read the mix coefficients at use instead: their
+    // registers would spill)
+    constexpr bool kPreMix = NV <= 4;
+    constexpr int NVM = kPreMix ? NV : 1;
+    const float* pp = prev_pool + (size_t)(slot < 0 ? 0 : slot) * C;
+    f32x4 cur[NV], prv[NV], lw[NV], lb[NV], mu[NMIX][NVM];
 #pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            const int c = t + j * kThreads;
-            f32x4 z = {0.f, 0.f, 0.f, 0.f};
-            prv.v[j] = (c < C4 && slot >= 0) ? *reinterpret_cast<const f32x4*>(p + 4 * c) : z;
+    for (int j = 0; j < NV; ++j) {
+        const int c = t + j * kThreads;
+        cur[j] = resid(m, e_cur, c);
+        if (first)
+            prv[j] = (c < C4 && slot >= 0) ? *reinterpret_cast<const f32x4*>(pp + 4 * c) : z;
+        else
+            prv[j] = resid(m - 1, e_prv, c);
+        lw[j] = c < C4 ? *reinterpret_cast<const f32x4*>(ln_w + 4 * c) : z;
+        lb[j] = c < C4 ? *reinterpret_cast<const f32x4*>(ln_b + 4 * c) : z;
+        if constexpr (kPreMix) {
+#pragma unroll
+            for (int q = 0; q < NMIX; ++q)
+                mu[q][j] = c < C4 ? *reinterpret_cast<const f32x4*>(mix + (size_t)q * C + 4 * c) : z;
         }
-    } else {
-        load_row<IO, NV>(src, m - 1, C4, prv);
     }
     // ln0 on the residual (layer 0); the previous row needs it too
-    if (src.ln0_w != nullptr) ln_regs<NV>(cur.v, prv.v, !first, C4, src.ln0_w, src.ln0_b, red);
+    if (src.ln0_w != nullptr) ln_regs<NV>(cur, prv, !first, C4, src.ln0_w, src.ln0_b, red);
     if (x_out != nullptr) {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = t + j * kThreads;
-            if (c < C4) *reinterpret_cast<f32x4*>(x_out + (size_t)m * C + 4 * c) = cur.v[j];
+            if (c < C4) *reinterpret_cast<f32x4*>(x_out + (size_t)m * C + 4 * c) = cur[j];
         }
     }
-    ln_regs<NV>(cur.v, prv.v, !first, C4, ln_w, ln_b, red);
+    ln_regs_pre<NV>(cur, prv, !first, C4, lw, lb, red);
 
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = t + j * kThreads;
         if (c < C4) {
-            const f32x4 x = cur.v[j];
-            const f32x4 xx = prv.v[j] - x;
+            const f32x4 x = cur[j];
+            const f32x4 xx = prv[j] - x;
 #pragma unroll
             for (int q = 0; q < NMIX; ++q) {
-                const f32x4 mu = *reinterpret_cast<const f32x4*>(mix + (size_t)q * C + 4 * c);
-                vec4io<IO>::store(out + ((size_t)q * M + m) * C + 4 * c, x + xx * mu);
+                f32x4 mq;
+                if constexpr (kPreMix) mq = mu[q][j];
+                else mq = *reinterpret_cast<const f32x4*>(mix + (size_t)q * C + 4 * c);
+                vec4io<IO>::store(out + ((size_t)q * M + m) * C + 4 * c, x + xx * mq);
             }
         }
     }
@@ -251,15 +295,21 @@ __global__ __launch_bounds__(kThreads) void shift_mix_kernel(
     if (first && slot >= 0 && last >= 0 && last < M) {
         float* dst = prev_pool + (size_t)slot * C;
         if (last != m) {
-            load_row<IO, NV>(src, last, C4, prv);
-            RowRegs<IO, NV> dummy;
-            if (src.ln0_w != nullptr) ln_regs<NV>(prv.v, dummy.v, false, C4, src.ln0_w, src.ln0_b, red);
-            ln_regs<NV>(prv.v, dummy.v, false, C4, ln_w, ln_b, red);
+            const IO* e_last = src.tokens != nullptr ? emb_row(last) : nullptr;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) prv[j] = resid(last, e_last, t + j * kThreads);
+            f32x4 none[NV];
+#pragma unroll
+            for (int j = 0; j < NV; ++j) none[j] = z;
+            if (src.ln0_w != nullptr) ln_regs<NV>(prv, none, false, C4, src.ln0_w, src.ln0_b, red);
+            ln_regs_pre<NV>(prv, none, false, C4, lw, lb, red);
+#pragma unroll
+            for (int j = 0; j < NV; ++j) cur[j] = prv[j];
         }
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = t + j * kThreads;
-            if (c < C4) *reinterpret_cast<f32x4*>(dst + 4 * c) = (last == m) ? cur.v[j] : prv.v[j];
+            if (c < C4) *reinterpret_cast<f32x4*>(dst + 4 * c) = cur[j];
         }
     }
 }
@@ -270,17 +320,23 @@ __global__ __launch_bounds__(kThreads) void final_norm_kernel(
     int C, ResidualSrc<IO> src, const int32_t* __restrict__ rows, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, IO* __restrict__ out)
 {
-    __shared__ float red[2 * kWaves];
+    __shared__ float red[4 * kWaves];
     const int n = blockIdx.x;
     const int m = rows != nullptr ? rows[n] : n;
     const int C4 = C >> 2;
-    RowRegs<IO, NV> cur, dummy;
-    load_row<IO, NV>(src, m, C4, cur);
-    ln_regs<NV>(cur.v, dummy.v, false, C4, ln_w, ln_b, red);
+    RowRegs<IO, NV> row;
+    load_row<IO, NV>(src, m, C4, row);
+    f32x4 cur[NV], none[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        cur[j] = row.v[j];
+        none[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    ln_regs<NV>(cur, none, false, C4, ln_w, ln_b, red);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = threadIdx.x + j * kThreads;
-        if (c < C4) vec4io<IO>::store(out + (size_t)n * C + 4 * c, cur.v[j]);
+        if (c < C4) vec4io<IO>::store(out + (size_t)n * C + 4 * c, cur[j]);
     }
 }
 
