@@ -81,17 +81,20 @@ struct GemmBatch {
     int bm, bn;       // tile of the launch (read by gemm_reduce_kernel)
 };
 
-// Block tile: WM x WN waves, each wave MS x NS MFMA tiles of 32 x 32; a ring
-// of R LDS stages.
-template <int WM_, int WN_, int MS_, int NS_, int R_>
+// Block tile: WM x WN x KG waves, each wave MS x NS MFMA tiles of 32 x 32 over
+// 1/KG of each stage's K steps (KG wave groups, summed at the end); a ring of
+// R LDS stages.  More waves per block means more waves issuing loads: one
+// wave's direct loads stream at ~35 GB/s (measured), a CU's at ~130 GB/s.
+template <int WM_, int WN_, int MS_, int NS_, int R_, int KG_ = 1>
 struct Tile {
-    static constexpr int WM = WM_, WN = WN_, MS = MS_, NS = NS_, R = R_;
-    static constexpr int NWAVE = WM * WN, THREADS = 64 * NWAVE;
+    static constexpr int WM = WM_, WN = WN_, MS = MS_, NS = NS_, R = R_, KG = KG_;
+    static constexpr int NWAVE = WM * WN * KG, THREADS = 64 * NWAVE;
     static constexpr int BM = 32 * MS * WM, BN = 32 * NS * WN;
     static constexpr int ROWS = BM + BN;          // stage rows: A rows, then B rows
     static constexpr int IPW = ROWS / 8 / NWAVE;  // direct loads per wave per stage (8 rows each)
     static constexpr int STAGE = ROWS * 128;      // bytes
-    static_assert(NWAVE == 4 || NWAVE == 8, "4 or 8 waves per block");
+    static_assert(NWAVE == 4 || NWAVE == 8 || NWAVE == 16, "4, 8 or 16 waves per block");
+    static_assert(KG == 1 || KG == 2 || KG == 4, "K-step groups divide the 4 steps of a stage");
     static_assert(BN % 64 == 0, "packed weights come in 64-row tiles");
     static_assert(IPW * 8 * NWAVE == ROWS, "loads split evenly over the waves");
     static_assert(R >= 2 && (R - 2) * IPW < 64, "vmcnt holds at most 63 outstanding loads");
@@ -192,15 +195,17 @@ __global__ __launch_bounds__(T::THREADS) void gemm_decode_kernel(GemmBatch batch
 #pragma unroll
         for (int b = 0; b < T::NS; ++b) acc[a][b] = f32x16{0.f};
     const int lr = lane & 31, hi = lane >> 5;
-    const int wm = (wave / T::WN) * (32 * T::MS), wn = (wave % T::WN) * (32 * T::NS);
+    const int wt = wave % (T::WM * T::WN), kgrp = wave / (T::WM * T::WN);
+    const int wm = (wt / T::WN) * (32 * T::MS), wn = (wt % T::WN) * (32 * T::NS);
+    constexpr int KS = 4 / T::KG;  // k steps of 16 per stage for this wave
     auto mma = [&](int s) {
         const uint8_t* st = ring + (s % T::R) * T::STAGE;
         // every operand of the stage is read before the first product, so the
         // LDS latency is paid once per stage rather than once per k step
-        bf16x8_t af[4][T::MS], bfr[4][T::NS];
+        bf16x8_t af[KS][T::MS], bfr[KS][T::NS];
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const int c = 2 * kk + hi;
+        for (int kk = 0; kk < KS; ++kk) {
+            const int c = 2 * (kgrp * KS + kk) + hi;
 #pragma unroll
             for (int a = 0; a < T::MS; ++a) {
                 const int row = wm + 32 * a + lr;
@@ -214,7 +219,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_decode_kernel(GemmBatch batch
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the products
 #pragma unroll
-        for (int kk = 0; kk < 4; ++kk)
+        for (int kk = 0; kk < KS; ++kk)
 #pragma unroll
             for (int a = 0; a < T::MS; ++a)
 #pragma unroll
@@ -239,6 +244,36 @@ __global__ __launch_bounds__(T::THREADS) void gemm_decode_kernel(GemmBatch batch
         asm volatile("" ::: "memory");  // no LDS read moves above the barrier
         if (s + T::R - 1 < nst) issue(s + T::R - 1);
         mma(s);
+    }
+
+    if constexpr (T::KG > 1) {
+        // sum the K groups' accumulators into group 0 through the (now idle) ring
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        float* red = reinterpret_cast<float*>(ring);
+        constexpr int PER = T::MS * T::NS * 16;  // floats per lane
+        static_assert((size_t)(T::KG - 1) * T::WM * T::WN * 64 * PER * 4 <= (size_t)T::R * T::STAGE, "LDS");
+        if (kgrp > 0) {
+            float* dst = red + ((size_t)((kgrp - 1) * T::WM * T::WN + wt) * PER) * 64 + lane;
+#pragma unroll
+            for (int a = 0; a < T::MS; ++a)
+#pragma unroll
+                for (int b = 0; b < T::NS; ++b)
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) dst[((a * T::NS + b) * 16 + q) * 64] = acc[a][b][q];
+        }
+        __syncthreads();
+        if (kgrp > 0) return;
+#pragma unroll
+        for (int g = 1; g < T::KG; ++g) {
+            const float* srcp = red + ((size_t)((g - 1) * T::WM * T::WN + wt) * PER) * 64 + lane;
+#pragma unroll
+            for (int a = 0; a < T::MS; ++a)
+#pragma unroll
+                for (int b = 0; b < T::NS; ++b)
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) acc[a][b][q] += srcp[((a * T::NS + b) * 16 + q) * 64];
+        }
     }
 
     if (P.splits == 1) {
@@ -398,13 +433,13 @@ hipError_t launch_tile(int M, int count, const void* const* A, const void* const
     return hipGetLastError();
 }
 
-// The library's tile: 64 x 64, 4 waves, 4 stages.  Sweeps over 64..256 x
-// 64..256 tiles, 4 or 8 waves, 2..8 stages and 1..8 K splits at the 1.5B
-// decode shapes (M = 32..256) put it first or within a few percent of the
-// best everywhere: a CU's load path, not the tile, bounds these launches.
+// The library's tile: 64 x 64, 8 waves (two K groups), 4 stages.  Sweeps over
+// 64..256 x 64..256 tiles, 4, 8 or 16 waves, 2..8 stages and 1..8 K splits at
+// the 1.5B decode shapes (M = 32..256) put it first or within a few percent of
+// the best everywhere: a CU's load path, not the tile, bounds these launches.
 // Launches aim at 384 blocks (1.5 per CU) by splitting K into ranges of at
 // least 512.
-using TileDecode = Tile<2, 2, 1, 1, 4>;
+using TileDecode = Tile<2, 2, 1, 1, 4, 2>;
 constexpr int kTarget = 384, kMinK = 512;
 
 Plan plan_for(int M, int count, const int* N, const int* K) {
