@@ -176,7 +176,12 @@ __global__ __launch_bounds__(T::THREADS) void gemm_decode_kernel(GemmBatch batch
         }
     }
     const bf16_t* zero = reinterpret_cast<const bf16_t*>(g_gemm_zero_chunk);
+    // A wave whose stage rows all lie in the A part past the last real row
+    // issues nothing: those rows feed only outputs that are never stored, so
+    // their LDS can hold anything.  (Its waits then pass at once.)
+    const bool idle = 8 * (wave + 1) * T::IPW <= T::BM && m0 + 8 * wave * T::IPW >= M;
     auto issue = [&](int s) {
+        if (idle) return;
         uint8_t* dst = ring + (s % T::R) * T::STAGE + wave * T::IPW * 8 * 128;
 #pragma unroll
         for (int i = 0; i < T::IPW; ++i) {

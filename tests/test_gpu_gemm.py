@@ -102,3 +102,4 @@ def test_strided_operands(gpu_device):
     RWKV7Model._gemm_group(37, [(A, PackedWeight(B), C, 0)], _lib.stream_of(C))
     torch.cuda.synchronize()
     assert close(C, ref(A, B, 0))
+
