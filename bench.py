@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of rwkvtune's batched-generation hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|decode|prefill|tmix]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|cfg5|decode|prefill|tmix]
 
 Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a message.
 
@@ -15,6 +15,10 @@ rollout (default)  GRPO rollout on RWKV-7 1.5B (L=24, C=2048, H=32, V=65536), bf
     ``GRPOBatchGenerator.generate``.  A step is one whole rollout; value = generated
     tokens / wall time over the K timed rollouts (prefill, first token, decode and
     result assembly included).
+cfg5               rollout on RWKV-7 7.2B (L=32, C=4096, H=64), bf16: 128 random 2048-token
+    prompts, chunked prefill (chunk 256), up to 1024 sampled tokens (temperature 1.0,
+    top_p 0.95) with Geometric(mean 600) stops, 128 slots; value = generated
+    tokens / wall time of the rollout.  No CPU baseline (7.2B in fp32 on the host).
 decode             isolated WKV7 decode kernel at B=256 slots, H=32 (cfg2); a step is
     one launch; value = algorithmic GB/s.
 tmix               the fused decode time-mix kernel alone at the rollout shape (the
@@ -117,11 +121,21 @@ def copy_reference(dev, n_bytes=256 * 32 * 64 * 64 * 4, reps=8):
     return n_bytes
 
 
-def tmix_decode_leg(dev, iters=480):
-    """Fused single-token time-mix at the rollout shape, 24 rotating layer pools."""
+def cfg5_workload(seed=5):
+    """cfg5: 128 random 2048-token prompts; per-sequence stop length
+    ~ Geometric(mean 600) capped at 1024."""
+    g = torch.Generator().manual_seed(seed)
+    prompts = [torch.randint(1, MAX_VALID_ID + 1, (2048,), generator=g).tolist() for _ in range(128)]
+    u = torch.rand(128, generator=g, dtype=torch.float64)
+    caps = torch.clamp(torch.ceil(torch.log1p(-u) / torch.log1p(torch.tensor(-1.0 / 600))), 1, 1024)
+    return prompts, [int(c) for c in caps]
+
+
+def tmix_decode_leg(dev, iters=480, S=256, H=32, L=24):
+    """Fused single-token time-mix at a rollout shape (default cfg4: 256 slots,
+    H=32), L rotating layer pools."""
     from rwkvtune_amd import _lib
     from rwkvtune_amd.workloads import wkv_state
-    S, H, L = 256, 32, 24
     C = H * N
     g = torch.Generator(device=dev).manual_seed(5)
     rnd = lambda *s: torch.randn(*s, generator=g, device=dev)
@@ -143,7 +157,7 @@ def tmix_decode_leg(dev, iters=480):
     us = time_launches(launch, iters, st)
     units = S * H
     gbs = units * TMIX_BYTES_PER_UNIT / (us * 1e-6) / 1e9
-    return {"kernel": "tmix_decode_kernel<bf16> (fused WKV decode time-mix)", "slots": S, "H": H,
+    return {"kernel": "tmix_decode_kernel<bf16> (fused WKV decode time-mix)", "slots": S, "H": H, "pools": L,
             "us_per_launch": us, "bytes_per_launch": units * TMIX_BYTES_PER_UNIT, "GBs": gbs,
             "frac": gbs / PEAK_HBM_GBS, "launches": iters}
 
@@ -281,6 +295,42 @@ def rollout(steps, warmup, dev):
                                   "ms_per_step": total_s / steps * 1e3, "runs": stats}
 
 
+def rollout_cfg5(steps, warmup, dev):
+    """cfg5: RWKV-7 7.2B (bf16, seeded dense init), 128 prompts x 2048 tokens,
+    chunked prefill (chunk 256), up to 1024 sampled tokens per sequence (temp 1.0,
+    top_p 0.95) with Geometric(600) stops, all 128 sequences in slots at once."""
+    from rwkvtune_amd.grpo_batch_generator import GRPOBatchGenerator
+    from rwkvtune_amd.model import build_model, config_from_preset
+    cfg = config_from_preset("rwkv7-7.2b")
+    log("[bench] building RWKV-7 7.2B (bf16, seeded dense init) ...")
+    model = build_model(cfg, dtype=torch.bfloat16, device=dev, seed=7272)
+    prompts, caps = cfg5_workload()
+    gen = GRPOBatchGenerator(model, NullTokenizer(), chunk_size=256, max_decode_batch_size=128,
+                             eos_token_id=None, verbose=False)
+    kw = dict(max_new_tokens=1024, num_generations=1, temperature=1.0, top_p=0.95, top_k=0,
+              max_new_tokens_per_seq=caps)
+    gen.generate(prompts[:2], 8, num_generations=1, temperature=1.0, top_p=0.95)
+    for i in range(warmup):
+        log(f"[bench] cfg5 warm-up rollout {i + 1}/{warmup}")
+        gen.generate(prompts, **kw)
+    total_gen, total_s, stats = 0, 0.0, []
+    for i in range(steps):
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        out = gen.generate(prompts, **kw)
+        torch.cuda.synchronize(dev)
+        dt = time.perf_counter() - t0
+        n_gen = int(out["masks"].sum())
+        total_gen += n_gen
+        total_s += dt
+        st = dict(gen.last_stats)
+        stats.append(st)
+        log(f"[bench] cfg5 rollout {i + 1}/{steps}: {n_gen} tokens in {dt:.3f} s = {n_gen / dt:.0f} tok/s "
+            f"(prefill {st['prefill_s']:.3f}s, decode {st['decode_s']:.3f}s, {st['decode_steps']} steps)")
+    return {"tokens": total_gen, "seconds": total_s, "value": total_gen / total_s,
+            "ms_per_step": total_s / steps * 1e3, "runs": stats, "prompt_tokens": sum(len(p) for p in prompts)}
+
+
 def cpu_baseline_rollout(model, prompts, paths=256, decode_steps=2):
     """The reference CPU rollout (oracle/: fp32 forward_with_state, batched
     sample_batch rules) on a bounded sample: one prompt prefilled, forked to
@@ -337,7 +387,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="rollout", choices=["rollout", "decode", "prefill", "tmix"])
+    ap.add_argument("--workload", default="rollout", choices=["rollout", "cfg5", "decode", "prefill", "tmix"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -388,6 +438,31 @@ def main():
             "wkv7_prefill_cfg3": {k: pf[k] for k in ("us_per_launch", "tokens_per_s", "mfma_bf16_TFLOPs",
                                                      "mfma_frac", "GBs", "hbm_frac", "speedup_vs_token_serial")},
             "cpu_baseline": cpu,
+        }
+    elif a.workload == "cfg5":
+        steps = 1 if a.steps is None else a.steps
+        warmup = 1 if a.warmup is None else a.warmup
+        ro = rollout_cfg5(steps, warmup, dev)
+        log("[bench] fused decode time-mix kernel at the cfg5 shape (roofline) ...")
+        tm = tmix_decode_leg(dev, S=128, H=64, L=32)
+        log(f"[bench] tmix_decode cfg5 shape: {tm['us_per_launch']:.2f} us/launch, {tm['GBs']:.0f} GB/s")
+        run = ro["runs"][-1]
+        out = {
+            "metric": METRIC, "value": ro["value"], "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": ro["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16 weights/activations, fp32 WKV state and element-wise",
+            "data": "synthetic (random prompts, seeded dense random-init weights)",
+            "config": {"workload": "cfg5 rollout: RWKV7-7.2B (L=32, C=4096, H=64), 128 prompts x 2048 tokens, "
+                                   "chunked prefill (chunk 256), temp 1.0, top_p 0.95, max 1024 new, "
+                                   "geometric(600) stops, 128 slots",
+                       "global_batch": 128, "seq_len": 2048 + 1024, "parallelism": "none (1 GPU)",
+                       "generated_tokens": ro["tokens"] // steps, "prompt_tokens": ro["prompt_tokens"],
+                       "decode_steps": run["decode_steps"], "prefill_s": run["prefill_s"],
+                       "decode_s": run["decode_s"]},
+            "roofline": {"bound": "hbm", "achieved": tm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": tm["frac"], "traffic": None, "kernel": tm["kernel"] + " at 128 slots, H=64",
+                         "us_per_launch": tm["us_per_launch"], "algorithmic_bytes": tm["bytes_per_launch"]},
+            "cpu_baseline": None,
         }
     elif a.workload == "tmix":
         # the roofline kernel alone (for kernel-trace / PMC runs), then a plain copy of
