@@ -98,21 +98,23 @@ template <> struct vec4io<f16_t> {
     }
 };
 
-// two block sums at once (LDS red: 2 * kWaves floats)
+// two sums over a TH-thread block at once (LDS red: 2 * TH / 64 floats)
+template <int TH>
 __device__ __forceinline__ f32x2 block_sum2(f32x2 v, float* red) {
+    constexpr int W = TH / 64;
     v.x = wave_sum(v.x);
     v.y = wave_sum(v.y);
     __syncthreads();
     if ((threadIdx.x & 63) == 0) {
         red[threadIdx.x >> 6] = v.x;
-        red[kWaves + (threadIdx.x >> 6)] = v.y;
+        red[W + (threadIdx.x >> 6)] = v.y;
     }
     __syncthreads();
     f32x2 s = {0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < kWaves; ++i) {
+    for (int i = 0; i < W; ++i) {
         s.x += red[i];
-        s.y += red[kWaves + i];
+        s.y += red[W + i];
     }
     return s;
 }
@@ -123,7 +125,7 @@ struct RowRegs {
 };
 
 // residual of row m into registers (emb lookup or x_in + add)
-template <typename IO, int NV>
+template <typename IO, int NV, int TH>
 __device__ __forceinline__ void load_row(const ResidualSrc<IO>& src, int m, int C4, RowRegs<IO, NV>& r) {
     const int t = threadIdx.x;
     if (src.tokens != nullptr) {
@@ -132,7 +134,7 @@ __device__ __forceinline__ void load_row(const ResidualSrc<IO>& src, int m, int 
         const IO* e = src.emb + (ok ? tk : 0) * (int64_t)C4 * 4;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const int c = t + j * kThreads;
+            const int c = t + j * TH;
             f32x4 z = {0.f, 0.f, 0.f, 0.f};
             r.v[j] = (c < C4 && ok) ? vec4io<IO>::load(e + 4 * c) : z;
         }
@@ -141,7 +143,7 @@ __device__ __forceinline__ void load_row(const ResidualSrc<IO>& src, int m, int 
         const IO* ad = src.add != nullptr ? src.add + (size_t)m * C4 * 4 : nullptr;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const int c = t + j * kThreads;
+            const int c = t + j * TH;
             f32x4 z = {0.f, 0.f, 0.f, 0.f};
             f32x4 a = (c < C4) ? *reinterpret_cast<const f32x4*>(x + 4 * c) : z;
             if (ad != nullptr && c < C4) a += vec4io<IO>::load(ad + 4 * c);
@@ -152,7 +154,7 @@ __device__ __forceinline__ void load_row(const ResidualSrc<IO>& src, int m, int 
 
 // in-place LayerNorm of register rows a (and b when two) with weight/bias held
 // in registers (ww, bb: the row's chunks of this thread)
-template <int NV>
+template <int NV, int TH>
 __device__ __forceinline__ void ln_regs_pre(f32x4 (&a)[NV], f32x4 (&b)[NV], bool two, int C4, const f32x4 (&ww)[NV],
                                             const f32x4 (&bb)[NV], float* red) {
     const int t = threadIdx.x;
@@ -160,17 +162,17 @@ __device__ __forceinline__ void ln_regs_pre(f32x4 (&a)[NV], f32x4 (&b)[NV], bool
     f32x2 s = {0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        if (t + j * kThreads < C4) {
+        if (t + j * TH < C4) {
             s.x += a[j].x + a[j].y + a[j].z + a[j].w;
             if (two) s.y += b[j].x + b[j].y + b[j].z + b[j].w;
         }
     }
-    s = block_sum2(s, red);
+    s = block_sum2<TH>(s, red);
     const float ma = s.x * invC, mb = s.y * invC;
     f32x2 q = {0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        if (t + j * kThreads < C4) {
+        if (t + j * TH < C4) {
             f32x4 da = a[j] - ma;
             q.x += da.x * da.x + da.y * da.y + da.z * da.z + da.w * da.w;
             if (two) {
@@ -179,12 +181,12 @@ __device__ __forceinline__ void ln_regs_pre(f32x4 (&a)[NV], f32x4 (&b)[NV], bool
             }
         }
     }
-    q = block_sum2(q, red + 2 * kWaves);
+    q = block_sum2<TH>(q, red + 2 * (TH / 64));
     const float ia = 1.0f / sqrtf(q.x * invC + 1e-5f);
     const float ib = 1.0f / sqrtf(q.y * invC + 1e-5f);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        if (t + j * kThreads < C4) {
+        if (t + j * TH < C4) {
             a[j] = (a[j] - ma) * ia * ww[j] + bb[j];
             if (two) b[j] = (b[j] - mb) * ib * ww[j] + bb[j];
         }
@@ -192,28 +194,28 @@ __device__ __forceinline__ void ln_regs_pre(f32x4 (&a)[NV], f32x4 (&b)[NV], bool
 }
 
 // the same with weight/bias read from memory
-template <int NV>
+template <int NV, int TH>
 __device__ __forceinline__ void ln_regs(f32x4 (&a)[NV], f32x4 (&b)[NV], bool two, int C4, const float* w,
                                         const float* bv, float* red) {
     f32x4 ww[NV], bb[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int c = threadIdx.x + j * kThreads;
+        const int c = threadIdx.x + j * TH;
         const f32x4 z = {0.f, 0.f, 0.f, 0.f};
         ww[j] = c < C4 ? *reinterpret_cast<const f32x4*>(w + 4 * c) : z;
         bb[j] = c < C4 ? *reinterpret_cast<const f32x4*>(bv + 4 * c) : z;
     }
-    ln_regs_pre<NV>(a, b, two, C4, ww, bb, red);
+    ln_regs_pre<NV, TH>(a, b, two, C4, ww, bb, red);
 }
 
-template <typename IO, int NV, int NMIX>
-__global__ __launch_bounds__(kThreads) void shift_mix_kernel(
+template <typename IO, int NV, int NMIX, int TH>
+__global__ __launch_bounds__(TH) void shift_mix_kernel(
     int M, int C, ResidualSrc<IO> src, float* __restrict__ x_out,
     const float* __restrict__ ln_w, const float* __restrict__ ln_b,
     float* __restrict__ prev_pool, int pool_slots, const int32_t* __restrict__ row_slot,
     const int32_t* __restrict__ row_last, const float* __restrict__ mix, IO* __restrict__ out)
 {
-    __shared__ float red[4 * kWaves];
+    __shared__ float red[4 * (TH / 64)];
     const int m = blockIdx.x;
     const int t = threadIdx.x;
     const int C4 = C >> 2;
@@ -242,15 +244,15 @@ __global__ __launch_bounds__(kThreads) void shift_mix_kernel(
     // Every operand is loaded up front - the row, the previous row (or the
     // slot's x_prev), the LayerNorm parameters and the mix coefficients - into
     // plain register arrays, so their latencies overlap.
-    // (wide rows, NV > 4, read the mix coefficients at use instead: their
-    // registers would spill)
-    constexpr bool kPreMix = NV <= 4;
+    // (with two chunks per thread in 1024-thread blocks - at most 128 registers -
+    // the mix coefficients are read at use instead: their registers would spill)
+    constexpr bool kPreMix = NV == 1 || TH < 1024;
     constexpr int NVM = kPreMix ? NV : 1;
     const float* pp = prev_pool + (size_t)(slot < 0 ? 0 : slot) * C;
     f32x4 cur[NV], prv[NV], lw[NV], lb[NV], mu[NMIX][NVM];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int c = t + j * kThreads;
+        const int c = t + j * TH;
         cur[j] = resid(m, e_cur, c);
         if (first)
             prv[j] = (c < C4 && slot >= 0) ? *reinterpret_cast<const f32x4*>(pp + 4 * c) : z;
@@ -265,19 +267,19 @@ __global__ __launch_bounds__(kThreads) void shift_mix_kernel(
         }
     }
     // ln0 on the residual (layer 0); the previous row needs it too
-    if (src.ln0_w != nullptr) ln_regs<NV>(cur, prv, !first, C4, src.ln0_w, src.ln0_b, red);
+    if (src.ln0_w != nullptr) ln_regs<NV, TH>(cur, prv, !first, C4, src.ln0_w, src.ln0_b, red);
     if (x_out != nullptr) {
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const int c = t + j * kThreads;
+            const int c = t + j * TH;
             if (c < C4) *reinterpret_cast<f32x4*>(x_out + (size_t)m * C + 4 * c) = cur[j];
         }
     }
-    ln_regs_pre<NV>(cur, prv, !first, C4, lw, lb, red);
+    ln_regs_pre<NV, TH>(cur, prv, !first, C4, lw, lb, red);
 
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int c = t + j * kThreads;
+        const int c = t + j * TH;
         if (c < C4) {
             const f32x4 x = cur[j];
             const f32x4 xx = prv[j] - x;
@@ -297,45 +299,45 @@ __global__ __launch_bounds__(kThreads) void shift_mix_kernel(
         if (last != m) {
             const IO* e_last = src.tokens != nullptr ? emb_row(last) : nullptr;
 #pragma unroll
-            for (int j = 0; j < NV; ++j) prv[j] = resid(last, e_last, t + j * kThreads);
+            for (int j = 0; j < NV; ++j) prv[j] = resid(last, e_last, t + j * TH);
             f32x4 none[NV];
 #pragma unroll
             for (int j = 0; j < NV; ++j) none[j] = z;
-            if (src.ln0_w != nullptr) ln_regs<NV>(prv, none, false, C4, src.ln0_w, src.ln0_b, red);
-            ln_regs_pre<NV>(prv, none, false, C4, lw, lb, red);
+            if (src.ln0_w != nullptr) ln_regs<NV, TH>(prv, none, false, C4, src.ln0_w, src.ln0_b, red);
+            ln_regs_pre<NV, TH>(prv, none, false, C4, lw, lb, red);
 #pragma unroll
             for (int j = 0; j < NV; ++j) cur[j] = prv[j];
         }
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const int c = t + j * kThreads;
+            const int c = t + j * TH;
             if (c < C4) *reinterpret_cast<f32x4*>(dst + 4 * c) = cur[j];
         }
     }
 }
 
 // y = LN_out(x_in[row] + add[row]) for the n listed rows (rows = null: 0..n-1)
-template <typename IO, int NV>
-__global__ __launch_bounds__(kThreads) void final_norm_kernel(
+template <typename IO, int NV, int TH>
+__global__ __launch_bounds__(TH) void final_norm_kernel(
     int C, ResidualSrc<IO> src, const int32_t* __restrict__ rows, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, IO* __restrict__ out)
 {
-    __shared__ float red[4 * kWaves];
+    __shared__ float red[4 * (TH / 64)];
     const int n = blockIdx.x;
     const int m = rows != nullptr ? rows[n] : n;
     const int C4 = C >> 2;
     RowRegs<IO, NV> row;
-    load_row<IO, NV>(src, m, C4, row);
+    load_row<IO, NV, TH>(src, m, C4, row);
     f32x4 cur[NV], none[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         cur[j] = row.v[j];
         none[j] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    ln_regs<NV>(cur, none, false, C4, ln_w, ln_b, red);
+    ln_regs<NV, TH>(cur, none, false, C4, ln_w, ln_b, red);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-        const int c = threadIdx.x + j * kThreads;
+        const int c = threadIdx.x + j * TH;
         if (c < C4) vec4io<IO>::store(out + (size_t)n * C + 4 * c, cur[j]);
     }
 }
@@ -345,17 +347,41 @@ __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + expf
 // softplus as torch computes it (threshold 20: identity above)
 __device__ __forceinline__ float softplusf_(float x) { return x > 20.f ? x : log1pf(expf(x)); }
 
+__device__ __forceinline__ float activation_fn(int kind, float v) {
+    if (kind == 0) return tanhf(v);
+    if (kind == 1) return sigmoidf_(v);
+    const float r = v > 0.f ? v : 0.f;
+    return r * r;
+}
+
+// 8 consecutive elements per thread; vec: x is 16-byte aligned, so whole groups
+// of 8 move with 16-byte (32-byte for float32) accesses
 template <typename IO>
-__global__ void activation_kernel(int kind, int64_t n, IO* __restrict__ x) {
+__global__ void activation_kernel(int kind, int64_t n, IO* __restrict__ x, int vec) {
     typedef io_traits<IO> tr;
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= n) return;
-    const float v = tr::to_f32(x[i]);
-    float o;
-    if (kind == 0) o = tanhf(v);
-    else if (kind == 1) o = sigmoidf_(v);
-    else { const float r = v > 0.f ? v : 0.f; o = r * r; }
-    x[i] = tr::from_f32(o);
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (i0 >= n) return;
+    if (vec && i0 + 8 <= n) {
+        if constexpr (sizeof(IO) == 2) {
+            uint4 u = *reinterpret_cast<const uint4*>(x + i0);
+            IO* e = reinterpret_cast<IO*>(&u);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) e[j] = tr::from_f32(activation_fn(kind, tr::to_f32(e[j])));
+            *reinterpret_cast<uint4*>(x + i0) = u;
+        } else {
+            f32x4 a = *reinterpret_cast<const f32x4*>(x + i0);
+            f32x4 b = *reinterpret_cast<const f32x4*>(x + i0 + 4);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                a[j] = activation_fn(kind, a[j]);
+                b[j] = activation_fn(kind, b[j]);
+            }
+            *reinterpret_cast<f32x4*>(x + i0) = a;
+            *reinterpret_cast<f32x4*>(x + i0 + 4) = b;
+        }
+        return;
+    }
+    for (int64_t i = i0; i < n && i < i0 + 8; ++i) x[i] = tr::from_f32(activation_fn(kind, tr::to_f32(x[i])));
 }
 
 struct TmixParams {
@@ -554,24 +580,42 @@ __global__ __launch_bounds__(64) void tmix_decode_kernel(
 // launchers (called from capi.hip)
 // ---------------------------------------------------------------------------
 
-template <typename IO, int NV>
+template <typename IO, int NV, int TH>
 static hipError_t launch_shift_mix_nv(int M, int C, const ResidualSrc<IO>& src, float* x_out, const float* ln_w,
                                       const float* ln_b, float* prev_pool, int pool_slots, const int32_t* row_slot,
                                       const int32_t* row_last, int n_mix, const float* mix, void* out, hipStream_t st)
 {
     if (n_mix == 7)
-        hipLaunchKernelGGL((shift_mix_kernel<IO, NV, 7>), dim3(M), dim3(kThreads), 0, st, M, C, src, x_out, ln_w,
+        hipLaunchKernelGGL((shift_mix_kernel<IO, NV, 7, TH>), dim3(M), dim3(TH), 0, st, M, C, src, x_out, ln_w,
                            ln_b, prev_pool, pool_slots, row_slot, row_last, mix, (IO*)out);
     else if (n_mix == 6)
-        hipLaunchKernelGGL((shift_mix_kernel<IO, NV, 6>), dim3(M), dim3(kThreads), 0, st, M, C, src, x_out, ln_w,
+        hipLaunchKernelGGL((shift_mix_kernel<IO, NV, 6, TH>), dim3(M), dim3(TH), 0, st, M, C, src, x_out, ln_w,
                            ln_b, prev_pool, pool_slots, row_slot, row_last, mix, (IO*)out);
     else if (n_mix == 1)
-        hipLaunchKernelGGL((shift_mix_kernel<IO, NV, 1>), dim3(M), dim3(kThreads), 0, st, M, C, src, x_out, ln_w,
+        hipLaunchKernelGGL((shift_mix_kernel<IO, NV, 1, TH>), dim3(M), dim3(TH), 0, st, M, C, src, x_out, ln_w,
                            ln_b, prev_pool, pool_slots, row_slot, row_last, mix, (IO*)out);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
 }
+
+// Threads per row block: one block holds a row, so wide rows get more waves
+// (a CU's load rate grows with the waves issuing loads); every thread holds
+// NV <= 2 float4 chunks of the row.
+static int row_threads(int C) {
+    const int C4 = C / 4;
+    return C4 >= 1024 ? 1024 : (C4 >= 512 ? 512 : 256);
+}
+
+#define RWKV7_ROW_DISPATCH(CALL)                                   \
+    {                                                              \
+        const int th = row_threads(C);                             \
+        const int nv = (C / 4 + th - 1) / th;                      \
+        if (nv < 1 || nv > 2) return hipErrorInvalidValue;         \
+        if (th == 1024) { if (nv == 1) CALL(1, 1024) else CALL(2, 1024) } \
+        else if (th == 512) { if (nv == 1) CALL(1, 512) else CALL(2, 512) } \
+        else { if (nv == 1) CALL(1, 256) else CALL(2, 256) }      \
+    }
 
 // n_mix in {1, 6, 7}; C a multiple of 4 and at most 8 * 1024
 template <typename IO>
@@ -582,22 +626,10 @@ hipError_t launch_shift_mix(int M, int C, const float* x_in, const void* add, co
                             int n_mix, const float* mix, void* out, hipStream_t st)
 {
     ResidualSrc<IO> src{x_in, (const IO*)add, tokens, (const IO*)emb, vocab, ln0_w, ln0_b};
-    const int nv = (C / 4 + kThreads - 1) / kThreads;
-    switch (nv) {
-        case 1: return launch_shift_mix_nv<IO, 1>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots, row_slot,
-                                                  row_last, n_mix, mix, out, st);
-        case 2: return launch_shift_mix_nv<IO, 2>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots, row_slot,
-                                                  row_last, n_mix, mix, out, st);
-        case 3: return launch_shift_mix_nv<IO, 3>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots, row_slot,
-                                                  row_last, n_mix, mix, out, st);
-        case 4: return launch_shift_mix_nv<IO, 4>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots, row_slot,
-                                                  row_last, n_mix, mix, out, st);
-        case 5: case 6: return launch_shift_mix_nv<IO, 6>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots,
-                                                          row_slot, row_last, n_mix, mix, out, st);
-        case 7: case 8: return launch_shift_mix_nv<IO, 8>(M, C, src, x_out, ln_w, ln_b, prev_pool, pool_slots,
-                                                          row_slot, row_last, n_mix, mix, out, st);
-        default: return hipErrorInvalidValue;
-    }
+#define RWKV7_SM(NVV, THH) return launch_shift_mix_nv<IO, NVV, THH>(M, C, src, x_out, ln_w, ln_b, prev_pool, \
+                                                                  pool_slots, row_slot, row_last, n_mix, mix, out, st);
+    RWKV7_ROW_DISPATCH(RWKV7_SM)
+#undef RWKV7_SM
 }
 
 template <typename IO>
@@ -605,27 +637,18 @@ hipError_t launch_final_norm(int n, int C, const float* x_in, const void* add, c
                              const float* ln_w, const float* ln_b, void* out, hipStream_t st)
 {
     ResidualSrc<IO> src{x_in, (const IO*)add, nullptr, nullptr, 0, nullptr, nullptr};
-    const int nv = (C / 4 + kThreads - 1) / kThreads;
-#define RWKV7_FN(NVV) hipLaunchKernelGGL((final_norm_kernel<IO, NVV>), dim3(n), dim3(kThreads), 0, st, C, src, rows, \
-                                         ln_w, ln_b, (IO*)out)
-    switch (nv) {
-        case 1: RWKV7_FN(1); break;
-        case 2: RWKV7_FN(2); break;
-        case 3: RWKV7_FN(3); break;
-        case 4: RWKV7_FN(4); break;
-        case 5: case 6: RWKV7_FN(6); break;
-        case 7: case 8: RWKV7_FN(8); break;
-        default: return hipErrorInvalidValue;
-    }
+#define RWKV7_FN(NVV, THH) { hipLaunchKernelGGL((final_norm_kernel<IO, NVV, THH>), dim3(n), dim3(THH), 0, st, C, src, \
+                                                rows, ln_w, ln_b, (IO*)out); return hipGetLastError(); }
+    RWKV7_ROW_DISPATCH(RWKV7_FN)
 #undef RWKV7_FN
-    return hipGetLastError();
 }
 
 template <typename IO>
 hipError_t launch_activation(int kind, int64_t n, void* x, hipStream_t st)
 {
-    const unsigned grid = (unsigned)((n + 255) / 256);
-    hipLaunchKernelGGL(activation_kernel<IO>, dim3(grid), dim3(256), 0, st, kind, n, (IO*)x);
+    const unsigned grid = (unsigned)((n + 8 * 256 - 1) / (8 * 256));
+    const int vec = (((uintptr_t)x) & 15) == 0;
+    hipLaunchKernelGGL(activation_kernel<IO>, dim3(grid), dim3(256), 0, st, kind, n, (IO*)x, vec);
     return hipGetLastError();
 }
 

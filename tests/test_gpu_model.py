@@ -157,3 +157,24 @@ def test_grouped_gemm_decode_path(gpu_device):
             check_states(st, ref_s, 3e-2)
     finally:
         m.use_grouped_gemm = False
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_activation_kernel(gpu_device, dtype):
+    """rwkv7_activation (tanh / sigmoid / relu^2 in place) against torch in float32
+    rounded once to the I/O dtype: whole 8-element groups, a ragged tail, and a
+    view that is not 16-byte aligned (the element-wise path)."""
+    from rwkvtune_amd import _lib
+    print(f"[case] activation {dtype}", flush=True)
+    g = torch.Generator(device=gpu_device).manual_seed(11)
+    base = (torch.randn(8 * 1000 + 13, generator=g, device=gpu_device) * 3).to(dtype)
+    refs = {0: torch.tanh, 1: torch.sigmoid, 2: lambda t: torch.relu(t) ** 2}
+    for kind, fn in refs.items():
+        for view in (base.clone(), base.clone()[1:]):
+            exp = fn(view.float()).to(dtype)
+            _lib.call("rwkv7_activation", _lib.dtype_code(dtype), kind, view.numel(), _lib.ptr(view),
+                      _lib.stream_of(view))
+            torch.cuda.synchronize()
+            d = (view.float() - exp.float()).abs()
+            ulp = torch.finfo(dtype).eps * exp.float().abs().clamp_min(torch.finfo(dtype).tiny)
+            assert bool((d <= 2 * ulp + 1e-7).all()), (kind, float(d.max()))
