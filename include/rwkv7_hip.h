@@ -309,6 +309,22 @@ int rwkv7_admit_copy(const int32_t *counters, const int32_t *admit_slot, const i
                      const float *src_kv, const float *src_ax, const float *src_fx,
                      float *dst_kv, float *dst_ax, float *dst_fx, void *stream);
 
+/* ------------------------------------------------------------------------
+ * Log-probabilities of chosen tokens
+ * ------------------------------------------------------------------------ */
+
+/*
+ * out[r] = log_softmax(logits[r, :V])[index[r]] for R rows of logits (row
+ * stride ld >= V, `dtype`), written in the logits' dtype: float32 rows give
+ * x[i] - logsumexp(x); bf16 / fp16 rows give x[i] - lse with lse the float32
+ * logsumexp rounded to the dtype, subtracted and rounded in the dtype.  index is
+ * int64 [R]; an index outside [0, V) gives NaN.  Replaces selective_log_softmax
+ * (rwkvtune/training/grpo/utils.py:13-103) as used by the GRPO log-prob
+ * recompute (grpo/lightning_module.py:1810-1964).
+ */
+int rwkv7_selective_log_softmax(int dtype, int64_t R, int64_t V, const void *logits, int64_t ld,
+                                const int64_t *index, void *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

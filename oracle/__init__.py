@@ -15,6 +15,9 @@ Contents
 ``model``     torch-CPU restatement of ``RWKV7Model.forward_with_state``
               (``rwkvtune/models/rwkv7/model.py:174-520``).
 ``sampler``   restatement of ``TokenSampler`` (``rwkvtune/inference/core.py:16-236``).
+``logprob``   restatement of the GRPO log-prob recompute
+              (``rwkvtune/training/grpo/utils.py:13-103``,
+              ``grpo/lightning_module.py:1810-1964``).
 ``rollout``   restatement of the GRPO rollout loop
               (``rwkvtune/inference/grpo_batch_generator.py:115-748``), used as the
               CPU baseline.

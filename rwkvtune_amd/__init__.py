@@ -1,6 +1,7 @@
 """gfx950 (MI355X) implementation of rwkvtune's batched-generation hot path:
 WKV7 decode / prefill kernels, the RWKV-7 stateful forward, device-side
-sampling and a GPU slot-table rollout engine behind rwkvtune's own front ends.
+sampling and a GPU slot-table rollout engine behind rwkvtune's own front ends,
+and the GRPO log-prob recompute that follows a rollout.
 
 Submodules import lazily so that loading the package needs neither a GPU nor
 the built HIP library; every compute entry point raises if the library is
@@ -10,6 +11,7 @@ missing (there is no CPU fallback).
 __all__ = [
     "GRPOBatchGenerator", "SchedulerCore", "BatchGenerator", "GenerationConfig", "TokenSampler",
     "SamplingParams", "RWKV7Model", "RWKV7Config", "load_wkv_operator", "rwkv7_wkv",
+    "selective_log_softmax", "compute_per_token_logps",
 ]
 
 _LAZY = {
@@ -23,6 +25,8 @@ _LAZY = {
     "RWKV7Config": ("model", "RWKV7Config"),
     "load_wkv_operator": ("operators", "load_wkv_operator"),
     "rwkv7_wkv": ("operators", "rwkv7_wkv"),
+    "selective_log_softmax": ("grpo_utils", "selective_log_softmax"),
+    "compute_per_token_logps": ("grpo_utils", "compute_per_token_logps"),
 }
 
 

@@ -565,3 +565,34 @@ extern "C" int rwkv7_gemm_pack(const void* B, int64_t ldb, int N, int K, void* o
         return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_pack: ldb >= K, ldb %% 8 == 0 and 16-byte aligned buffers required");
     return launch_status(launch_gemm_pack(B, ldb, N, K, out, (hipStream_t)stream), "gemm_pack_kernel");
 }
+
+// ---------------------------------------------------------------------------
+// Selective log-softmax (logprob.hip)
+// ---------------------------------------------------------------------------
+
+template <typename LT>
+hipError_t launch_selective_logsoftmax(int R, int V, const void* logits, int64_t ld, const int64_t* index, void* out,
+                                       hipStream_t st);
+
+extern "C" int rwkv7_selective_log_softmax(int dtype, int64_t R, int64_t V, const void* logits, int64_t ld,
+                                           const int64_t* index, void* out, void* stream) {
+    if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_selective_log_softmax: bad dtype %d", dtype);
+    if (R < 0 || R > kMaxInt || V < 1 || V > kMaxInt || ld < V)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_selective_log_softmax: need 0 <= R, 1 <= V <= ld (R=%lld V=%lld ld=%lld)",
+                    (long long)R, (long long)V, (long long)ld);
+    if (R == 0) return ok();
+    if (!logits || !index || !out) return fail(RWKV7_ERR_INVALID, "rwkv7_selective_log_softmax: null pointer");
+    hipError_t e;
+    switch (dtype) {
+        case RWKV7_DTYPE_F32:
+            e = launch_selective_logsoftmax<float>((int)R, (int)V, logits, ld, index, out, (hipStream_t)stream);
+            break;
+        case RWKV7_DTYPE_F16:
+            e = launch_selective_logsoftmax<f16_t>((int)R, (int)V, logits, ld, index, out, (hipStream_t)stream);
+            break;
+        default:
+            e = launch_selective_logsoftmax<bf16_t>((int)R, (int)V, logits, ld, index, out, (hipStream_t)stream);
+            break;
+    }
+    return launch_status(e, "selective_logsoftmax_kernel");
+}

@@ -637,10 +637,26 @@ class RWKV7Model(nn.Module):
         return logits.view(B, T, -1), new_states
 
     @torch.no_grad()
+    def forward_hidden(self, idx: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+        """ln_out hidden states ``[len(rows), n_embd]`` (model dtype) of a stateless
+        forward over ``idx [B, T]`` from a zero state, for the flat positions
+        ``rows`` (int32, b * T + t): the input of the head in ``forward``."""
+        self._check_device()
+        B, T = idx.shape
+        pool = StatePool(self.config, B, self.device)
+        tokens = idx.to(device=self.device, dtype=torch.int64).reshape(-1).contiguous()
+        slot, last, cu, seq_slot = self._meta_uniform(B, T, self.device)
+        rows = rows.to(device=self.device, dtype=torch.int32).contiguous()
+        return self.forward_pooled(tokens, slot, last, pool, decode=(T == 1), cu_seqlens=cu, seq_slot=seq_slot,
+                                   logit_rows=rows, n_logit_rows=rows.numel(), return_hidden=True)
+
+    @torch.no_grad()
     def forward(self, idx: torch.Tensor, logits_to_keep: Optional[int] = None):
         """Stateless full-sequence logits (``model.py:435-466``), zero initial state."""
         self._check_device()
         B, T = idx.shape
+        if T > self.config.ctx_len:
+            raise AssertionError(f"Sequence length {T} exceeds max length {self.config.ctx_len}")
         pool = StatePool(self.config, B, self.device)
         tokens = idx.to(device=self.device, dtype=torch.int64).reshape(-1).contiguous()
         slot, last, cu, seq_slot = self._meta_uniform(B, T, self.device)
