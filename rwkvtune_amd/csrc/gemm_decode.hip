@@ -95,7 +95,7 @@ struct Tile {
     static constexpr int STAGE = ROWS * 128;      // bytes
     static_assert(NWAVE == 4 || NWAVE == 8 || NWAVE == 16, "4, 8 or 16 waves per block");
     static_assert(KG == 1 || KG == 2 || KG == 4, "K-step groups divide the 4 steps of a stage");
-    static_assert(BN % 64 == 0, "packed weights come in 64-row tiles");
+    static_assert(BN % 32 == 0, "column tiles of 32 or whole 64-row packed tiles");
     static_assert(IPW * 8 * NWAVE == ROWS, "loads split evenly over the waves");
     static_assert(R >= 2 && (R - 2) * IPW < 64, "vmcnt holds at most 63 outstanding loads");
     static_assert(R * STAGE <= 160 * 1024, "LDS");
@@ -167,12 +167,12 @@ __global__ __launch_bounds__(T::THREADS) void gemm_decode_kernel(GemmBatch batch
             kc[i] = 8 * c;
             src[i] = P.A + (int64_t)min(m0 + row, M - 1) * P.lda + kb + 8 * c;
         } else {
-            // B rows rr0 .. rr0 + 7 lie in one 64-row packed tile; tiles past
+            // weight rows n0 + rr0 .. +7 lie in one 64-row packed tile; tiles past
             // the weight (N not a multiple of BN) re-read its last tile
-            const int rr0 = row0 - T::BM;
-            const int t64 = min(ntile * (T::BN / 64) + rr0 / 64, P.n64 - 1);
+            const int wr0 = n0 + row0 - T::BM;
+            const int t64 = min(wr0 / 64, P.n64 - 1);
             kc[i] = -1;
-            src[i] = P.B + ((int64_t)t64 * P.k_tiles + kt0) * (64 * BK) + (rr0 % 64) * BK + lane * 8;
+            src[i] = P.B + ((int64_t)t64 * P.k_tiles + kt0) * (64 * BK) + (wr0 % 64) * BK + lane * 8;
         }
     }
     const bf16_t* zero = reinterpret_cast<const bf16_t*>(g_gemm_zero_chunk);
@@ -218,8 +218,10 @@ __global__ __launch_bounds__(T::THREADS) void gemm_decode_kernel(GemmBatch batch
             }
 #pragma unroll
             for (int b = 0; b < T::NS; ++b) {
-                const int row = wn + 32 * b + lr;  // row of the B part
-                bfr[kk][b] = *reinterpret_cast<const bf16x8_t*>(st + (T::BM + row) * 128 + ((c ^ swz(row)) << 4));
+                // row of the B part; its chunks are swizzled by its row in the packed tile
+                const int row = wn + 32 * b + lr;
+                bfr[kk][b] = *reinterpret_cast<const bf16x8_t*>(st + (T::BM + row) * 128 +
+                                                                 ((c ^ swz((n0 + row) & 63)) << 4));
             }
         }
         __builtin_amdgcn_sched_barrier(0);  // keep the reads ahead of the products
@@ -445,9 +447,14 @@ hipError_t launch_tile(int M, int count, const void* const* A, const void* const
 // Launches aim at 384 blocks (1.5 per CU) by splitting K into ranges of at
 // least 512.
 using TileDecode = Tile<2, 2, 1, 1, 4, 2>;
+// At most 32 rows (the ragged tail of a rollout) every block only streams
+// weights, and a 32 x 32 tile (4 K groups) gives twice the column tiles and
+// half the dead activation rows: ~7% faster there (measured).
+using TileNarrow = Tile<1, 1, 1, 1, 4, 4>;
 constexpr int kTarget = 384, kMinK = 512;
 
 Plan plan_for(int M, int count, const int* N, const int* K) {
+    if (M <= 32) return make_plan(TileNarrow::BM, TileNarrow::BN, M, count, N, K, kTarget, kMinK, 0);
     return make_plan(TileDecode::BM, TileDecode::BN, M, count, N, K, kTarget, kMinK, 0);
 }
 
@@ -465,6 +472,7 @@ hipError_t launch_gemm_decode(int M, int count, const void* const* A, const void
                               const int* epi, float* ws, hipStream_t st)
 {
     const Plan pl = plan_for(M, count, N, K);
+    if (M <= 32) return launch_tile<TileNarrow>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl);
     return launch_tile<TileDecode>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl);
 }
 
