@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of rwkvtune's batched-generation hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|cfg5|decode|prefill|tmix]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|cfg5|decode|prefill|tmix|logprob]
 
 Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a message.
 
@@ -19,6 +19,11 @@ cfg5               rollout on RWKV-7 7.2B (L=32, C=4096, H=64), bf16: 128 random
     prompts, chunked prefill (chunk 256), up to 1024 sampled tokens (temperature 1.0,
     top_p 0.95) with Geometric(mean 600) stops, 128 slots; value = generated
     tokens / wall time of the rollout.  No CPU baseline (7.2B in fp32 on the host).
+logprob            GRPO log-prob recompute after a cfg4 rollout (RWKV-7 1.5B, bf16):
+    512 sequences of 1024 prompt + 512 completion tokens through
+    ``compute_per_token_logps``; a step is one whole batch; value = forward
+    tokens/s; roofline = GEMM flops (block matrices at every position, head at
+    the completion positions) per second against the 2.5 PFLOP/s bf16 peak.
 decode             isolated WKV7 decode kernel at B=256 slots, H=32 (cfg2); a step is
     one launch; value = algorithmic GB/s.
 tmix               the fused decode time-mix kernel alone at the rollout shape (the
@@ -331,6 +336,71 @@ def rollout_cfg5(steps, warmup, dev):
             "ms_per_step": total_s / steps * 1e3, "runs": stats, "prompt_tokens": sum(len(p) for p in prompts)}
 
 
+def logprob_workload(seed=6, B=512, P=1024, C=512, V=65536):
+    g = torch.Generator().manual_seed(seed)
+    prompt = torch.randint(1, MAX_VALID_ID + 1, (B // 8, P), generator=g).repeat_interleave(8, 0)
+    completion = torch.randint(1, MAX_VALID_ID + 1, (B, C), generator=g)
+    return prompt, completion
+
+
+def matrix_macs(model):
+    """Multiply-adds per token of the blocks' matrices (projections, LoRAs, FFN)."""
+    return sum(p.numel() for n, p in model.named_parameters()
+               if p.ndim == 2 and n not in ("emb.weight", "head.weight") and not n.endswith(".r_k"))
+
+
+def logprob_recompute(steps, warmup, dev):
+    """GRPO log-prob recompute after a cfg4-sized rollout: 512 sequences (64 prompts
+    x 8 generations) of 1024 prompt + 512 completion tokens on RWKV-7 1.5B, through
+    ``compute_per_token_logps`` (forward over prompt + completion[:-1] padded to
+    1536, ln_out + head + selective log-softmax at the 512 completion positions)."""
+    from rwkvtune_amd.grpo_utils import compute_per_token_logps
+    from rwkvtune_amd.model import build_model, config_from_preset
+    cfg = config_from_preset("rwkv7-1.5b", ctx_len=2048)
+    log("[bench] building RWKV-7 1.5B (bf16, seeded dense init) ...")
+    model = build_model(cfg, dtype=torch.bfloat16, device=dev, seed=1234)
+    prompt, completion = logprob_workload()
+    prompt, completion = prompt.to(dev), completion.to(dev)
+    B, P = prompt.shape
+    C = completion.shape[1]
+    T = -(-(P + C - 1) // 16) * 16
+    compute_per_token_logps(model, prompt[:16, :64], completion[:16, :16])
+    for i in range(warmup):
+        compute_per_token_logps(model, prompt, completion)
+    torch.cuda.synchronize(dev)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        out = compute_per_token_logps(model, prompt, completion)
+    torch.cuda.synchronize(dev)
+    dt = (time.perf_counter() - t0) / steps
+    assert out.shape == (B, C) and bool(torch.isfinite(out).all())
+    macs = matrix_macs(model)
+    flops = 2.0 * macs * B * T + 2.0 * cfg.n_embd * cfg.vocab_size * B * C
+    log(f"[bench] logprob recompute: {dt:.3f} s per batch, {B * T / dt:.0f} forward tok/s, "
+        f"{flops / dt / 1e12:.0f} TFLOP/s of GEMM work")
+    return model, {"seconds": dt, "tokens": B * T, "value": B * T / dt, "completion_tokens": B * C,
+                   "gemm_TFLOPs": flops / dt / 1e12, "flops": flops, "T": T}
+
+
+def cpu_baseline_logprob(model, P=1024, C=512):
+    """The restated reference recompute (oracle/logprob.py, fp32) for one sequence."""
+    from oracle import logprob as olp
+    from oracle import model as om
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    sd = om.cast_state_dict(model.state_dict(), torch.float32)
+    prompt, completion = logprob_workload()
+    pr, co = prompt[:1, :P], completion[:1, :C]
+    t0 = time.perf_counter()
+    olp.per_token_logps(sd, pr, co, ctx_len=model.config.ctx_len, dtype=torch.float32)
+    dt = time.perf_counter() - t0
+    T = -(-(P + C - 1) // 16) * 16
+    return {"value": T / dt, "unit": "forward tokens/s", "cores": cores, "kind": "port",
+            "sample": f"one sequence of {P} prompt + {C} completion tokens ({T} forward tokens) through the "
+                      f"restated reference recompute (fp32 forward, full logits, selective log-softmax); "
+                      f"{dt:.1f} s"}
+
+
 def cpu_baseline_rollout(model, prompts, paths=256, decode_steps=2):
     """The reference CPU rollout (oracle/: fp32 forward_with_state, batched
     sample_batch rules) on a bounded sample: one prompt prefilled, forked to
@@ -387,7 +457,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="rollout", choices=["rollout", "cfg5", "decode", "prefill", "tmix"])
+    ap.add_argument("--workload", default="rollout", choices=["rollout", "cfg5", "decode", "prefill", "tmix", "logprob"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -463,6 +533,30 @@ def main():
                          "frac": tm["frac"], "traffic": None, "kernel": tm["kernel"] + " at 128 slots, H=64",
                          "us_per_launch": tm["us_per_launch"], "algorithmic_bytes": tm["bytes_per_launch"]},
             "cpu_baseline": None,
+        }
+    elif a.workload == "logprob":
+        steps = 2 if a.steps is None else a.steps
+        warmup = 1 if a.warmup is None else a.warmup
+        model, lp = logprob_recompute(steps, warmup, dev)
+        cpu = None
+        if not a.no_cpu_baseline:
+            log("[bench] cpu baseline (restated reference recompute, one sequence) ...")
+            cpu = cpu_baseline_logprob(model)
+            log(f"[bench] cpu: {cpu['sample']}")
+        out = {
+            "metric": METRIC, "value": lp["value"], "unit": "forward tokens/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": lp["seconds"] * 1e3, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16 weights/activations, fp32 WKV state and log-softmax",
+            "data": "synthetic (random ids, seeded dense random-init weights)",
+            "config": {"workload": "GRPO log-prob recompute after a cfg4 rollout: RWKV7-1.5B, 512 seqs "
+                                   "(64 prompts x 8) of 1024 prompt + 512 completion tokens, padded to "
+                                   f"{lp['T']}", "global_batch": 512, "seq_len": lp["T"],
+                       "parallelism": "none (1 GPU)", "completion_tokens": lp["completion_tokens"]},
+            "roofline": {"bound": "mfma", "achieved": lp["gemm_TFLOPs"], "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": lp["gemm_TFLOPs"] / PEAK_BF16_TFLOPS, "traffic": None,
+                         "kernel": "whole recompute (block GEMMs at every position + head at the completion "
+                                   "positions), per second of wall time", "flops_per_step": lp["flops"]},
+            "cpu_baseline": cpu,
         }
     elif a.workload == "tmix":
         # the roofline kernel alone (for kernel-trace / PMC runs), then a plain copy of
