@@ -151,16 +151,19 @@ __global__ __launch_bounds__(T::THREADS) void gemm_decode_kernel(GemmBatch batch
     const int nst = (kspan + BK - 1) / BK;
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    // Direct loads: load i of wave w fills stage rows 8 (w IPW + i) .. +7, A rows
-    // first.  For an A row, lane L brings logical chunk (L%8) ^ swz(row) of row
-    // 8 (w IPW + i) + L/8 to LDS position L%8 of that row; a B load is a linear
-    // 1 KB piece of the packed tile, which holds the same arrangement.
+    // Direct loads: load i of wave w fills stage rows 8 (i NWAVE + w) .. +7, A rows
+    // first, so the activation and the weight loads are spread over all the
+    // waves (with BM = BN every wave issues one of each per stage, which streams
+    // ~10% faster than giving the two halves to separate waves).  For an A row,
+    // lane L brings logical chunk (L%8) ^ swz(row) of row 8 (i NWAVE + w) + L/8 to
+    // LDS position L%8 of that row; a B load is a linear 1 KB piece of the packed
+    // tile, which holds the same arrangement.
     const bf16_t* src[T::IPW];
     int kc[T::IPW];  // k offset of the lane's A chunk within a stage (-1: B load)
     const int kt0 = kb / BK;
 #pragma unroll
     for (int i = 0; i < T::IPW; ++i) {
-        const int row0 = 8 * (wave * T::IPW + i);
+        const int row0 = 8 * (i * T::NWAVE + wave);
         if (row0 < T::BM) {
             const int row = row0 + (lane >> 3);
             const int c = (lane & 7) ^ swz(row);
@@ -176,21 +179,20 @@ __global__ __launch_bounds__(T::THREADS) void gemm_decode_kernel(GemmBatch batch
         }
     }
     const bf16_t* zero = reinterpret_cast<const bf16_t*>(g_gemm_zero_chunk);
-    // A wave whose stage rows all lie in the A part past the last real row
-    // issues nothing: those rows feed only outputs that are never stored, so
-    // their LDS can hold anything.  (Its waits then pass at once.)
-    const bool idle = 8 * (wave + 1) * T::IPW <= T::BM && m0 + 8 * wave * T::IPW >= M;
+    // An A load whose 8 rows all lie past the last real row reads the zero page
+    // (an L2 hit): those rows feed only outputs that are never stored.  Every
+    // wave issues IPW loads per stage, which the waits below count on.
     auto issue = [&](int s) {
-        if (idle) return;
-        uint8_t* dst = ring + (s % T::R) * T::STAGE + wave * T::IPW * 8 * 128;
+        uint8_t* dst = ring + (s % T::R) * T::STAGE;
 #pragma unroll
         for (int i = 0; i < T::IPW; ++i) {
+            const int row0 = 8 * (i * T::NWAVE + wave);  // wave-uniform
             const bf16_t* g;
-            if (8 * (wave * T::IPW + i) >= T::BM)  // wave-uniform
+            if (row0 >= T::BM)
                 g = src[i] + s * (64 * BK);
             else
-                g = (s * BK + kc[i] < kspan) ? src[i] + s * BK : zero;
-            __builtin_amdgcn_global_load_lds(g, dst + i * 8 * 128, 16, 0, 0);
+                g = (m0 + row0 < M && s * BK + kc[i] < kspan) ? src[i] + s * BK : zero;
+            __builtin_amdgcn_global_load_lds(g, dst + row0 * 128, 16, 0, 0);
         }
     };
 
