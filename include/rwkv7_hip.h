@@ -113,7 +113,12 @@ int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t total_tokens,
 /*
  * Residual source + LayerNorm + token shift + lerps.  The residual of row m is
  * emb[tokens[m]] (tokens non-null) or x_in[m] (+ add[m] when add is non-null),
- * then ln0 when ln0_w is non-null; it is written to x_out (nullable, float32
+ * then ln0 when ln0_w is non-null.  add_parts = 0: add is [M, C] in the I/O
+ * dtype.  add_parts = P >= 1 (not with tokens): add is float32 partial sums,
+ * plane q at add + q * add_part_stride floats (16-byte aligned, stride a multiple
+ * of 4 and >= M * C), and add[m] is the in-order sum of the P planes' row m
+ * rounded to the I/O dtype - the output of rwkv7_gemm_decode_partials, which
+ * this consumes in place of the split-K reduction; it is written to x_out (nullable, float32
  * [M, C]).  h = LayerNorm(residual; ln_w, ln_b, eps 1e-5); h_prev is the previous
  * row's h, or prev_pool[slot] on a sequence's first row; out[j][m] =
  * h + (h_prev - h) * mix[j] for j < n_mix (out: [n_mix, M, C]).  The sequence's
@@ -122,17 +127,19 @@ int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t total_tokens,
  * (att_x_prev), and with n_mix = 1 model.py:406-407, 315-321 (ln2, FFN shift).
  */
 int rwkv7_shift_mix(int dtype, int64_t M, int64_t C, const float *x_in, const void *add,
+                    int add_parts, int64_t add_part_stride,
                     const int64_t *tokens, const void *emb, int64_t vocab,
                     const float *ln0_w, const float *ln0_b, float *x_out,
                     const float *ln_w, const float *ln_b, float *prev_pool,
                     int64_t pool_slots, const int32_t *row_slot, const int32_t *row_last,
                     int n_mix, const float *mix, void *out, void *stream);
 
-/* out[n] = LayerNorm(x_in[rows[n]] + add[rows[n]]) (rows NULL: row n; add nullable).
+/* out[n] = LayerNorm(x_in[rows[n]] + add[rows[n]]) (rows NULL: row n; add nullable;
+ * add_parts / add_part_stride as for rwkv7_shift_mix, stride >= C).
  * Replaces ln_out (model.py:494) restricted to the rows whose logits are used. */
 int rwkv7_final_norm(int dtype, int64_t n, int64_t C, const float *x_in, const void *add,
-                     const int32_t *rows, const float *ln_w, const float *ln_b, void *out,
-                     void *stream);
+                     int add_parts, int64_t add_part_stride, const int32_t *rows,
+                     const float *ln_w, const float *ln_b, void *out, void *stream);
 
 /* In-place element-wise activation of n elements: kind 0 = tanh (decay LoRA,
  * model.py:211), 1 = sigmoid (gate LoRA, model.py:221), 2 = relu(x)^2 (FFN,
@@ -182,7 +189,7 @@ int rwkv7_tmix_decode(int dtype, int64_t M, int64_t H, int layer0, const void *r
  * accumulation.  epi: 0 none, 1 relu(x)^2, 2 tanh, 3 sigmoid.  K_i % 8 == 0,
  * lda_i % 8 == 0 and >= K_i, A_i and B_i 16-byte aligned.  The pointer and
  * size arrays are host arrays of `count` entries.  Problems whose K is split
- * across blocks write float32 partial tiles to `workspace` (contents need no
+ * across blocks write float32 partial rows to `workspace` (contents need no
  * initialisation) and a second launch on `stream` reduces them;
  * rwkv7_gemm_decode_workspace gives the floats a problem set needs (-1 on
  * invalid sizes).  Calls that share a workspace must not overlap.  Replaces
@@ -194,6 +201,21 @@ int rwkv7_gemm_decode(int64_t M, int count, const void *const *A, const void *co
                       void *const *C, const int64_t *lda, const int64_t *ldc,
                       const int *N, const int *K, const int *epi,
                       float *workspace, int64_t workspace_floats, void *stream);
+
+/*
+ * One problem of rwkv7_gemm_decode (epi 0) without its reduction: the products
+ * of the plan's P = rwkv7_gemm_decode_partial_count(M, N, K) K ranges are left in
+ * `workspace` as float32 planes [P][M][N] (16-byte aligned, P * M * N floats),
+ * and *parts (host) receives P (also when P = 1).  Their in-order sum rounded to
+ * bf16 equals rwkv7_gemm_decode's C; rwkv7_shift_mix / rwkv7_final_norm take the
+ * planes directly (add_parts = P, add_part_stride = M * N), which saves the
+ * reduction launch.  For the FFN value projection (model.py:338) ahead of the
+ * next layer's residual add.  partial_count returns -1 on invalid sizes.
+ */
+int rwkv7_gemm_decode_partial_count(int64_t M, int N, int K);
+int rwkv7_gemm_decode_partials(int64_t M, const void *A, const void *B, int64_t lda, int N, int K,
+                               float *workspace, int64_t workspace_floats, int32_t *parts,
+                               void *stream);
 
 /*
  * Weight packing for rwkv7_gemm_decode: B [N][K] bf16 (row stride ldb, a

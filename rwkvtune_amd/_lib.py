@@ -32,9 +32,9 @@ SIGNATURES = {
     "rwkv7s_forward": (_I32, [_I32, _I64, _I64, _I64, _I64] + [_P] * 8 + [_P]),
     "rwkv7_wkv_decode": (_I32, [_I32, _I64, _I64, _P, _I64, _P] + [_P] * 7 + [_P]),
     "rwkv7_wkv_prefill": (_I32, [_I32, _I64, _I64, _I64, _P, _P, _P, _I64] + [_P] * 7 + [_I32, _P]),
-    "rwkv7_shift_mix": (_I32, [_I32, _I64, _I64, _P, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _I64,
-                               _P, _P, _I32, _P, _P, _P]),
-    "rwkv7_final_norm": (_I32, [_I32, _I64, _I64, _P, _P, _P, _P, _P, _P, _P]),
+    "rwkv7_shift_mix": (_I32, [_I32, _I64, _I64, _P, _P, _I32, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P,
+                               _I64, _P, _P, _I32, _P, _P, _P]),
+    "rwkv7_final_norm": (_I32, [_I32, _I64, _I64, _P, _P, _I32, _I64, _P, _P, _P, _P, _P]),
     "rwkv7_activation": (_I32, [_I32, _I32, _I64, _P, _P]),
     "rwkv7_tmix_prep": (_I32, [_I32, _I64, _I64, _I32] + [_P] * 6 + [_P, _P, _P, _P]),
     "rwkv7_tmix_post": (_I32, [_I32, _I64, _I64] + [_P] * 5 + [_P, _P, _P]),
@@ -48,6 +48,8 @@ SIGNATURES = {
     "rwkv7_admit_copy": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64] + [_P] * 6 + [_P]),
     "rwkv7_gemm_decode_workspace": (_I64, [_I64, _I32, _P, _P]),
     "rwkv7_gemm_decode": (_I32, [_I64, _I32] + [_P] * 8 + [_P, _I64, _P]),
+    "rwkv7_gemm_decode_partial_count": (_I32, [_I64, _I32, _I32]),
+    "rwkv7_gemm_decode_partials": (_I32, [_I64, _P, _P, _I64, _I32, _I32, _P, _I64, _P, _P]),
     "rwkv7_gemm_packed_elems": (_I64, [_I32, _I32]),
     "rwkv7_gemm_pack": (_I32, [_P, _I64, _I32, _I32, _P, _P]),
     "rwkv7_selective_log_softmax": (_I32, [_I32, _I64, _I64, _P, _I64, _P, _P, _P]),

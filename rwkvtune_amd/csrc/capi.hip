@@ -179,14 +179,14 @@ extern "C" int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t tot
 // ---------------------------------------------------------------------------
 
 template <typename IO>
-hipError_t launch_shift_mix(int M, int C, const float* x_in, const void* add, const int64_t* tokens,
-                            const void* emb, int64_t vocab, const float* ln0_w, const float* ln0_b,
-                            float* x_out, const float* ln_w, const float* ln_b, float* prev_pool,
-                            int pool_slots, const int32_t* row_slot, const int32_t* row_last,
+hipError_t launch_shift_mix(int M, int C, const float* x_in, const void* add, int add_parts, int64_t part_stride,
+                            const int64_t* tokens, const void* emb, int64_t vocab, const float* ln0_w,
+                            const float* ln0_b, float* x_out, const float* ln_w, const float* ln_b,
+                            float* prev_pool, int pool_slots, const int32_t* row_slot, const int32_t* row_last,
                             int n_mix, const float* mix, void* out, hipStream_t st);
 template <typename IO>
-hipError_t launch_final_norm(int n, int C, const float* x_in, const void* add, const int32_t* rows,
-                             const float* ln_w, const float* ln_b, void* out, hipStream_t st);
+hipError_t launch_final_norm(int n, int C, const float* x_in, const void* add, int add_parts, int64_t part_stride,
+                             const int32_t* rows, const float* ln_w, const float* ln_b, void* out, hipStream_t st);
 template <typename IO>
 hipError_t launch_activation(int kind, int64_t n, void* x, hipStream_t st);
 template <typename IO>
@@ -214,9 +214,18 @@ namespace {
 constexpr int64_t kMaxC = 8000;  // two fp32 rows of LDS per block
 bool bad_c(int64_t C) { return C <= 0 || C > kMaxC; }
 bool bad_h(int64_t H) { return H <= 0 || (H % 4) != 0 || H * RWKV7_HEAD > kMaxC; }
+constexpr int kMaxAddParts = 64;
+// add_parts > 0: `add` is float32 partial sums, 16-byte aligned, planes
+// part_stride floats apart (a multiple of 4, at least min_stride)
+bool bad_parts(int add_parts, const void* add, int64_t part_stride, int64_t min_stride) {
+    if (add_parts == 0) return false;
+    return add_parts < 0 || add_parts > kMaxAddParts || add == nullptr || (((uintptr_t)add) & 15) != 0 ||
+           (add_parts > 1 && (part_stride < min_stride || (part_stride % 4) != 0));
+}
 }  // namespace
 
 extern "C" int rwkv7_shift_mix(int dtype, int64_t M, int64_t C, const float* x_in, const void* add,
+                               int add_parts, int64_t add_part_stride,
                                const int64_t* tokens, const void* emb, int64_t vocab,
                                const float* ln0_w, const float* ln0_b, float* x_out,
                                const float* ln_w, const float* ln_b, float* prev_pool,
@@ -237,22 +246,31 @@ extern "C" int rwkv7_shift_mix(int dtype, int64_t M, int64_t C, const float* x_i
         return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: ln0 weight and bias go together");
     if (!ln_w || !ln_b || !prev_pool || !row_slot || !row_last || !mix || !out)
         return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: null pointer");
+    if (bad_parts(add_parts, add, add_part_stride, M * C) || (add_parts > 0 && tokens != nullptr))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_shift_mix: bad partial sums (parts=%d stride=%lld; 1..%d planes of "
+                    "M x C floats, 16-byte aligned, not with tokens)", add_parts, (long long)add_part_stride,
+                    kMaxAddParts);
     hipError_t e;
-    RWKV7_DISPATCH(dtype, (launch_shift_mix<IO>((int)M, (int)C, x_in, add, tokens, emb, vocab, ln0_w, ln0_b,
+    RWKV7_DISPATCH(dtype, (launch_shift_mix<IO>((int)M, (int)C, x_in, add, add_parts, add_part_stride, tokens,
+                                                emb, vocab, ln0_w, ln0_b,
                                                 x_out, ln_w, ln_b, prev_pool, (int)pool_slots, row_slot,
                                                 row_last, n_mix, mix, out, (hipStream_t)stream)));
     return launch_status(e, "shift_mix_kernel");
 }
 
 extern "C" int rwkv7_final_norm(int dtype, int64_t n, int64_t C, const float* x_in, const void* add,
-                                const int32_t* rows, const float* ln_w, const float* ln_b, void* out,
-                                void* stream) {
+                                int add_parts, int64_t add_part_stride, const int32_t* rows,
+                                const float* ln_w, const float* ln_b, void* out, void* stream) {
     if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_final_norm: bad dtype code %d", dtype);
     if (n < 0 || bad_c(C) || (C % 4) != 0 || n > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_final_norm: bad sizes");
     if (n == 0) return ok();
     if (!x_in || !ln_w || !ln_b || !out) return fail(RWKV7_ERR_INVALID, "rwkv7_final_norm: null pointer");
+    if (bad_parts(add_parts, add, add_part_stride, C))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_final_norm: bad partial sums (parts=%d stride=%lld)", add_parts,
+                    (long long)add_part_stride);
     hipError_t e;
-    RWKV7_DISPATCH(dtype, (launch_final_norm<IO>((int)n, (int)C, x_in, add, rows, ln_w, ln_b, out,
+    RWKV7_DISPATCH(dtype, (launch_final_norm<IO>((int)n, (int)C, x_in, add, add_parts, add_part_stride, rows,
+                                                 ln_w, ln_b, out,
                                                  (hipStream_t)stream)));
     return launch_status(e, "final_norm_kernel");
 }
@@ -503,6 +521,9 @@ int gemm_decode_max_problems();
 int64_t gemm_decode_workspace(int M, int count, const int* N, const int* K);
 int64_t gemm_packed_elems(int N, int K);
 hipError_t launch_gemm_pack(const void* B, int64_t ldb, int N, int K, void* out, hipStream_t st);
+int gemm_decode_partial_splits(int M, int N, int K);
+hipError_t launch_gemm_decode_partials(int M, const void* A, const void* B, int64_t lda, int N, int K, float* ws,
+                                       hipStream_t st);
 namespace {
 int check_gemm_problems(const char* fn, int64_t M, int count, const int* N, const int* K) {
     if (count < 1 || count > gemm_decode_max_problems())
@@ -546,6 +567,36 @@ extern "C" int rwkv7_gemm_decode(int64_t M, int count, const void* const* A, con
                     (long long)need_ws, (long long)workspace_floats);
     return launch_status(launch_gemm_decode((int)M, count, A, B, C, lda, ldc, N, K, epi, workspace,
                                             (hipStream_t)stream),
+                         "gemm_decode_kernel");
+}
+
+extern "C" int rwkv7_gemm_decode_partial_count(int64_t M, int N, int K) {
+    if (check_gemm_problems("rwkv7_gemm_decode_partial_count", M, 1, &N, &K) != RWKV7_OK) return -1;
+    ok();
+    return gemm_decode_partial_splits((int)(M > 0 ? M : 1), N, K);
+}
+
+extern "C" int rwkv7_gemm_decode_partials(int64_t M, const void* A, const void* B, int64_t lda, int N, int K,
+                                          float* workspace, int64_t workspace_floats, int32_t* parts,
+                                          void* stream) {
+    if (check_gemm_problems("rwkv7_gemm_decode_partials", M, 1, &N, &K) != RWKV7_OK) return RWKV7_ERR_INVALID;
+    if (!parts) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode_partials: null parts");
+    const int np = gemm_decode_partial_splits((int)(M > 0 ? M : 1), N, K);
+    *parts = np;
+    if (M == 0) return ok();
+    if (!A || !B) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode_partials: null pointer");
+    if (lda < K || (lda % 8) != 0)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode_partials: lda >= K and lda %% 8 == 0 required");
+    if ((((uintptr_t)A) | ((uintptr_t)B) | ((uintptr_t)workspace)) & 15)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode_partials: A, packed B and the workspace must be 16-byte "
+                    "aligned");
+    if (((M + 31) / 32) * (int64_t)((N + 63) / 64 + 7) * 8 * np > kMaxInt)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode_partials: too many tiles");
+    const int64_t need_ws = (int64_t)np * M * N;
+    if (workspace == nullptr || workspace_floats < need_ws)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode_partials: needs a workspace of %lld floats (have %lld)",
+                    (long long)need_ws, (long long)workspace_floats);
+    return launch_status(launch_gemm_decode_partials((int)M, A, B, lda, N, K, workspace, (hipStream_t)stream),
                          "gemm_decode_kernel");
 }
 

@@ -39,9 +39,10 @@
 //   * blocks are ordered so that the row tiles and K ranges of one column tile
 //     run back to back on one XCD (blocks are dealt to the 8 XCDs round-robin),
 //     where they share the weight rows through that XCD's L2;
-//   * problems with too few tiles to fill the GPU split K; each range writes a
-//     float32 partial tile to the caller's workspace and gemm_reduce_kernel sums
-//     the ranges in order (deterministic) and applies the epilogue.
+//   * problems with too few tiles to fill the GPU split K; each range writes
+//     float32 partial rows to the caller's workspace and gemm_reduce_kernel sums
+//     the ranges in order (deterministic) and applies the epilogue - or, for
+//     launch_gemm_decode_partials, the consumer of the result does.
 // MFMA operand layout (gfx950): lane l supplies row l%32 of A and of B, k =
 // 8*(l/32) .. +7; accumulator q of lane l is C[8*(q/4) + 4*(l/32) + q%4][l%32].
 #include "common.hpp"
@@ -72,13 +73,14 @@ struct GemmProblem {
     int splits;       // K ranges
     int k_per;        // K per range (multiple of BK)
     int red_begin;    // first block of this problem in gemm_reduce_kernel
+    int partial;      // 1: write float32 partials even when splits == 1 (no epilogue)
 };
 
 struct GemmBatch {
     GemmProblem p[kMaxProblems];
     int count;
     int M;
-    int bm, bn;       // tile of the launch (read by gemm_reduce_kernel)
+    int bm, bn;       // tile of the launch
 };
 
 // Block tile: WM x WN x KG waves, each wave MS x NS MFMA tiles of 32 x 32 over
@@ -285,7 +287,7 @@ __global__ __launch_bounds__(T::THREADS) void gemm_decode_kernel(GemmBatch batch
         }
     }
 
-    if (P.splits == 1) {
+    if (P.splits == 1 && !P.partial) {
 #pragma unroll
         for (int a = 0; a < T::MS; ++a)
 #pragma unroll
@@ -300,44 +302,49 @@ __global__ __launch_bounds__(T::THREADS) void gemm_decode_kernel(GemmBatch batch
             }
         return;
     }
-    // split-K: publish this range's partial tile; gemm_reduce_kernel, launched
-    // next on the same stream, sums the ranges (a kernel boundary is what makes
-    // another block's writes visible: the L2 of each XCD is private)
-    const int tile = mtile * P.n_tiles + ntile;
-    const int ntiles = mt * P.n_tiles;
-    float* part = ws + P.ws_off + ((int64_t)split * ntiles + tile) * (T::BM * T::BN);
+    // split-K: publish this range's partial products as rows of the float32
+    // [splits][M][N] array at the problem's workspace offset; gemm_reduce_kernel,
+    // launched next on the same stream, or the consumer of the partials sums
+    // the ranges in order (a kernel boundary is what makes another block's
+    // writes visible: the L2 of each XCD is private)
+    float* part = ws + P.ws_off + (int64_t)split * M * P.N;
 #pragma unroll
     for (int a = 0; a < T::MS; ++a)
 #pragma unroll
-        for (int b = 0; b < T::NS; ++b)
+        for (int b = 0; b < T::NS; ++b) {
+            const int col = n0 + wn + 32 * b + lr;
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-                const int rr = wm + 32 * a + 8 * (q >> 2) + 4 * hi + (q & 3);
-                part[rr * T::BN + wn + 32 * b + lr] = acc[a][b][q];
+                const int row = m0 + wm + 32 * a + 8 * (q >> 2) + 4 * hi + (q & 3);
+                if (row < M && col < P.N) part[(int64_t)row * P.N + col] = acc[a][b][q];
             }
+        }
 }
 
-// Sum the split-K partial tiles in split order (deterministic), apply the
-// epilogue and write bf16.  Thread e of problem p covers 4 consecutive
-// elements of one partial tile; red_begin is the problem's first block here.
+// Sum the split-K partials in split order (deterministic), apply the epilogue
+// and write bf16.  Thread e of problem p covers 4 consecutive elements of the
+// problem's [M][N] partial rows; red_begin is the problem's first block here.
 __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmBatch batch, const float* __restrict__ ws) {
     const GemmProblem P = select_problem(batch, blockIdx.x, true);
-    const int M = batch.M, BM = batch.bm, BN = batch.bn;
-    const int mt = (M + BM - 1) / BM;
-    const int ntiles = mt * P.n_tiles;
-    const int elems = BM * BN;
+    const int M = batch.M;
+    const int64_t total = (int64_t)M * P.N;
     const int64_t e = ((int64_t)(blockIdx.x - P.red_begin) * 256 + threadIdx.x) * 4;
-    if (P.splits <= 1 || e >= (int64_t)ntiles * elems) return;
-    const int tile = (int)(e / elems), te = (int)(e % elems);
-    const int row = (tile / P.n_tiles) * BM + te / BN, col = (tile % P.n_tiles) * BN + te % BN;
-    if (row >= M) return;
+    if (P.splits <= 1 || e >= total) return;
     const float* base = ws + P.ws_off + e;
-    const int64_t stride = (int64_t)ntiles * elems;
-    f32x4 v = *reinterpret_cast<const f32x4*>(base);
-    for (int s = 1; s < P.splits; ++s) v += *reinterpret_cast<const f32x4*>(base + s * stride);
+    if ((P.N & 3) == 0) {  // 4 elements of one row
+        f32x4 v = *reinterpret_cast<const f32x4*>(base);
+        for (int s = 1; s < P.splits; ++s) v += *reinterpret_cast<const f32x4*>(base + s * total);
+        const int row = (int)(e / P.N), col = (int)(e % P.N);
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-        if (col + c < P.N) P.C[(int64_t)row * P.ldc + col + c] = f32_to_bf16(epi_fn(P.epi, v[c]));
+        for (int c = 0; c < 4; ++c) P.C[(int64_t)row * P.ldc + col + c] = f32_to_bf16(epi_fn(P.epi, v[c]));
+        return;
+    }
+    for (int c = 0; c < 4 && e + c < total; ++c) {
+        float v = base[c];
+        for (int s = 1; s < P.splits; ++s) v += base[c + s * total];
+        const int row = (int)((e + c) / P.N), col = (int)((e + c) % P.N);
+        P.C[(int64_t)row * P.ldc + col] = f32_to_bf16(epi_fn(P.epi, v));
+    }
 }
 
 // Pack an nn.Linear weight B [N][K] (row stride ldb) into 64 x 64 tiles: tile
@@ -391,8 +398,8 @@ Plan make_plan(int bm, int bn, int M, int count, const int* N, const int* K, int
         pl.k_per[i] = kp;
         pl.blocks += 8 * ((n_tiles + 7) / 8) * mt * si;
         if (si > 1) {
-            pl.ws_floats += (int64_t)si * nt * bm * bn;
-            pl.red_tiles += (int)((nt * bm * bn / 4 + 255) / 256);
+            pl.ws_floats += (int64_t)si * M * N[i];
+            pl.red_tiles += (int)((((int64_t)M * N[i] + 3) / 4 + 255) / 256);
         }
     }
     return pl;
@@ -401,7 +408,7 @@ Plan make_plan(int bm, int bn, int M, int count, const int* N, const int* K, int
 template <class T>
 hipError_t launch_tile(int M, int count, const void* const* A, const void* const* B, void* const* C,
                        const int64_t* lda, const int64_t* ldc, const int* N, const int* K,
-                       const int* epi, float* ws, hipStream_t st, const Plan& pl) {
+                       const int* epi, float* ws, hipStream_t st, const Plan& pl, int partial = 0) {
     GemmBatch b{};
     b.count = count;
     b.M = M;
@@ -429,15 +436,15 @@ hipError_t launch_tile(int M, int count, const void* const* A, const void* const
         p.ws_off = ws_off;
         p.red_begin = red;
         blocks += 8 * ((p.n_tiles + 7) / 8) * mt * p.splits;
-        const int nt = mt * p.n_tiles;
-        if (p.splits > 1) {
-            ws_off += (int64_t)p.splits * nt * T::BM * T::BN;
-            red += (nt * T::BM * T::BN / 4 + 255) / 256;
+        p.partial = partial;
+        if (p.splits > 1 || partial) {
+            ws_off += (int64_t)p.splits * M * N[i];
+            if (!partial) red += (int)((((int64_t)M * N[i] + 3) / 4 + 255) / 256);
         }
     }
     hipLaunchKernelGGL((gemm_decode_kernel<T>), dim3(blocks), dim3(T::THREADS), 0, st, b, ws);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || red == 0) return e;
+    if (e != hipSuccess || red == 0 || partial) return e;
     hipLaunchKernelGGL(gemm_reduce_kernel, dim3(red), dim3(256), 0, st, b, (const float*)ws);
     return hipGetLastError();
 }
@@ -476,6 +483,23 @@ hipError_t launch_gemm_decode(int M, int count, const void* const* A, const void
     const Plan pl = plan_for(M, count, N, K);
     if (M <= 32) return launch_tile<TileNarrow>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl);
     return launch_tile<TileDecode>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl);
+}
+
+// One problem, its K-range partial products left as float32 [splits][M][N] rows
+// at the start of ws (no epilogue, no reduction pass; one range when the plan
+// does not split).  Their in-order sum rounded to bf16 is what
+// launch_gemm_decode writes with epi 0.
+int gemm_decode_partial_splits(int M, int N, int K) { return plan_for(M, 1, &N, &K).splits[0]; }
+
+hipError_t launch_gemm_decode_partials(int M, const void* A, const void* B, int64_t lda, int N, int K, float* ws,
+                                       hipStream_t st)
+{
+    const Plan pl = plan_for(M, 1, &N, &K);
+    void* C = nullptr;
+    const int64_t ldc = N;
+    const int epi = 0;
+    if (M <= 32) return launch_tile<TileNarrow>(M, 1, &A, &B, &C, &lda, &ldc, &N, &K, &epi, ws, st, pl, 1);
+    return launch_tile<TileDecode>(M, 1, &A, &B, &C, &lda, &ldc, &N, &K, &epi, ws, st, pl, 1);
 }
 
 int64_t gemm_packed_elems(int N, int K) { return (int64_t)((N + 63) / 64) * 64 * ((K + BK - 1) / BK) * BK; }

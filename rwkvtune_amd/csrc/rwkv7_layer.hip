@@ -65,6 +65,9 @@ struct ResidualSrc {
     int64_t vocab;
     const float* ln0_w;     // nullable: apply ln0 after the lookup / add
     const float* ln0_b;
+    const float* parts;     // instead of add: float32 partial sums [n_parts][rows][C], nullable
+    int n_parts;
+    int64_t part_stride;    // floats between consecutive partial planes
 };
 
 // ---------------------------------------------------------------------------
@@ -97,6 +100,23 @@ template <> struct vec4io<f16_t> {
         *reinterpret_cast<h4*>(p) = h;
     }
 };
+
+// the branch output added to the residual at (row, chunk c): the I/O-dtype
+// tensor, or the in-order sum of the float32 partials rounded to the I/O dtype
+// (what the split-K reduction would have stored)
+template <typename IO>
+__device__ __forceinline__ f32x4 add_term(const ResidualSrc<IO>& src, int64_t row, int C, int c) {
+    if (src.parts != nullptr) {
+        const float* p = src.parts + row * C + 4 * c;
+        f32x4 v = *reinterpret_cast<const f32x4*>(p);
+        for (int q = 1; q < src.n_parts; ++q) v += *reinterpret_cast<const f32x4*>(p + q * src.part_stride);
+        if constexpr (sizeof(IO) == 4) return v;
+        IO t[4];
+        vec4io<IO>::store(t, v);
+        return vec4io<IO>::load(t);
+    }
+    return vec4io<IO>::load(src.add + row * C + 4 * c);
+}
 
 // two sums over a TH-thread block at once (LDS red: 2 * TH / 64 floats)
 template <int TH>
@@ -140,13 +160,13 @@ __device__ __forceinline__ void load_row(const ResidualSrc<IO>& src, int m, int 
         }
     } else {
         const float* x = src.x_in + (size_t)m * C4 * 4;
-        const IO* ad = src.add != nullptr ? src.add + (size_t)m * C4 * 4 : nullptr;
+        const bool has_add = src.add != nullptr || src.parts != nullptr;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = t + j * TH;
             f32x4 z = {0.f, 0.f, 0.f, 0.f};
             f32x4 a = (c < C4) ? *reinterpret_cast<const f32x4*>(x + 4 * c) : z;
-            if (ad != nullptr && c < C4) a += vec4io<IO>::load(ad + 4 * c);
+            if (has_add && c < C4) a += add_term(src, m, 4 * C4, c);
             r.v[j] = a;
         }
     }
@@ -237,7 +257,7 @@ __global__ __launch_bounds__(TH) void shift_mix_kernel(
         if (c >= C4) return z;
         if (src.tokens != nullptr) return e != nullptr ? vec4io<IO>::load(e + 4 * c) : z;
         f32x4 a = *reinterpret_cast<const f32x4*>(src.x_in + (size_t)row * C + 4 * c);
-        if (src.add != nullptr) a += vec4io<IO>::load(src.add + (size_t)row * C + 4 * c);
+        if (src.add != nullptr || src.parts != nullptr) a += add_term(src, row, C, c);
         return a;
     };
 
@@ -619,13 +639,14 @@ static int row_threads(int C) {
 
 // n_mix in {1, 6, 7}; C a multiple of 4 and at most 8 * 1024
 template <typename IO>
-hipError_t launch_shift_mix(int M, int C, const float* x_in, const void* add, const int64_t* tokens,
-                            const void* emb, int64_t vocab, const float* ln0_w, const float* ln0_b,
-                            float* x_out, const float* ln_w, const float* ln_b, float* prev_pool,
-                            int pool_slots, const int32_t* row_slot, const int32_t* row_last,
+hipError_t launch_shift_mix(int M, int C, const float* x_in, const void* add, int add_parts, int64_t part_stride,
+                            const int64_t* tokens, const void* emb, int64_t vocab, const float* ln0_w,
+                            const float* ln0_b, float* x_out, const float* ln_w, const float* ln_b,
+                            float* prev_pool, int pool_slots, const int32_t* row_slot, const int32_t* row_last,
                             int n_mix, const float* mix, void* out, hipStream_t st)
 {
-    ResidualSrc<IO> src{x_in, (const IO*)add, tokens, (const IO*)emb, vocab, ln0_w, ln0_b};
+    ResidualSrc<IO> src{x_in, add_parts > 0 ? nullptr : (const IO*)add, tokens, (const IO*)emb, vocab, ln0_w,
+                        ln0_b, add_parts > 0 ? (const float*)add : nullptr, add_parts, part_stride};
 #define RWKV7_SM(NVV, THH) return launch_shift_mix_nv<IO, NVV, THH>(M, C, src, x_out, ln_w, ln_b, prev_pool, \
                                                                   pool_slots, row_slot, row_last, n_mix, mix, out, st);
     RWKV7_ROW_DISPATCH(RWKV7_SM)
@@ -633,10 +654,11 @@ hipError_t launch_shift_mix(int M, int C, const float* x_in, const void* add, co
 }
 
 template <typename IO>
-hipError_t launch_final_norm(int n, int C, const float* x_in, const void* add, const int32_t* rows,
-                             const float* ln_w, const float* ln_b, void* out, hipStream_t st)
+hipError_t launch_final_norm(int n, int C, const float* x_in, const void* add, int add_parts, int64_t part_stride,
+                             const int32_t* rows, const float* ln_w, const float* ln_b, void* out, hipStream_t st)
 {
-    ResidualSrc<IO> src{x_in, (const IO*)add, nullptr, nullptr, 0, nullptr, nullptr};
+    ResidualSrc<IO> src{x_in, add_parts > 0 ? nullptr : (const IO*)add, nullptr, nullptr, 0, nullptr, nullptr,
+                        add_parts > 0 ? (const float*)add : nullptr, add_parts, part_stride};
 #define RWKV7_FN(NVV, THH) { hipLaunchKernelGGL((final_norm_kernel<IO, NVV, THH>), dim3(n), dim3(THH), 0, st, C, src, \
                                                 rows, ln_w, ln_b, (IO*)out); return hipGetLastError(); }
     RWKV7_ROW_DISPATCH(RWKV7_FN)
@@ -694,13 +716,14 @@ hipError_t launch_tmix_decode(int M, int H, int layer0, const void* r, const voi
 }
 
 #define RWKV7_INST_LAYER(IO)                                                                        \
-    template hipError_t launch_shift_mix<IO>(int, int, const float*, const void*, const int64_t*,  \
-                                             const void*, int64_t, const float*, const float*,     \
-                                             float*, const float*, const float*, float*, int,      \
-                                             const int32_t*, const int32_t*, int, const float*,    \
-                                             void*, hipStream_t);                                  \
-    template hipError_t launch_final_norm<IO>(int, int, const float*, const void*, const int32_t*, \
-                                              const float*, const float*, void*, hipStream_t);     \
+    template hipError_t launch_shift_mix<IO>(int, int, const float*, const void*, int, int64_t,    \
+                                             const int64_t*, const void*, int64_t, const float*,   \
+                                             const float*, float*, const float*, const float*,     \
+                                             float*, int, const int32_t*, const int32_t*, int,     \
+                                             const float*, void*, hipStream_t);                    \
+    template hipError_t launch_final_norm<IO>(int, int, const float*, const void*, int, int64_t,   \
+                                              const int32_t*, const float*, const float*, void*,   \
+                                              hipStream_t);                                        \
     template hipError_t launch_activation<IO>(int, int64_t, void*, hipStream_t);                   \
     template hipError_t launch_tmix_prep<IO>(int, int, int, const void*, const void*, const void*, \
                                              const void*, const void*, const void*, float*,        \

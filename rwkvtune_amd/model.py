@@ -468,6 +468,28 @@ class RWKV7Model(nn.Module):
         _lib.call("rwkv7_gemm_decode", M, n, arrA, arrB, arrC, lda, ldc, N, K, epi,
                   P(ws.ws.data_ptr()), ws.ws.numel(), stream)
 
+    @staticmethod
+    def _gemm_partials(M: int, a, b, stream):
+        """The grouped GEMM's K-range partial products of A . B^T (B a
+        ``PackedWeight``) left as float32 planes [P][M][B.N] in the shared
+        workspace; returns (workspace tensor, P).  The next row kernel sums
+        them (``add_parts``) in place of the reduction launch."""
+        if a.dtype != torch.bfloat16 or a.shape != (M, b.K) or a.stride(1) != 1:
+            raise ValueError(f"grouped GEMM operand: A {tuple(a.shape)} {a.dtype} for a {b.N} x {b.K} weight")
+        lib = _lib.load()
+        parts = lib.rwkv7_gemm_decode_partial_count(M, b.N, b.K)
+        if parts < 1:
+            raise ValueError("rwkv7_gemm_decode_partial_count: " + lib.rwkv7_last_error().decode())
+        dev = a.device
+        ws = RWKV7Model._gemm_ws.get(dev)
+        if ws is None:
+            ws = RWKV7Model._gemm_ws[dev] = RWKV7Model.GemmWorkspace(dev)
+        ws.ensure(parts * M * b.N)
+        got = ctypes.c_int32(0)
+        _lib.call("rwkv7_gemm_decode_partials", M, _lib.ptr(a), _lib.ptr(b.t), a.stride(0), b.N, b.K,
+                  _lib.ptr(ws.ws), ws.ws.numel(), ctypes.c_void_p(ctypes.addressof(got)), stream)
+        return ws.ws, got.value
+
     @torch.no_grad()
     def forward_pooled(self, tokens: torch.Tensor, row_slot: torch.Tensor, row_last: torch.Tensor,
                        pool: StatePool, *, decode: bool, cu_seqlens: Optional[torch.Tensor] = None,
@@ -507,6 +529,7 @@ class RWKV7Model(nn.Module):
             ops_ptrs = (ctypes.c_void_p * 6)(*[ops[i].data_ptr() for i in range(6)])
             y = torch.empty((M, C), dtype=dt, device=dev)
         ffn_out = None
+        ffn_parts, ffn_stride = 0, 0  # > 0: ffn_out holds the FFN value's float32 partial planes
         S = pool.n_slots
         # decode rows of a bf16 model use the grouped MFMA GEMM (small M, many
         # projections); prefill and other dtypes use library GEMMs
@@ -517,12 +540,13 @@ class RWKV7Model(nn.Module):
             kv, ax, fx = pool.kv[l], pool.att_x[l], pool.ffn_x[l]
             # residual (+ previous FFN) -> ln0/ln1 -> shift -> 6 lerps
             if l == 0:
-                _lib.call("rwkv7_shift_mix", code, M, C, None, None, P(tokens), P(self.emb.weight),
+                _lib.call("rwkv7_shift_mix", code, M, C, None, None, 0, 0, P(tokens), P(self.emb.weight),
                           cfg.vocab_size, P(pk.ln0[0]) if pk.ln0 else None, P(pk.ln0[1]) if pk.ln0 else None,
                           P(x_res), P(pk.ln1[0]), P(pk.ln1[1]), P(ax), S, P(row_slot), P(row_last), 7,
                           P(pk.mix7), P(mixes), st)
             else:
-                _lib.call("rwkv7_shift_mix", code, M, C, P(x_mid), P(ffn_out), None, None, 0, None, None,
+                _lib.call("rwkv7_shift_mix", code, M, C, P(x_mid), P(ffn_out), ffn_parts, ffn_stride, None, None,
+                          0, None, None,
                           P(x_res), P(pk.ln1[0]), P(pk.ln1[1]), P(ax), S, P(row_slot), P(row_last), 7,
                           P(pk.mix7), P(mixes), st)
             xr, xk, xv, xw, xa, xg, _ = mixes.unbind(0)
@@ -572,24 +596,27 @@ class RWKV7Model(nn.Module):
                           pk.tparams, P(o), st)
             att_out = self._lin(o, att.output.weight)
             # residual + attention -> ln2 -> FFN shift/lerp
-            _lib.call("rwkv7_shift_mix", code, M, C, P(x_res), P(att_out), None, None, 0, None, None,
+            _lib.call("rwkv7_shift_mix", code, M, C, P(x_res), P(att_out), 0, 0, None, None, 0, None, None,
                       P(x_mid), P(pk.ln2[0]), P(pk.ln2[1]), P(fx), S, P(row_slot), P(row_last), 1,
                       P(pk.mixk), P(xk_ffn), st)
             if grouped:
                 # FFN key with relu^2 as its epilogue, then the value projection
                 hk = torch.empty((M, pk.gp["fk"].N), dtype=dt, device=dev)
                 self._gemm_group(M, [(xk_ffn[0], pk.gp["fk"], hk, 1)], st)
-                ffn_out = torch.empty((M, C), dtype=dt, device=dev)
-                self._gemm_group(M, [(hk, pk.gp["fv"], ffn_out, 0)], st)
+                # the value projection's K-range partials stay in the workspace;
+                # the next row kernel (shift_mix / final_norm) sums them
+                ffn_out, ffn_parts = self._gemm_partials(M, hk, pk.gp["fv"], st)
+                ffn_stride = M * C
             else:
                 hk = self._lin(xk_ffn[0], ffn.key.weight)
                 _lib.call("rwkv7_activation", code, 2, hk.numel(), P(hk), st)
                 ffn_out = self._lin(hk, ffn.value.weight)
+                ffn_parts, ffn_stride = 0, 0
         n_out = M if logit_rows is None else (n_logit_rows if n_logit_rows is not None else logit_rows.numel())
         if n_out == 0:
             return None
         xo = torch.empty((n_out, C), dtype=dt, device=dev)
-        _lib.call("rwkv7_final_norm", code, n_out, C, P(x_mid), P(ffn_out), P(logit_rows),
+        _lib.call("rwkv7_final_norm", code, n_out, C, P(x_mid), P(ffn_out), ffn_parts, ffn_stride, P(logit_rows),
                   P(self._ln_out[0]), P(self._ln_out[1]), P(xo), st)
         if return_hidden:
             return xo

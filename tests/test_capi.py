@@ -107,3 +107,24 @@ def test_gemm_host_side_errors(lib):
     assert lib.rwkv7_gemm_decode(*args(64, 64, 32, 0)) == 1 and b"lda" in lib.rwkv7_last_error()
     assert lib.rwkv7_gemm_decode(*args(64, 64, 64, 5)) == 1 and b"epi" in lib.rwkv7_last_error()
     assert lib.rwkv7_gemm_decode_workspace(256, 1, one(2048), one(60)) == -1
+
+
+def test_partials_host_side_errors(lib):
+    P = ctypes.c_void_p
+    fake = P(16)
+    parts = ctypes.c_int32(0)
+    pp = P(ctypes.addressof(parts))
+    assert lib.rwkv7_gemm_decode_partial_count(4, 32, 12) == -1 and b"K % 8" in lib.rwkv7_last_error()
+    n = lib.rwkv7_gemm_decode_partial_count(256, 2048, 8192)
+    assert 1 <= n <= 8
+    # workspace too small for n planes of 256 x 2048 floats; the count is reported anyway
+    assert lib.rwkv7_gemm_decode_partials(256, fake, fake, 8192, 2048, 8192, fake, 10, pp, None) == 1
+    assert parts.value == n and b"workspace" in lib.rwkv7_last_error()
+    assert lib.rwkv7_gemm_decode_partials(256, fake, fake, 8192, 2048, 8192, fake, 1 << 30, None, None) == 1
+    # row kernels: partial planes need x_in (not tokens), alignment and a stride of M * C floats
+    row = (2, 4, 8, fake)  # dtype bf16, M, C, x_in
+    rest = (None, None, 0, None, None, fake, fake, fake, fake, 4, fake, fake, 7, fake, fake, None)
+    assert lib.rwkv7_shift_mix(*row, fake, 2, 8, *rest) == 1 and b"partial" in lib.rwkv7_last_error()
+    assert lib.rwkv7_shift_mix(*row, P(18), 1, 0, *rest) == 1  # misaligned planes
+    assert lib.rwkv7_shift_mix(*row, fake, 65, 32, *rest) == 1  # too many planes
+    assert lib.rwkv7_final_norm(2, 4, 8, fake, fake, 2, 4, None, fake, fake, fake, None) == 1

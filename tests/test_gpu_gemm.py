@@ -103,3 +103,73 @@ def test_strided_operands(gpu_device):
     torch.cuda.synchronize()
     assert close(C, ref(A, B, 0))
 
+
+
+@pytest.mark.parametrize("M", [1, 33, 256])
+@pytest.mark.parametrize("seq", [False, True])
+def test_partials_feed_row_kernels(gpu_device, M, seq):
+    """rwkv7_gemm_decode_partials at the FFN value shape, summed by the next row
+    kernels (shift_mix, final_norm with add_parts), equals rwkv7_gemm_decode
+    (split-K reduction to bf16) followed by the same kernels reading its output:
+    bit for bit.  seq: the rows form one sequence, so the token shift also reads
+    the previous row's sum; else every row is its own sequence (decode)."""
+    print(f"[case] gemm partials M={M} seq={seq}", flush=True)
+    g = torch.Generator(device=gpu_device).manual_seed(100 + M)
+    C, K = 2048, 8192
+    A = torch.randn(M, K, generator=g, device=gpu_device).bfloat16()
+    pw = PackedWeight((torch.randn(C, K, generator=g, device=gpu_device) / K ** 0.5).bfloat16())
+    st = _lib.stream_of(A)
+    out = torch.empty(M, C, device=gpu_device).bfloat16()
+    RWKV7Model._gemm_group(M, [(A, pw, out, 0)], st)
+    ws, parts = RWKV7Model._gemm_partials(M, A, pw, st)
+    assert parts == _lib.load().rwkv7_gemm_decode_partial_count(M, C, K) >= 1
+    planes = ws[:parts * M * C].view(parts, M, C)
+    tot = planes[0].clone()
+    for q in range(1, parts):
+        tot += planes[q]
+    assert torch.equal(tot.bfloat16(), out)
+
+    code = _lib.dtype_code(torch.bfloat16)
+    P = _lib.ptr
+    x_in = torch.randn(M, C, generator=g, device=gpu_device)
+    ln_w = torch.rand(C, generator=g, device=gpu_device) + 0.5
+    ln_b = torch.randn(C, generator=g, device=gpu_device) * 0.1
+    mix = torch.rand(7, C, generator=g, device=gpu_device)
+    row_slot = torch.arange(M, dtype=torch.int32, device=gpu_device)
+    if seq:
+        row_slot = torch.zeros(M, dtype=torch.int32, device=gpu_device)
+        row_last = torch.full((M,), -1, dtype=torch.int32, device=gpu_device)
+        row_last[0] = M - 1
+    else:
+        row_last = torch.arange(M, dtype=torch.int32, device=gpu_device)
+    pool0 = torch.randn(M, C, generator=g, device=gpu_device)
+    res = []
+    for add, n_parts, stride in [(out, 0, 0), (ws, parts, M * C)]:
+        x_out = torch.empty(M, C, device=gpu_device)
+        pool = pool0.clone()
+        mixed = torch.empty(7, M, C, device=gpu_device).bfloat16()
+        _lib.call("rwkv7_shift_mix", code, M, C, P(x_in), P(add), n_parts, stride, None, None, 0, None, None,
+                  P(x_out), P(ln_w), P(ln_b), P(pool), M, P(row_slot), P(row_last), 7, P(mix), P(mixed), st)
+        rows = torch.arange(M - 1, -1, -1, dtype=torch.int32, device=gpu_device)
+        y = torch.empty(M, C, device=gpu_device).bfloat16()
+        _lib.call("rwkv7_final_norm", code, M, C, P(x_in), P(add), n_parts, stride, P(rows), P(ln_w), P(ln_b),
+                  P(y), st)
+        res.append((x_out, pool, mixed, y))
+    torch.cuda.synchronize()
+    for a, b in zip(*res):
+        assert torch.equal(a, b)
+
+
+def test_reduce_ragged_columns(gpu_device):
+    """Split-K reduction of a problem whose N is not a multiple of 4 (element-wise
+    path of gemm_reduce_kernel)."""
+    g = torch.Generator(device=gpu_device).manual_seed(11)
+    M, N, K = 3, 97, 4096
+    A = torch.randn(M, K, generator=g, device=gpu_device).bfloat16()
+    B = (torch.randn(N, K, generator=g, device=gpu_device) / K ** 0.5).bfloat16()
+    C = torch.empty(M, N, device=gpu_device).bfloat16()
+    assert _lib.load().rwkv7_gemm_decode_partial_count(M, N, K) > 1  # the plan splits K
+    RWKV7Model._gemm_group(M, [(A, PackedWeight(B), C, 0)], _lib.stream_of(C))
+    torch.cuda.synchronize()
+    assert close(C, ref(A, B, 0))
+
