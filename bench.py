@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of rwkvtune's batched-generation hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|cfg5|decode|prefill|tmix|logprob]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|cfg5|decode|prefill|tmix|logprob|train]
 
 Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a message.
 
@@ -24,6 +24,10 @@ logprob            GRPO log-prob recompute after a cfg4 rollout (RWKV-7 1.5B, bf
     ``compute_per_token_logps``; a step is one whole batch; value = forward
     tokens/s; roofline = GEMM flops (block matrices at every position, head at
     the completion positions) per second against the 2.5 PFLOP/s bf16 peak.
+train              WKV7 training operator (forward with 16-token checkpoints + backward,
+    bf16) at one layer of a 1.5B training step: B=8 x T=4096 tokens, H=32; value =
+    tokens/s of forward + backward; roofline = algorithmic HBM bytes of the
+    backward kernel per second against 8 TB/s.
 decode             isolated WKV7 decode kernel at B=256 slots, H=32 (cfg2); a step is
     one launch; value = algorithmic GB/s.
 tmix               the fused decode time-mix kernel alone at the rollout shape (the
@@ -401,6 +405,67 @@ def cpu_baseline_logprob(model, P=1024, C=512):
                       f"{dt:.1f} s"}
 
 
+# algorithmic bytes per (token, head) of the training operator: forward reads 6 bf16
+# inputs and writes y (bf16), sa (fp32) and the 16-token checkpoints (16 KB / 16);
+# backward reads 7 bf16 inputs, sa and the checkpoints and writes 6 bf16 gradients
+TRAIN_FWD_BYTES = 6 * N * 2 + N * 2 + N * 4 + N * N * 4 // 16
+TRAIN_BWD_BYTES = 7 * N * 2 + N * 4 + N * N * 4 // 16 + 6 * N * 2
+
+
+def train_leg(dev, steps, warmup, B=8, T=4096, H=32):
+    """WKV7 training operator (forward + backward, bf16) at one layer of a 1.5B
+    training step on B x T tokens; HIP events around each kernel."""
+    from rwkvtune_amd import operators as ops
+    g = torch.Generator(device=dev).manual_seed(21)
+    shp = (B, T, H, N)
+    r, k, v = (torch.randn(shp, generator=g, device=dev).bfloat16() for _ in range(3))
+    w = (torch.rand(shp, generator=g, device=dev) * -5.5 - 0.5).bfloat16()
+    kk = torch.nn.functional.normalize(torch.randn(shp, generator=g, device=dev), dim=-1)
+    a, b = (-kk).bfloat16(), (kk * torch.rand(shp, generator=g, device=dev)).bfloat16()
+    dy = torch.randn(shp, generator=g, device=dev).bfloat16()
+    st = torch.cuda.current_stream(dev)
+    for _ in range(warmup):
+        _, ck, sa = ops._train_forward(w, r, k, v, a, b)
+        ops._train_backward(w, r, k, v, a, b, dy, ck, sa)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    fwd = bwd = 0.0
+    for _ in range(steps):
+        ev[0].record(st)
+        _, ck, sa = ops._train_forward(w, r, k, v, a, b)
+        ev[1].record(st)
+        ops._train_backward(w, r, k, v, a, b, dy, ck, sa)
+        ev[2].record(st)
+        ev[2].synchronize()
+        fwd += ev[0].elapsed_time(ev[1]) / steps
+        bwd += ev[1].elapsed_time(ev[2]) / steps
+    units = B * T * H
+    fgbs = units * TRAIN_FWD_BYTES / (fwd * 1e-3) / 1e9
+    bgbs = units * TRAIN_BWD_BYTES / (bwd * 1e-3) / 1e9
+    return {"fwd_ms": fwd, "bwd_ms": bwd, "tokens_per_s": B * T / ((fwd + bwd) * 1e-3), "fwd_GBs": fgbs,
+            "bwd_GBs": bgbs, "B": B, "T": T, "H": H,
+            "kernels": "wkv7_train_fwd_kernel<bf16>, wkv7_train_bwd_kernel<bf16>"}
+
+
+def cpu_baseline_train(T=64, H=32):
+    """The reference's CPU path for training (the restated wkv_cpu.py recurrence,
+    float32, with torch autograd for the backward) on one sequence of T tokens."""
+    from oracle.wkv7 import wkv7_cpu
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(3)
+    C = H * N
+    xs = [torch.randn(1, T, C, generator=g) for _ in range(6)]
+    xs[1] = torch.rand(1, T, C, generator=g) * -5.5 - 0.5
+    xs = [x.requires_grad_(True) for x in xs]
+    t0 = time.perf_counter()
+    y, _ = wkv7_cpu(*xs, N)
+    y.sum().backward()
+    dt = time.perf_counter() - t0
+    return {"value": T / dt, "unit": "tokens/s (forward + backward, one layer)", "cores": cores, "kind": "port",
+            "sample": f"one sequence of {T} tokens, H={H}, through the restated wkv_cpu.py recurrence (fp32) "
+                      f"and torch autograd; {dt:.1f} s"}
+
+
 def cpu_baseline_rollout(model, prompts, paths=256, decode_steps=2):
     """The reference CPU rollout (oracle/: fp32 forward_with_state, batched
     sample_batch rules) on a bounded sample: one prompt prefilled, forked to
@@ -457,7 +522,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="rollout", choices=["rollout", "cfg5", "decode", "prefill", "tmix", "logprob"])
+    ap.add_argument("--workload", default="rollout", choices=["rollout", "cfg5", "decode", "prefill", "tmix", "logprob", "train"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     a = ap.parse_args()
     if a.gpus != 1:
@@ -556,6 +621,24 @@ def main():
                          "unit": "TFLOP/s", "frac": lp["gemm_TFLOPs"] / PEAK_BF16_TFLOPS, "traffic": None,
                          "kernel": "whole recompute (block GEMMs at every position + head at the completion "
                                    "positions), per second of wall time", "flops_per_step": lp["flops"]},
+            "cpu_baseline": cpu,
+        }
+    elif a.workload == "train":
+        steps = 5 if a.steps is None else a.steps
+        warmup = 1 if a.warmup is None else a.warmup
+        tr = train_leg(dev, steps, warmup)
+        log(f"[bench] train op: fwd {tr['fwd_ms']:.2f} ms ({tr['fwd_GBs']:.0f} GB/s), bwd {tr['bwd_ms']:.2f} ms "
+            f"({tr['bwd_GBs']:.0f} GB/s), {tr['tokens_per_s']:.0f} tokens/s")
+        cpu = None if a.no_cpu_baseline else cpu_baseline_train()
+        out = {
+            "metric": METRIC, "value": tr["tokens_per_s"], "unit": "tokens/s (WKV7 forward + backward, one layer)",
+            "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": tr["fwd_ms"] + tr["bwd_ms"],
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": "bf16 I/O, fp32 state and checkpoints", "data": "synthetic",
+            "config": {"workload": f"WKV7 training operator, B={tr['B']} x T={tr['T']}, H={tr['H']}, N=64",
+                       "fwd_ms": tr["fwd_ms"], "bwd_ms": tr["bwd_ms"], "fwd_GBs": tr["fwd_GBs"]},
+            "roofline": {"bound": "hbm", "achieved": tr["bwd_GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": tr["bwd_GBs"] / PEAK_HBM_GBS, "traffic": None, "kernel": tr["kernels"]},
             "cpu_baseline": cpu,
         }
     elif a.workload == "tmix":

@@ -97,6 +97,37 @@ int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t total_tokens,
                       const void *a, const void *b, void *y, int chunk_len,
                       void *stream);
 
+/*
+ * Training operator: replaces torch.ops.wind_backstepping.forward / backward
+ * (rwkvtune/models/rwkv7/operators/cuda/wkv7_op.cpp:6-18, kernels
+ * wkv7_cuda.cu:10-142) and, with s0 / ds_in / ds0, the infinite-context op
+ * (wkv7_infctx_op.cpp, wkv7_infctx_cuda.cu:24-305).  Inputs r, w (raw: the
+ * decay is exp(-exp(w))), k, v, a, b, y, dy and the gradients are [B, T, H, 64]
+ * in the I/O dtype (any T >= 1; the standard op's caller requires T % 16 == 0).
+ *
+ * forward: y; sa = S_{t-1} a_t (float32 [B, T, H, 64]); ckpt = the float32 state
+ * [64][64] (row = value index) after every 16th token and after the last one,
+ * [B, H, ceil(T/16), 64, 64] (rwkv7_wkv_train_ckpt_floats floats, 16-byte
+ * aligned).  s0: initial state [B, H, 64, 64] float32 (NULL: zero); s_out
+ * (nullable, may alias s0) receives the final state.
+ * backward: from dy and the forward's ckpt and sa, the gradients dr, dw (w.r.t.
+ * the raw w), dk, dv, da, db; ds_in (nullable) is the gradient of the final
+ * state, ds0 (nullable) receives the initial state's.  The state is stepped
+ * back one token at a time from the checkpoints (S_{t-1} = (S_t - v k^T -
+ * sa b^T) / w~, as the reference), so it needs w~ = exp(-exp(w)) > 0.
+ */
+int64_t rwkv7_wkv_train_ckpt_floats(int64_t B, int64_t T, int64_t H);
+int rwkv7_wkv_train_forward(int dtype, int64_t B, int64_t T, int64_t H, const void *r,
+                            const void *w, const void *k, const void *v, const void *a,
+                            const void *b, void *y, const float *s0, float *s_out,
+                            float *ckpt, float *sa, void *stream);
+int rwkv7_wkv_train_backward(int dtype, int64_t B, int64_t T, int64_t H, const void *r,
+                             const void *w, const void *k, const void *v, const void *a,
+                             const void *b, const void *dy, const float *ckpt,
+                             const float *sa, const float *ds_in, void *dr, void *dw,
+                             void *dk, void *dv, void *da, void *db, float *ds0,
+                             void *stream);
+
 /* ------------------------------------------------------------------------
  * Layer kernels of the stateful model forward.  They replace the eager torch
  * op chains of RWKV7Block / RWKV7TimeMix / RWKV7ChannelMix.forward_with_state

@@ -32,6 +32,9 @@ SIGNATURES = {
     "rwkv7s_forward": (_I32, [_I32, _I64, _I64, _I64, _I64] + [_P] * 8 + [_P]),
     "rwkv7_wkv_decode": (_I32, [_I32, _I64, _I64, _P, _I64, _P] + [_P] * 7 + [_P]),
     "rwkv7_wkv_prefill": (_I32, [_I32, _I64, _I64, _I64, _P, _P, _P, _I64] + [_P] * 7 + [_I32, _P]),
+    "rwkv7_wkv_train_ckpt_floats": (_I64, [_I64, _I64, _I64]),
+    "rwkv7_wkv_train_forward": (_I32, [_I32, _I64, _I64, _I64] + [_P] * 11 + [_P]),
+    "rwkv7_wkv_train_backward": (_I32, [_I32, _I64, _I64, _I64] + [_P] * 17 + [_P]),
     "rwkv7_shift_mix": (_I32, [_I32, _I64, _I64, _P, _P, _I32, _I64, _P, _P, _I64, _P, _P, _P, _P, _P, _P,
                                _I64, _P, _P, _I32, _P, _P, _P]),
     "rwkv7_final_norm": (_I32, [_I32, _I64, _I64, _P, _P, _I32, _I64, _P, _P, _P, _P, _P]),

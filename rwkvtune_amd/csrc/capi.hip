@@ -511,6 +511,77 @@ extern "C" int rwkv7_admit_copy(const int32_t* counters, const int32_t* admit_sl
 }
 
 // ---------------------------------------------------------------------------
+// Training operator (wkv7_train.hip)
+// ---------------------------------------------------------------------------
+
+int64_t wkv7_train_ckpt_floats(int B, int T, int H);
+template <typename IO>
+hipError_t launch_wkv7_train_fwd(int B, int T, int H, const void* r, const void* w, const void* k, const void* v,
+                                 const void* a, const void* b, void* y, const float* s0, float* s_out, float* ckpt,
+                                 float* sa, hipStream_t st);
+template <typename IO>
+hipError_t launch_wkv7_train_bwd(int B, int T, int H, const void* r, const void* w, const void* k, const void* v,
+                                 const void* a, const void* b, const void* dy, const float* ckpt, const float* sa,
+                                 const float* ds_in, void* dr, void* dw, void* dk, void* dv, void* da, void* db,
+                                 float* ds0, hipStream_t st);
+
+namespace {
+int train_sizes(const char* fn, int64_t B, int64_t T, int64_t H) {
+    if (B < 0 || T < 0 || H <= 0)
+        return fail(RWKV7_ERR_INVALID, "%s: bad sizes B=%lld T=%lld H=%lld", fn, (long long)B, (long long)T,
+                    (long long)H);
+    if (B * H > kMaxInt || T > kMaxInt || B * T * H * RWKV7_HEAD > ((int64_t)1 << 40))
+        return fail(RWKV7_ERR_INVALID, "%s: problem too large", fn);
+    return RWKV7_OK;
+}
+bool f32_misaligned(const float* p) { return (((uintptr_t)p) & 15) != 0; }
+}  // namespace
+
+extern "C" int64_t rwkv7_wkv_train_ckpt_floats(int64_t B, int64_t T, int64_t H) {
+    if (train_sizes("rwkv7_wkv_train_ckpt_floats", B, T, H) != RWKV7_OK) return -1;
+    ok();
+    return wkv7_train_ckpt_floats((int)B, (int)T, (int)H);
+}
+
+extern "C" int rwkv7_wkv_train_forward(int dtype, int64_t B, int64_t T, int64_t H, const void* r, const void* w,
+                                       const void* k, const void* v, const void* a, const void* b, void* y,
+                                       const float* s0, float* s_out, float* ckpt, float* sa, void* stream) {
+    if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_train_forward: bad dtype code %d", dtype);
+    if (train_sizes("rwkv7_wkv_train_forward", B, T, H) != RWKV7_OK) return RWKV7_ERR_INVALID;
+    if (B == 0 || T == 0) return ok();
+    if (any_null(r, w, k, v, a, b, y, ckpt) || !sa)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_train_forward: null pointer");
+    if (f32_misaligned(ckpt) || f32_misaligned(s0) || f32_misaligned(s_out))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_train_forward: checkpoints and states must be 16-byte aligned");
+    hipError_t e;
+    RWKV7_DISPATCH(dtype, (launch_wkv7_train_fwd<IO>((int)B, (int)T, (int)H, r, w, k, v, a, b, y, s0, s_out, ckpt,
+                                                     sa, (hipStream_t)stream)));
+    return launch_status(e, "wkv7_train_fwd_kernel");
+}
+
+extern "C" int rwkv7_wkv_train_backward(int dtype, int64_t B, int64_t T, int64_t H, const void* r, const void* w,
+                                        const void* k, const void* v, const void* a, const void* b, const void* dy,
+                                        const float* ckpt, const float* sa, const float* ds_in, void* dr, void* dw,
+                                        void* dk, void* dv, void* da, void* db, float* ds0, void* stream) {
+    if (!dtype_ok(dtype)) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_train_backward: bad dtype code %d", dtype);
+    if (train_sizes("rwkv7_wkv_train_backward", B, T, H) != RWKV7_OK) return RWKV7_ERR_INVALID;
+    if (B == 0) return ok();
+    if (T == 0) {
+        if (ds0 == nullptr) return ok();
+        return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_train_backward: T = 0 with an initial-state gradient "
+                    "(copy ds_in instead)");
+    }
+    if (any_null(r, w, k, v, a, b, dy, ckpt) || !sa || any_null(dr, dw, dk, dv, da, db, sa, ckpt))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_train_backward: null pointer");
+    if (f32_misaligned(ckpt) || f32_misaligned(ds0))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_train_backward: checkpoints and ds0 must be 16-byte aligned");
+    hipError_t e;
+    RWKV7_DISPATCH(dtype, (launch_wkv7_train_bwd<IO>((int)B, (int)T, (int)H, r, w, k, v, a, b, dy, ckpt, sa, ds_in,
+                                                     dr, dw, dk, dv, da, db, ds0, (hipStream_t)stream)));
+    return launch_status(e, "wkv7_train_bwd_kernel");
+}
+
+// ---------------------------------------------------------------------------
 // Grouped decode GEMM (gemm_decode.hip)
 // ---------------------------------------------------------------------------
 

@@ -1,0 +1,346 @@
+// WKV7 training operator on gfx950: forward with state checkpoints and the
+// backward pass ("wind backstepping"), with an optional initial state and its
+// gradient for chunked infinite-context training.
+//
+// Reference semantics (rwkvtune/models/rwkv7/operators/cuda/wkv7_cuda.cu:10-142):
+// per (sequence b, head h), zero initial state (or s0), for t = 0 .. T-1
+//   sa_i = sum_j a_j S_ij                            (old state)
+//   S_ij = S_ij w~_j + k_j v_i + sa_i b_j,  w~ = exp(-exp(w_raw))
+//   y_i  = sum_j S_ij r_j
+// The forward saves sa (float32) and the state after every 16th token and after
+// the last one; the backward walks t = T-1 .. 0 carrying dS in both orientations,
+// reloads S_t from the checkpoint at each segment end and steps it back one token
+// at a time, S_{t-1} = (S_t - v k^T - sa b^T) diag(1 / w~) (as the reference), so
+// at most 15 divisions separate any state from a stored one.  Gradients:
+//   dr_i = sum_j S_t[j][i] dy_j,   dS_t += dy r^T
+//   dw_i = (sum_j dS_t[j][i] S_{t-1}[j][i]) * w~_i * (-exp(w_raw_i))
+//   dk_i = sum_j dS_t[j][i] v_j,   dv_i = sum_j dS_t[i][j] k_j
+//   dsa_i = sum_j dS_t[i][j] b_j,  db_i = sum_j dS_t[j][i] sa_j
+//   da_i = sum_j S_{t-1}[j][i] dsa_j
+//   dS_{t-1}[i][j] = dS_t[i][j] w~_j + dsa_i a_j
+// (the infinite-context variant, wkv7_infctx_cuda.cu:105-305, adds the incoming
+// gradient of the final state and returns the initial state's gradient.)
+//
+// Layout (CDNA, not the reference's one-thread-per-row): a 512-thread block per
+// (b, h); thread (i, q) = (tid / 8, tid % 8) holds 8 columns j = 8q .. 8q+7 of
+// row i (forward) or of row i and column i (backward), so a sum over j is 8 FMAs
+// (two chains) and a three-step DPP reduction over the row's 8 lanes; two waves
+// per SIMD hide each other's LDS and reduction latency.  Inputs [B, T, H, 64] in
+// the I/O dtype move through LDS 16 tokens (one checkpoint segment) at a time,
+// double-buffered: the next segment's global loads (12 or 16 per thread, issued
+// together) are in flight while the current one computes, so the memory latency
+// is paid once per segment, not once per token.
+#include "common.hpp"
+
+namespace {
+
+constexpr int NH = 64;
+constexpr int SEG = 16;  // checkpoint interval (tokens)
+constexpr int TPR = 8;   // threads per state row
+constexpr int JPT = NH / TPR;  // columns per thread
+constexpr int TH = NH * TPR;
+
+// sum over the 8 lanes of a row (lanes 8i .. 8i+7): quad sums, then the other quad
+__device__ __forceinline__ float row_sum(float x) {
+    x += dpp_xor1(x);
+    x += dpp_xor2(x);
+    return x + dpp_xor7(x);
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+template <typename IO>
+__global__ __launch_bounds__(TH) void wkv7_train_fwd_kernel(
+    int T, int H, const IO* __restrict__ r, const IO* __restrict__ w, const IO* __restrict__ k,
+    const IO* __restrict__ v, const IO* __restrict__ a, const IO* __restrict__ b, IO* __restrict__ y,
+    const float* __restrict__ s0, float* __restrict__ s_out, float* __restrict__ ckpt, float* __restrict__ sa_out)
+{
+    typedef io_traits<IO> tr;
+    // [buffer][array][token of the segment][j]: arrays r, decay, k, a, b, v
+    constexpr int NA = 6;
+    __shared__ __attribute__((aligned(16))) float in[2][NA][SEG][NH];
+    const int bh = blockIdx.x;
+    const int bb = bh / H, hh = bh - bb * H;
+    const int tid = threadIdx.x;
+    const int i = tid / TPR, q = tid % TPR, j0 = JPT * q;
+    const int nck = (T + SEG - 1) / SEG;
+
+    float S[JPT];
+    if (s0 != nullptr) {
+        const float* p = s0 + ((size_t)bh * NH + i) * NH + j0;
+#pragma unroll
+        for (int c = 0; c < JPT / 4; ++c) {
+            const f32x4 x = *reinterpret_cast<const f32x4*>(p + 4 * c);
+            S[4 * c] = x.x; S[4 * c + 1] = x.y; S[4 * c + 2] = x.z; S[4 * c + 3] = x.w;
+        }
+    } else {
+#pragma unroll
+        for (int jj = 0; jj < JPT; ++jj) S[jj] = 0.f;
+    }
+
+    // staging of a segment: flat element f = tid + TH m (m < NL) is element
+    // f % 64 of token f / 64 % 16 of array f / 1024
+    constexpr int NL = NA * SEG * NH / TH;
+    float xr[NL];
+    auto fetch = [&](int c) {
+#pragma unroll
+        for (int m = 0; m < NL; ++m) {
+            const int f = tid + TH * m, arr = f >> 10, t = c * SEG + ((f >> 6) & (SEG - 1)), e = f & 63;
+            const IO* sp = arr == 0 ? r : arr == 1 ? w : arr == 2 ? k : arr == 3 ? a : arr == 4 ? b : v;
+            xr[m] = t < T ? tr::to_f32(sp[(((size_t)bb * T + t) * H + hh) * NH + e]) : 0.f;
+        }
+    };
+    const int nseg = (T + SEG - 1) / SEG;
+    fetch(0);
+    for (int c = 0; c < nseg; ++c) {
+        const int buf = c & 1;
+#pragma unroll
+        for (int m = 0; m < NL; ++m) {
+            const int f = tid + TH * m, arr = f >> 10;
+            in[buf][arr][(f >> 6) & (SEG - 1)][f & 63] = arr == 1 ? expf(-expf(xr[m])) : xr[m];
+        }
+        __syncthreads();
+        if (c + 1 < nseg) fetch(c + 1);
+        const int n = min(SEG, T - c * SEG);
+        for (int u = 0; u < n; ++u) {
+            const int t = c * SEG + u;
+            const float* rr = in[buf][0][u] + j0;
+            const float* dec = in[buf][1][u] + j0;
+            const float* kk = in[buf][2][u] + j0;
+            const float* aa = in[buf][3][u] + j0;
+            const float* bv = in[buf][4][u] + j0;
+            float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+            for (int jj = 0; jj < JPT; jj += 2) {
+                s1 = fmaf(aa[jj], S[jj], s1);
+                s2 = fmaf(aa[jj + 1], S[jj + 1], s2);
+            }
+            const float sa = row_sum(s1 + s2);
+            const float vi = in[buf][5][u][i];
+            float y1 = 0.f, y2 = 0.f;
+#pragma unroll
+            for (int jj = 0; jj < JPT; ++jj) {
+                const float sv = fmaf(S[jj], dec[jj], fmaf(kk[jj], vi, sa * bv[jj]));
+                S[jj] = sv;
+                if (jj & 1) y2 = fmaf(sv, rr[jj], y2); else y1 = fmaf(sv, rr[jj], y1);
+            }
+            const float yi = row_sum(y1 + y2);
+            const size_t o = (((size_t)bb * T + t) * H + hh) * NH + i;
+            if (q == 0) {
+                y[o] = tr::from_f32(yi);
+                sa_out[o] = sa;
+            }
+        }
+        // the state after the segment's last token
+        float* p = ckpt + (((size_t)bh * nck + c) * NH + i) * NH + j0;
+#pragma unroll
+        for (int cc = 0; cc < JPT / 4; ++cc)
+            *reinterpret_cast<f32x4*>(p + 4 * cc) = f32x4{S[4 * cc], S[4 * cc + 1], S[4 * cc + 2], S[4 * cc + 3]};
+    }
+    if (s_out != nullptr) {
+        // every thread read its part of s0 at the start, so s_out may alias s0
+        float* p = s_out + ((size_t)bh * NH + i) * NH + j0;
+#pragma unroll
+        for (int c = 0; c < JPT / 4; ++c)
+            *reinterpret_cast<f32x4*>(p + 4 * c) = f32x4{S[4 * c], S[4 * c + 1], S[4 * c + 2], S[4 * c + 3]};
+    }
+}
+
+// ---------------------------------------------------------------------------
+// backward
+// ---------------------------------------------------------------------------
+template <typename IO>
+__global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
+    int T, int H, const IO* __restrict__ r, const IO* __restrict__ w, const IO* __restrict__ k,
+    const IO* __restrict__ v, const IO* __restrict__ a, const IO* __restrict__ b, const IO* __restrict__ dy,
+    const float* __restrict__ ckpt, const float* __restrict__ sa_in, const float* __restrict__ ds_in,
+    IO* __restrict__ dr, IO* __restrict__ dw, IO* __restrict__ dk, IO* __restrict__ dv, IO* __restrict__ da,
+    IO* __restrict__ db, float* __restrict__ ds0)
+{
+    typedef io_traits<IO> tr;
+    // [buffer][array][token of the segment][j]: arrays r, decay, k, v, a, b, dy,
+    // sa, log-decay (-exp(w_raw))
+    constexpr int NA = 9;
+    __shared__ __attribute__((aligned(16))) float in[2][NA][SEG][NH];
+    __shared__ __attribute__((aligned(16))) float dsa_sh[2][NH];
+    const int bh = blockIdx.x;
+    const int bb = bh / H, hh = bh - bb * H;
+    const int tid = threadIdx.x;
+    const int i = tid / TPR, q = tid % TPR, j0 = JPT * q;
+    const int nck = (T + SEG - 1) / SEG;
+
+    float sT[JPT], dS[JPT], dST[JPT];  // S[j][i], dS[i][j], dS[j][i] for j = j0 + jj
+    if (ds_in != nullptr) {
+        const float* p = ds_in + (size_t)bh * NH * NH;
+#pragma unroll
+        for (int jj = 0; jj < JPT; ++jj) {
+            dS[jj] = p[i * NH + j0 + jj];
+            dST[jj] = p[(j0 + jj) * NH + i];
+        }
+    } else {
+#pragma unroll
+        for (int jj = 0; jj < JPT; ++jj) dS[jj] = dST[jj] = 0.f;
+    }
+#pragma unroll
+    for (int jj = 0; jj < JPT; ++jj) sT[jj] = 0.f;
+
+    // staging of a segment: flat element f = tid + TH m (m < NL) is element
+    // f % 64 of token f / 64 % 16 of input array f / 1024 (r, w, k, v, a, b, dy,
+    // sa); w also yields the log-decay array
+    constexpr int NL = 8 * SEG * NH / TH;
+    float xr[NL];
+    auto fetch = [&](int c) {
+#pragma unroll
+        for (int m = 0; m < NL; ++m) {
+            const int f = tid + TH * m, arr = f >> 10, t = c * SEG + ((f >> 6) & (SEG - 1)), e = f & 63;
+            const size_t idx = (((size_t)bb * T + min(t, T - 1)) * H + hh) * NH + e;
+            if (arr == 7) {
+                xr[m] = sa_in[idx];
+            } else {
+                const IO* sp = arr == 0 ? r : arr == 1 ? w : arr == 2 ? k : arr == 3 ? v : arr == 4 ? a
+                             : arr == 5 ? b : dy;
+                xr[m] = tr::to_f32(sp[idx]);
+            }
+        }
+    };
+    const int nseg = (T + SEG - 1) / SEG;
+    fetch(nseg - 1);
+    int par = 0;  // dsa_sh buffer of the current token
+    for (int c = nseg - 1; c >= 0; --c) {
+        const int buf = c & 1;
+#pragma unroll
+        for (int m = 0; m < NL; ++m) {
+            const int f = tid + TH * m, arr = f >> 10, u = (f >> 6) & (SEG - 1), e = f & 63;
+            if (arr == 1) {
+                const float lw = -expf(xr[m]);
+                in[buf][1][u][e] = expf(lw);
+                in[buf][8][u][e] = lw;
+            } else {
+                in[buf][arr][u][e] = xr[m];
+            }
+        }
+        __syncthreads();
+        if (c > 0) fetch(c - 1);
+        // S after the segment's last token
+        {
+            const float* p = ckpt + ((size_t)bh * nck + c) * NH * NH;
+#pragma unroll
+            for (int jj = 0; jj < JPT; ++jj) sT[jj] = p[(j0 + jj) * NH + i];
+        }
+        const int n = min(SEG, T - c * SEG);
+        for (int u = n - 1; u >= 0; --u) {
+            const int t = c * SEG + u;
+            const float* rr = in[buf][0][u];
+            const float* dec = in[buf][1][u];
+            const float* kk = in[buf][2][u];
+            const float* vv = in[buf][3][u];
+            const float* aa = in[buf][4][u];
+            const float* bv = in[buf][5][u];
+            const float* dyv = in[buf][6][u];
+            const float* sav = in[buf][7][u];
+            float g1 = 0.f, g2 = 0.f;  // dr_i
+#pragma unroll
+            for (int jj = 0; jj < JPT; jj += 2) {
+                g1 = fmaf(sT[jj], dyv[j0 + jj], g1);
+                g2 = fmaf(sT[jj + 1], dyv[j0 + jj + 1], g2);
+            }
+            const float g = row_sum(g1 + g2);
+            const float ri = rr[i], ki = kk[i], bi = bv[i], dyi = dyv[i], ai = aa[i], wi = dec[i];
+            const float iwi = 1.0f / wi;
+            float gw = 0.f, gk = 0.f, gv = 0.f, gsa = 0.f, gb = 0.f;
+#pragma unroll
+            for (int jj = 0; jj < JPT; ++jj) {
+                const int j = j0 + jj;
+                sT[jj] = (sT[jj] - ki * vv[j] - bi * sav[j]) * iwi;
+                dS[jj] = fmaf(dyi, rr[j], dS[jj]);
+                dST[jj] = fmaf(ri, dyv[j], dST[jj]);
+                gw = fmaf(dST[jj], sT[jj], gw);
+                gk = fmaf(dST[jj], vv[j], gk);
+                gv = fmaf(dS[jj], kk[j], gv);
+                gsa = fmaf(dS[jj], bv[j], gsa);
+                gb = fmaf(dST[jj], sav[j], gb);
+            }
+            gw = row_sum(gw);
+            gk = row_sum(gk);
+            gv = row_sum(gv);
+            gsa = row_sum(gsa);
+            gb = row_sum(gb);
+            const size_t o = (((size_t)bb * T + t) * H + hh) * NH + i;
+            if (q == 0) {
+                dr[o] = tr::from_f32(g);
+                dw[o] = tr::from_f32(gw * wi * in[buf][8][u][i]);
+                dk[o] = tr::from_f32(gk);
+                dv[o] = tr::from_f32(gv);
+                db[o] = tr::from_f32(gb);
+                dsa_sh[par][i] = gsa;
+            }
+            // one barrier per token: dsa_sh alternates, so the next token's write
+            // goes to the other buffer, read by nobody until after this barrier
+            __syncthreads();
+            const float* ds = dsa_sh[par];
+            float a1 = 0.f, a2 = 0.f;
+#pragma unroll
+            for (int jj = 0; jj < JPT; jj += 2) {
+                a1 = fmaf(sT[jj], ds[j0 + jj], a1);
+                a2 = fmaf(sT[jj + 1], ds[j0 + jj + 1], a2);
+            }
+            const float ga = row_sum(a1 + a2);
+            if (q == 0) da[o] = tr::from_f32(ga);
+#pragma unroll
+            for (int jj = 0; jj < JPT; ++jj) {
+                const int j = j0 + jj;
+                dS[jj] = fmaf(dS[jj], dec[j], gsa * aa[j]);
+                dST[jj] = fmaf(dST[jj], wi, ai * ds[j]);
+            }
+            par ^= 1;
+        }
+    }
+    if (ds0 != nullptr) {
+        float* p = ds0 + ((size_t)bh * NH + i) * NH + j0;
+#pragma unroll
+        for (int c = 0; c < JPT / 4; ++c)
+            *reinterpret_cast<f32x4*>(p + 4 * c) = f32x4{dS[4 * c], dS[4 * c + 1], dS[4 * c + 2], dS[4 * c + 3]};
+    }
+}
+
+}  // namespace
+
+int64_t wkv7_train_ckpt_floats(int B, int T, int H) {
+    return (int64_t)B * H * ((T + SEG - 1) / SEG) * NH * NH;
+}
+
+template <typename IO>
+hipError_t launch_wkv7_train_fwd(int B, int T, int H, const void* r, const void* w, const void* k, const void* v,
+                                 const void* a, const void* b, void* y, const float* s0, float* s_out, float* ckpt,
+                                 float* sa, hipStream_t st)
+{
+    hipLaunchKernelGGL(wkv7_train_fwd_kernel<IO>, dim3((unsigned)(B * H)), dim3(TH), 0, st, T, H, (const IO*)r,
+                       (const IO*)w, (const IO*)k, (const IO*)v, (const IO*)a, (const IO*)b, (IO*)y, s0, s_out, ckpt,
+                       sa);
+    return hipGetLastError();
+}
+
+template <typename IO>
+hipError_t launch_wkv7_train_bwd(int B, int T, int H, const void* r, const void* w, const void* k, const void* v,
+                                 const void* a, const void* b, const void* dy, const float* ckpt, const float* sa,
+                                 const float* ds_in, void* dr, void* dw, void* dk, void* dv, void* da, void* db,
+                                 float* ds0, hipStream_t st)
+{
+    hipLaunchKernelGGL(wkv7_train_bwd_kernel<IO>, dim3((unsigned)(B * H)), dim3(TH), 0, st, T, H, (const IO*)r,
+                       (const IO*)w, (const IO*)k, (const IO*)v, (const IO*)a, (const IO*)b, (const IO*)dy, ckpt, sa,
+                       ds_in, (IO*)dr, (IO*)dw, (IO*)dk, (IO*)dv, (IO*)da, (IO*)db, ds0);
+    return hipGetLastError();
+}
+
+#define RWKV7_INST_TRAIN(IO)                                                                                         \
+    template hipError_t launch_wkv7_train_fwd<IO>(int, int, int, const void*, const void*, const void*, const void*, \
+                                                  const void*, const void*, void*, const float*, float*, float*,   \
+                                                  float*, hipStream_t);                                             \
+    template hipError_t launch_wkv7_train_bwd<IO>(int, int, int, const void*, const void*, const void*, const void*, \
+                                                  const void*, const void*, const void*, const float*,             \
+                                                  const float*, const float*, void*, void*, void*, void*, void*,   \
+                                                  void*, float*, hipStream_t);
+RWKV7_INST_TRAIN(float)
+RWKV7_INST_TRAIN(bf16_t)
+RWKV7_INST_TRAIN(f16_t)

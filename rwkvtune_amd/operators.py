@@ -18,11 +18,25 @@ Plus the slot-table entry points the engine uses directly: ``wkv7_decode``
 (single token on a resident state pool, rows addressed through ``slot_idx``) and
 ``wkv7_prefill`` (ragged packed prompts, ``cu_seqlens``).
 
+``load_wkv_operator(device='cuda', for_inference=False)`` / ``load_hip_operator_train``
+    the training operator ``RUN_CUDA_RWKV7g(q, w, k, v, a, b)`` of
+    ``wkv_loader.py:201-356``: inputs cast to bf16 and viewed ``[B, T, H, 64]``,
+    ``T % 16 == 0`` asserted, ``y`` bf16 ``[B, T, C]``, gradients (bf16) for all
+    six inputs through ``WindBackstepping`` on ``rwkv7_wkv_train_forward`` /
+    ``_backward``.
+``rwkv7_wkv_infctx(w, q, k, v, a, b, state=None, scale=1.0)``
+    ``operators/wkv_infctx.py:164-210``: ``(y, final_state)`` with gradients for the
+    inputs and the initial state, and a final-state gradient flowing in;
+    ``load_hip_operator_infctx()`` returns the raw ``forward`` / ``backward`` pair of
+    ``wkv7_infctx_op`` (``wkv_loader.py:588-705``).
+
 Differences, on purpose: no JIT build, lock file or barrier (the library is built
 ahead of time); no CPU fallback when the library is missing - the call raises;
-the training operator (``for_inference=False``) and the CPU operator are not
-part of this library (``NotImplementedError``); the kernels run on torch's
-current stream instead of the legacy default stream.
+the CPU operator is not part of this library (``NotImplementedError``); the
+kernels run on torch's current stream instead of the legacy default stream; the
+infinite-context backward recomputes the forward once (checkpoints every 16
+tokens) instead of re-running it from the initial state for every segment.
+The reference's loader names (``load_cuda_operator_*``) are aliases here.
 """
 
 from __future__ import annotations
@@ -119,6 +133,173 @@ def load_hip_operator_inference(head_size: int = HEAD_SIZE) -> Callable:
     return _inference_op
 
 
+# ---------------------------------------------------------------------------
+# Training operator (wkv_loader.py:201-356) and infinite-context operator
+# (operators/wkv_infctx.py, wkv_loader.py:588-705)
+# ---------------------------------------------------------------------------
+
+CHUNK_LEN = 16  # wkv_loader.py:263: the standard training op needs T % 16 == 0
+
+_train_op = None
+_infctx_op = None
+
+
+def _train_forward(w, q, k, v, a, b, s0=None, s_out=None):
+    """Launch ``rwkv7_wkv_train_forward`` on ``[B, T, H, 64]`` contiguous inputs of
+    one dtype; returns ``(y, ckpt, sa)``."""
+    B, T, H, N = q.shape
+    dev = q.device
+    y = torch.empty_like(v)
+    nck = (T + CHUNK_LEN - 1) // CHUNK_LEN
+    ckpt = torch.empty((B, H, nck, N, N), dtype=torch.float32, device=dev)
+    sa = torch.empty((B, T, H, N), dtype=torch.float32, device=dev)
+    P = _lib.ptr
+    _lib.call("rwkv7_wkv_train_forward", _lib.dtype_code(q.dtype), B, T, H, P(q), P(w), P(k), P(v), P(a), P(b),
+              P(y), P(s0), P(s_out), P(ckpt), P(sa), _lib.stream_of(q))
+    return y, ckpt, sa
+
+
+def _train_backward(w, q, k, v, a, b, dy, ckpt, sa, ds_in=None, want_ds0=False):
+    B, T, H, N = q.shape
+    grads = [torch.empty_like(x) for x in (w, q, k, v, a, b)]
+    dw, dq, dk, dv, da, db = grads
+    ds0 = torch.empty((B, H, N, N), dtype=torch.float32, device=q.device) if want_ds0 else None
+    P = _lib.ptr
+    _lib.call("rwkv7_wkv_train_backward", _lib.dtype_code(q.dtype), B, T, H, P(q), P(w), P(k), P(v), P(a), P(b),
+              P(dy), P(ckpt), P(sa), P(ds_in), P(dq), P(dw), P(dk), P(dv), P(da), P(db), P(ds0),
+              _lib.stream_of(q))
+    return dw, dq, dk, dv, da, db, ds0
+
+
+class WindBackstepping(torch.autograd.Function):
+    """``wkv_loader.py:309-334``: forward saves the inputs, the state checkpoints
+    and sa; backward returns bf16 gradients of (w, q, k, v, z, b)."""
+
+    @staticmethod
+    def forward(ctx, w, q, k, v, z, b):
+        B, T, H, C = w.shape
+        assert T % CHUNK_LEN == 0, f"Sequence length {T} must be divisible by {CHUNK_LEN}"
+        w, q, k, v, z, b = [i.to(torch.bfloat16) if i.dtype != torch.bfloat16 else i
+                            for i in [w, q, k, v, z, b]]
+        assert all(i.is_contiguous() for i in [w, q, k, v, z, b])
+        y, ckpt, sa = _train_forward(w, q, k, v, z, b)
+        ctx.save_for_backward(w, q, k, v, z, b, ckpt, sa)
+        return y
+
+    @staticmethod
+    def backward(ctx, *grad_outputs):
+        (dy,) = grad_outputs
+        assert dy.dtype == torch.bfloat16
+        dy = dy.contiguous()
+        w, q, k, v, z, b, ckpt, sa = ctx.saved_tensors
+        dw, dq, dk, dv, dz, db, _ = _train_backward(w, q, k, v, z, b, dy, ckpt, sa)
+        return dw, dq, dk, dv, dz, db
+
+
+def _make_train_op(head_size: int) -> Callable:
+    def RUN_CUDA_RWKV7g(q, w, k, v, a, b):
+        """``wkv_loader.py:336-349``: inputs ``[B, T, H*64]``, output bf16 ``[B, T, H*64]``."""
+        B, T, HC = q.shape
+        q, w, k, v, a, b = [i.to(torch.bfloat16) if i.dtype != torch.bfloat16 else i for i in [q, w, k, v, a, b]]
+        if not q.is_cuda:
+            raise RuntimeError("the WKV7 training operator runs on the HIP library only: inputs must be on a GPU")
+        q, w, k, v, a, b = [i.view(B, T, HC // head_size, head_size) for i in [q, w, k, v, a, b]]
+        y = WindBackstepping.apply(w, q, k, v, a, b)
+        return torch.reshape(y, (B, T, HC))
+    return RUN_CUDA_RWKV7g
+
+
+def load_hip_operator_train(head_size: int = HEAD_SIZE) -> Callable:
+    """Counterpart of ``load_cuda_operator_train`` (``wkv_loader.py:201-356``)."""
+    global _train_op
+    if head_size != HEAD_SIZE:
+        raise RuntimeError(f"head_size {head_size} not supported (library is built for {HEAD_SIZE})")
+    if _train_op is not None:
+        return _train_op
+    with _op_lock:
+        if _train_op is None:
+            _lib.load()
+            _train_op = _make_train_op(head_size)
+    return _train_op
+
+
+class WKV7InfctxFunction(torch.autograd.Function):
+    """``operators/wkv_infctx.py:18-160``: forward saves the inputs and the initial
+    state; backward recomputes the forward's checkpoints and runs the backward
+    pass with the incoming final-state gradient."""
+
+    @staticmethod
+    def forward(ctx, w, q, k, v, a, b, state):
+        B, T, H, C = q.shape
+        if state is None:
+            state = torch.zeros(B, H, C, C, dtype=torch.float32, device=q.device)
+        if state.dtype != torch.float32:
+            state = state.to(torch.float32)
+        state = state.contiguous()
+        s = torch.empty_like(state)
+        y, _, _ = _train_forward(w, q, k, v, a, b, s0=state, s_out=s)
+        ctx.save_for_backward(w, q, k, v, a, b, state)
+        return y, s
+
+    @staticmethod
+    def backward(ctx, dy, dstate_out):
+        w, q, k, v, a, b, s0 = ctx.saved_tensors
+        dy = dy.contiguous()
+        ds_in = None if dstate_out is None else dstate_out.to(torch.float32).contiguous()
+        _, ckpt, sa = _train_forward(w, q, k, v, a, b, s0=s0)
+        dw, dq, dk, dv, da, db, ds0 = _train_backward(w, q, k, v, a, b, dy, ckpt, sa, ds_in=ds_in, want_ds0=True)
+        return dw, dq, dk, dv, da, db, ds0
+
+
+def rwkv7_wkv_infctx(w, q, k, v, a, b, state=None, scale: float = 1.0):
+    """``operators/wkv_infctx.py:164-210``: ``[B, T, H, 64]`` inputs (cast to q's
+    dtype), optional float32 initial state ``[B, H, 64, 64]``; returns
+    ``(y, final_state)``."""
+    if scale != 1.0:
+        q = q * scale
+    B, T, H, C = q.shape
+    if state is None:
+        state = torch.zeros(B, H, C, C, dtype=torch.float32, device=q.device)
+    if not q.is_cuda:
+        raise RuntimeError("the WKV7 infctx operator runs on the HIP library only: inputs must be on a GPU")
+    if q.dtype not in _lib.DTYPE_CODE:
+        raise RuntimeError(f"Unsupported dtype for the infctx operator: {q.dtype}")
+    dt = q.dtype
+    w, k, v, a, b = (x.to(dt).contiguous() for x in (w, k, v, a, b))
+    q = q.contiguous()
+    return WKV7InfctxFunction.apply(w, q, k, v, a, b, state)
+
+
+class _InfctxModule:
+    """The raw ``forward`` / ``backward`` of ``wkv7_infctx_op``
+    (``wkv7_infctx_op.cpp``), in place on caller-owned tensors."""
+
+    @staticmethod
+    def forward(w, q, k, v, a, b, s, y):
+        """y <- WKV7 from initial state s; s <- final state (float32, in place)."""
+        out, _, _ = _train_forward(w, q, k, v, a, b, s0=s, s_out=s)
+        y.copy_(out)
+
+    @staticmethod
+    def backward(w, q, k, v, a, b, dy, s0, ds_in, dw, dq, dk, dv, da, db, ds):
+        ds_in = ds_in if (ds_in is not None and ds_in.numel() > 0) else None
+        _, ckpt, sa = _train_forward(w, q, k, v, a, b, s0=s0)
+        g = _train_backward(w, q, k, v, a, b, dy.contiguous(), ckpt, sa, ds_in=ds_in, want_ds0=True)
+        for dst, src in zip((dw, dq, dk, dv, da, db, ds), g):
+            dst.copy_(src)
+
+
+def load_hip_operator_infctx():
+    """Counterpart of ``load_cuda_operator_infctx`` (``wkv_loader.py:588-705``)."""
+    global _infctx_op
+    if _infctx_op is None:
+        with _op_lock:
+            if _infctx_op is None:
+                _lib.load()
+                _infctx_op = _InfctxModule()
+    return _infctx_op
+
+
 def load_wkv_operator(device: str = "cuda", for_inference: bool = False,
                       head_size: int = HEAD_SIZE) -> Callable:
     if device == "cpu":
@@ -127,12 +308,14 @@ def load_wkv_operator(device: str = "cuda", for_inference: bool = False,
     if device == "cuda":
         if for_inference:
             return load_hip_operator_inference(head_size)
-        raise NotImplementedError(
-            "the training WKV7 operator (for_inference=False) is not part of this library")
+        return load_hip_operator_train(head_size)
     raise ValueError(f"Unsupported device type: {device}, only 'cpu' or 'cuda' supported")
 
 
 load_wkv7_operator = load_wkv_operator
+load_cuda_operator_train = load_hip_operator_train
+load_cuda_operator_inference = load_hip_operator_inference
+load_cuda_operator_infctx = load_hip_operator_infctx
 
 
 def rwkv7_wkv(q, w, k, v, a, b, head_size=HEAD_SIZE, state=None, return_state=False):
@@ -141,7 +324,9 @@ def rwkv7_wkv(q, w, k, v, a, b, head_size=HEAD_SIZE, state=None, return_state=Fa
         device_type = "cuda" if q.is_cuda else "cpu"
     for_inference = (state is not None) or return_state
     operator = load_wkv_operator(device=device_type, for_inference=for_inference, head_size=head_size)
-    return operator(q, w, k, v, a, b, state, return_state)
+    if for_inference:
+        return operator(q, w, k, v, a, b, state, return_state)
+    return operator(q, w, k, v, a, b)
 
 
 # ---------------------------------------------------------------------------

@@ -128,3 +128,31 @@ def test_partials_host_side_errors(lib):
     assert lib.rwkv7_shift_mix(*row, P(18), 1, 0, *rest) == 1  # misaligned planes
     assert lib.rwkv7_shift_mix(*row, fake, 65, 32, *rest) == 1  # too many planes
     assert lib.rwkv7_final_norm(2, 4, 8, fake, fake, 2, 4, None, fake, fake, fake, None) == 1
+
+
+def test_train_host_side_errors(lib):
+    P = ctypes.c_void_p
+    fake = P(16)
+    assert lib.rwkv7_wkv_train_ckpt_floats(2, 33, 3) == 2 * 3 * 3 * 64 * 64
+    assert lib.rwkv7_wkv_train_ckpt_floats(2, 33, 0) == -1
+    ins = [fake] * 7  # r, w, k, v, a, b, y
+    assert lib.rwkv7_wkv_train_forward(7, 1, 16, 1, *ins, None, None, fake, fake, None) == 1  # dtype
+    assert lib.rwkv7_wkv_train_forward(2, 1, 16, 1, *ins, None, None, None, fake, None) == 1  # no ckpt
+    assert lib.rwkv7_wkv_train_forward(2, 1, 16, 1, *ins, P(20), None, fake, fake, None) == 1  # misaligned s0
+    assert b"aligned" in lib.rwkv7_last_error()
+    assert lib.rwkv7_wkv_train_forward(2, 0, 16, 1, *ins, None, None, None, None, None) == 0  # empty batch
+    grads = [fake] * 6
+    assert lib.rwkv7_wkv_train_backward(2, 1, 16, 1, *[fake] * 7, fake, fake, None, *grads[:5], None, None,
+                                        None) == 1  # null db
+
+
+def test_training_operator_needs_gpu_tensors():
+    import torch
+    from rwkvtune_amd import operators as ops
+    op = ops.load_wkv_operator(device="cuda", for_inference=False)
+    assert op is ops.load_cuda_operator_train()
+    x = torch.zeros(1, 16, 64)
+    with pytest.raises(RuntimeError, match="GPU"):
+        op(x, x, x, x, x, x)
+    with pytest.raises(RuntimeError, match="GPU"):
+        ops.rwkv7_wkv_infctx(*(x.view(1, 16, 1, 64),) * 6)
