@@ -15,21 +15,61 @@
 //     always the first token (core.py:214-228); logp = log_softmax(filtered)[token].
 //
 // Design: one 1024-thread block per row; the row (V <= 65536) lives in registers,
-// 64 values per thread, element i = j*1024 + tid.  The k-th largest value and the
-// nucleus boundary are found by bisection over the order-preserving integer
-// encoding of the float values (32 block reductions each), so no sort and no
-// scratch memory.  Sampling draws u from a counter-based hash of (seed, row key,
-// row counter) and walks the kept tokens in a fixed order (thread-major); ties at
-// a threshold are kept together (the reference's sort keeps an arbitrary subset).
+// 64 values per thread, read with 16-byte loads (layout at load_row).  A token is the bit pattern of
+// its unnormalised probability q = exp(l - max) (orders like the logit).  The
+// k-th largest key and the nucleus boundary are found by a three-level radix
+// select over the keys (11, 10 and 10 bits: 1024 LDS bins per level, built with
+// LDS atomics, then one block scan from the top bin down), counting tokens for
+// top-k and summing their probability in 31-bit fixed point (q * 2^31, 64-bit
+// sums: integer, so the result does not depend on the order of the atomics) for
+// top-p.  Sampling draws u from a counter-based hash of (seed, row key, row
+// counter) and walks the kept tokens in a fixed order (thread-major); ties at a
+// threshold are kept together (the reference's sort keeps an arbitrary subset).
 #include "common.hpp"
 
 namespace {
 
+// sample_kernel and greedy_kernel: 1024 threads x 64 values
 constexpr int kT = 1024;
 constexpr int kVPT = 64;  // values per thread
-constexpr int kW = kT / 64;
+constexpr int kTG = 1024, kVPTG = 64;
+constexpr int kWMax = 16;  // waves of the larger block
+constexpr int kBins = 1024;  // radix bins per level (one per thread)
 
 enum { RULE_BATCH = 0, RULE_SINGLE = 1 };
+
+// Row layout in registers: thread t holds x[8c + e] = element 8192 c + 8 t + e
+// (c < 8, e < 8), so each group of 8 is one 16-byte load of a 16-bit row.
+constexpr int kGroup = 8, kStride = kT * kGroup;
+__device__ __forceinline__ int elem_of(int j, int tid) { return (j / kGroup) * kStride + tid * kGroup + (j % kGroup); }
+__device__ __forceinline__ int owner_of(int i) { return (i % kStride) / kGroup; }
+__device__ __forceinline__ int slot_of(int i) { return (i / kStride) * kGroup + (i % kGroup); }
+
+// the row's values with entries past vmax (banned ids and padding) as -inf;
+// whole in-range groups of an aligned row are read with one 16-byte load
+// (two for float32)
+template <typename LT>
+__device__ __forceinline__ void load_row(const LT* lg, int vmax, float (&x)[kVPT]) {
+    typedef io_traits<LT> tr;
+    const int tid = threadIdx.x;
+    const bool vec = (((uintptr_t)lg) & 15) == 0;
+#pragma unroll
+    for (int c = 0; c < kVPT / kGroup; ++c) {
+        const int i0 = c * kStride + tid * kGroup;
+        if (vec && i0 + kGroup - 1 <= vmax) {
+            const f32x4 a = tr::load4(lg + i0), b = tr::load4(lg + i0 + 4);
+            x[c * kGroup + 0] = a.x; x[c * kGroup + 1] = a.y; x[c * kGroup + 2] = a.z; x[c * kGroup + 3] = a.w;
+            x[c * kGroup + 4] = b.x; x[c * kGroup + 5] = b.y; x[c * kGroup + 6] = b.z; x[c * kGroup + 7] = b.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < kGroup; ++e)
+                x[c * kGroup + e] = (i0 + e <= vmax) ? tr::to_f32(lg[i0 + e]) : -INFINITY;
+        }
+    }
+}
+
+// exp(x) as one v_exp_f32 of x * log2(e) (a few ulp: sampling weights)
+__device__ __forceinline__ float fast_exp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
 
 __device__ __forceinline__ uint32_t okey(float f) {
     const uint32_t u = __float_as_uint(f);
@@ -64,9 +104,8 @@ __device__ __forceinline__ float wave_reduce_max(float v) {
 }
 
 struct Red {
-    float f[kW];
-    unsigned u[kW];
-    double d[kW];
+    float f[kWMax];
+    unsigned u[kWMax];
 };
 
 __device__ float block_sum_f(float v, Red* red) {
@@ -76,7 +115,7 @@ __device__ float block_sum_f(float v, Red* red) {
     __syncthreads();
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < kW; ++i) s += red->f[i];
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s += red->f[i];
     return s;
 }
 
@@ -87,7 +126,7 @@ __device__ float block_max_f(float v, Red* red) {
     __syncthreads();
     float s = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kW; ++i) s = fmaxf(s, red->f[i]);
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s = fmaxf(s, red->f[i]);
     return s;
 }
 
@@ -98,8 +137,26 @@ __device__ unsigned block_sum_u(unsigned v, Red* red) {
     __syncthreads();
     unsigned s = 0;
 #pragma unroll
-    for (int i = 0; i < kW; ++i) s += red->u[i];
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s += red->u[i];
     return s;
+}
+
+// inclusive prefix sum over the block in thread order (wave scans, then the
+// wave totals); `wsum` holds one entry per wave
+template <typename T>
+__device__ T block_incl_scan(T v, T* wsum) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const T n = __shfl_up(v, o, 64);
+        if (lane >= o) v += n;
+    }
+    __syncthreads();  // wsum of a previous scan has been read
+    if (lane == 63) wsum[w] = v;
+    __syncthreads();
+    T off = 0;
+    for (int i = 0; i < w; ++i) off += wsum[i];
+    return v + off;
 }
 
 // argmax with the lowest index on ties: pack (key, ~index) into 64 bits
@@ -114,8 +171,59 @@ __device__ unsigned long long block_max_u64(unsigned long long v, unsigned long 
     __syncthreads();
     unsigned long long s = 0;
 #pragma unroll
-    for (int i = 0; i < kW; ++i) s = red[i] > s ? red[i] : s;
+    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s = red[i] > s ? red[i] : s;
     return s;
+}
+
+// One level of the radix select.  Tokens with key >= lo whose bits above
+// `shift + 10` equal `prefix` (all of them when `first`) are binned by bits
+// shift .. shift+9 of the key; a bin holds their count (COUNT) or their mass in
+// fixed point (q * 2^31, truncated).  Walking the bins from the top, starting
+// from `above` (the amount in the higher bins of earlier levels), the selected
+// bin is the one where the running total first exceeds `target` (COUNT: first
+// reaches it).  `frac` > 0 sets target = frac * (this level's total) first (the
+// nucleus: the first level bins every kept token).  Returns the bin; `above`
+// becomes the amount in the bins above it.
+template <bool COUNT>
+__device__ uint32_t radix_level(const uint32_t (&key)[kVPT], uint32_t lo, int shift, uint32_t prefix, bool first,
+                                unsigned long long& above, unsigned long long& target, float frac,
+                                unsigned long long* bins, unsigned long long* wsum, int* pick_bin,
+                                unsigned long long* pick_val) {
+    const int tid = threadIdx.x;
+    static_assert(kBins == kT, "one bin per thread");
+    bins[tid] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < kVPT; ++j) {
+        const uint32_t kj = key[j];
+        const bool in = kj >= lo && (first || (kj >> (shift + 10)) == prefix);
+        if (in) {
+            const unsigned long long add =
+                COUNT ? 1ull : (unsigned long long)(uint32_t)(__uint_as_float(kj) * 2147483648.0f);
+            atomicAdd(&bins[(kj >> shift) & 1023], add);
+        }
+    }
+    __syncthreads();
+    const uint32_t b = kBins - 1 - tid;  // thread 0 takes the top bin
+    const unsigned long long val = bins[b];
+    const unsigned long long incl = block_incl_scan(val, wsum);
+    if (frac > 0.f) {
+        if (tid == kT - 1) *pick_val = incl;  // the level's total
+        __syncthreads();
+        target = (unsigned long long)((double)frac * (double)(*pick_val));
+        __syncthreads();
+    }
+    const unsigned long long lo_sum = above + incl - val, hi_sum = above + incl;
+    const bool hit = COUNT ? (hi_sum >= target && lo_sum < target) : (hi_sum > target && lo_sum <= target);
+    if (hit) {
+        *pick_bin = (int)b;
+        *pick_val = lo_sum;
+    }
+    __syncthreads();
+    above = *pick_val;
+    const uint32_t r = (uint32_t)*pick_bin;
+    __syncthreads();  // pick_* are rewritten by the next level
+    return r;
 }
 
 template <typename LT>
@@ -129,8 +237,11 @@ __global__ __launch_bounds__(kT) void sample_kernel(
 {
     typedef io_traits<LT> tr;
     __shared__ Red red;
-    __shared__ unsigned long long red64[kW];
-    __shared__ float thread_mass[kT];
+    __shared__ unsigned long long bins[kBins];
+    __shared__ unsigned long long wsum[kWMax];
+    __shared__ float fsum[kWMax];
+    __shared__ int pick_bin;
+    __shared__ unsigned long long pick_val;
     __shared__ int pick;
     const int row = blockIdx.x;
     if (active != nullptr && active[row] == 0) return;  // whole block
@@ -138,28 +249,27 @@ __global__ __launch_bounds__(kT) void sample_kernel(
     const LT* lg = logits + (size_t)row * ld;
     const int vmax = max_valid_id < V - 1 ? max_valid_id : V - 1;
 
-    float x[kVPT];
-#pragma unroll
-    for (int j = 0; j < kVPT; ++j) {
-        const int i = j * kT + tid;
-        x[j] = (i <= vmax) ? tr::to_f32(lg[i]) : -INFINITY;  // banned and padding: -inf
-    }
-
     const float temp = temperature[row];
     if (!(temp >= 1e-6f)) return;  // greedy rows belong to greedy_kernel
-    // temperature, then logit bias (clamped), core.py:86-95
+    float x[kVPT];
+    load_row(lg, vmax, x);  // banned and padding: -inf
+    // temperature (a multiply by its reciprocal: within an ulp of the division),
+    // then logit bias (clamped), core.py:86-95
+    if (temp != 1.0f) {
+        const float it = 1.0f / temp;
 #pragma unroll
-    for (int j = 0; j < kVPT; ++j) x[j] = x[j] / temp;
+        for (int j = 0; j < kVPT; ++j) x[j] *= it;
+    }
     if (bias_off != nullptr) {
         const int b0 = bias_off[row], b1 = bias_off[row + 1];
         for (int q = b0; q < b1; ++q) {
             const int id = bias_ids[q];
-            if (id >= 0 && id < V && (id % kT) == tid) {
+            if (id >= 0 && id < V && owner_of(id) == tid) {
                 const float bv = fminf(100.f, fmaxf(-100.f, bias_val[q]));
                 // static register index: unrolled select
 #pragma unroll
                 for (int j = 0; j < kVPT; ++j)
-                    if (j == id / kT) x[j] += bv;
+                    if (j == slot_of(id)) x[j] += bv;
             }
         }
     }
@@ -168,18 +278,15 @@ __global__ __launch_bounds__(kT) void sample_kernel(
 #pragma unroll
     for (int j = 0; j < kVPT; ++j) mm = fmaxf(mm, x[j]);
     const float mx = block_max_f(mm, &red);
-    // From here on a token is its key: the bit pattern of its unnormalised
-    // probability q = exp(l - max) >= 0 (0 for banned and padding entries).  For
-    // non-negative floats the bit pattern orders like the value, so keys order
-    // tokens like their logits, q is read back by reinterpreting the key (no
-    // instruction, nothing for the compiler to hoist), and one 32-bit register
-    // per token keeps the row resident.
+    // From here on a token is its key: the bit pattern of q = exp(l - max) >= 0
+    // (0 for banned and padding entries), which orders like the logit; q is read
+    // back by reinterpreting the key, and one register per token keeps the row.
     uint32_t key[kVPT];
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < kVPT; ++j) {
-        const float q = (x[j] == -INFINITY) ? 0.f : expf(x[j] - mx);
-        key[j] = __float_as_uint(q);  // padding: q = 0
+        const float q = (x[j] == -INFINITY) ? 0.f : fminf(fast_exp(x[j] - mx), 1.0f);
+        key[j] = __float_as_uint(q);
         s += q;
     }
     const float Z = block_sum_f(s, &red);
@@ -191,15 +298,15 @@ __global__ __launch_bounds__(kT) void sample_kernel(
     const int k = top_k[row];
     const float p = top_p[row];
     if (!uniform && k > 0 && k < V) {
-        // largest K with count(key >= K) >= k  (the k-th largest value)
-        uint32_t K = 0;
-        for (int bit = 31; bit >= 0; --bit) {
-            const uint32_t cand = K | (1u << bit);
-            unsigned c = 0;
-#pragma unroll
-            for (int j = 0; j < kVPT; ++j) c += key[j] >= cand ? 1u : 0u;
-            if (block_sum_u(c, &red) >= (unsigned)k) K = cand;
-        }
+        // the k-th largest key: the highest K with count(key >= K) >= k
+        unsigned long long above = 0, target = (unsigned long long)k;
+        const uint32_t b1 = radix_level<true>(key, 0u, 20, 0u, true, above, target, 0.f, bins, wsum, &pick_bin,
+                                              &pick_val);
+        const uint32_t b2 = radix_level<true>(key, 0u, 10, b1, false, above, target, 0.f, bins, wsum, &pick_bin,
+                                              &pick_val);
+        const uint32_t b3 = radix_level<true>(key, 0u, 0, (b1 << 10) | b2, false, above, target, 0.f, bins, wsum,
+                                              &pick_bin, &pick_val);
+        const uint32_t K = (b1 << 20) | (b2 << 10) | b3;
         lo = K > 1u ? K : 1u;
         float sk = 0.f;
 #pragma unroll
@@ -208,19 +315,16 @@ __global__ __launch_bounds__(kT) void sample_kernel(
     }
     const bool nucleus = !uniform && p < 1.0f && (rule == RULE_BATCH || k <= 0);
     if (nucleus) {
-        // largest K' with mass(key >= max(K', lo)) > p * W: the key of the token
-        // whose inclusion crosses p.  The mass counts only top-k survivors, so the
-        // predicate holds for every K' <= lo and the bisection starts from 0.
-        const float target = p * W;
-        uint32_t K = 0;
-        for (int bit = 31; bit >= 0; --bit) {
-            const uint32_t cand = K | (1u << bit);
-            const uint32_t thr = cand > lo ? cand : lo;
-            float ms = 0.f;
-#pragma unroll
-            for (int j = 0; j < kVPT; ++j) ms += key[j] >= thr ? __uint_as_float(key[j]) : 0.f;
-            if (block_sum_f(ms, &red) > target) K = cand;
-        }
+        // the key of the token whose inclusion crosses p: the highest K' with
+        // mass(key >= max(K', lo)) > p * mass(key >= lo), in fixed point
+        unsigned long long above = 0, target = 0;
+        const uint32_t b1 = radix_level<false>(key, lo, 20, 0u, true, above, target, fmaxf(p, 1e-30f), bins, wsum,
+                                               &pick_bin, &pick_val);
+        const uint32_t b2 = radix_level<false>(key, lo, 10, b1, false, above, target, 0.f, bins, wsum, &pick_bin,
+                                               &pick_val);
+        const uint32_t b3 = radix_level<false>(key, lo, 0, (b1 << 10) | b2, false, above, target, 0.f, bins, wsum,
+                                               &pick_bin, &pick_val);
+        const uint32_t K = (b1 << 20) | (b2 << 10) | b3;
         // RULE_SINGLE keeps the crossing token, RULE_BATCH stops before it but
         // always keeps the most probable token (q = 1)
         uint32_t nlo = (rule == RULE_SINGLE) ? K : K + 1u;
@@ -246,22 +350,13 @@ __global__ __launch_bounds__(kT) void sample_kernel(
     float tm = 0.f;
 #pragma unroll
     for (int j = 0; j < kVPT; ++j) tm += key[j] >= lo ? __uint_as_float(key[j]) : 0.f;
-    thread_mass[tid] = tm;
     if (tid == 0) pick = -1;
+    const float acc = block_incl_scan(tm, fsum);  // [before, acc) of consecutive threads tile [0, total)
+    if (tid == kT - 1) fsum[0] = acc;             // total (fsum is free once every thread has its offset)
     __syncthreads();
-    // inclusive scan of the 1024 thread masses (Hillis-Steele in LDS)
-    float acc = tm;
-    for (int o = 1; o < kT; o <<= 1) {
-        const float add = tid >= o ? thread_mass[tid - o] : 0.f;
-        __syncthreads();
-        acc += add;
-        thread_mass[tid] = acc;
-        __syncthreads();
-    }
-    // [before, acc) of consecutive threads tile [0, total) exactly
-    const float total = thread_mass[kT - 1];
+    const float total = fsum[0];
     const float target = u * total;
-    const float before = tid > 0 ? thread_mass[tid - 1] : 0.f;
+    const float before = acc - tm;
     if (tm > 0.f && target >= before && (target < acc || acc >= total)) {
         // fully unrolled (no early exit) so key[] stays in registers
         float c = before;
@@ -271,7 +366,7 @@ __global__ __launch_bounds__(kT) void sample_kernel(
         for (int j = 0; j < kVPT; ++j) {
             const float w = key[j] >= lo ? __uint_as_float(key[j]) : 0.f;
             if (!done && w > 0.f) {
-                chosen = j * kT + tid;
+                chosen = elem_of(j, tid);
                 c += w;
                 done = c > target;
             }
@@ -280,48 +375,47 @@ __global__ __launch_bounds__(kT) void sample_kernel(
     }
     __syncthreads();
     const int tok = pick;
-    if (tok >= 0 && tid == (tok % kT)) {
+    if (tok >= 0 && tid == owner_of(tok)) {
         uint32_t kq = 0;
 #pragma unroll
         for (int j = 0; j < kVPT; ++j)
-            if (j == tok / kT) kq = key[j];
+            if (j == slot_of(tok)) kq = key[j];
         const float q = __uint_as_float(kq);
         out_tok[row] = tok;
         out_logp[row] = (rule == RULE_SINGLE) ? logf(q / W + 1e-10f) : logf(q) - logf(W);
     }
 }
 
-
 // Greedy rows (temperature < 1e-6, core.py:80-83, 184-188): argmax of the banned
 // logits with the lowest index on ties, logp = log_softmax(banned logits)[token].
 // A kernel of its own: sharing one kernel with the sampling path doubles its
 // register footprint.
 template <typename LT>
-__global__ __launch_bounds__(kT) void greedy_kernel(
+__global__ __launch_bounds__(kTG) void greedy_kernel(
     int M, int V, const LT* __restrict__ logits, int64_t ld, int max_valid_id,
     const float* __restrict__ temperature, const uint8_t* __restrict__ active,
     int64_t* __restrict__ out_tok, float* __restrict__ out_logp)
 {
     typedef io_traits<LT> tr;
     __shared__ Red red;
-    __shared__ unsigned long long red64[kW];
+    __shared__ unsigned long long red64[kWMax];
     const int row = blockIdx.x;
     if (active != nullptr && active[row] == 0) return;
     if (temperature[row] >= 1e-6f) return;  // sampled rows belong to sample_kernel
     const int tid = threadIdx.x;
     const LT* lg = logits + (size_t)row * ld;
     const int vmax = max_valid_id < V - 1 ? max_valid_id : V - 1;
-    float x[kVPT];
+    float x[kVPTG];
 #pragma unroll
-    for (int j = 0; j < kVPT; ++j) {
-        const int i = j * kT + tid;
+    for (int j = 0; j < kVPTG; ++j) {
+        const int i = j * kTG + tid;
         x[j] = (i <= vmax) ? tr::to_f32(lg[i]) : -INFINITY;
     }
     // padding is -inf at the highest indices, so it never wins a tie
     unsigned long long best = 0;
 #pragma unroll
-    for (int j = 0; j < kVPT; ++j) {
-        const unsigned i = (unsigned)(j * kT + tid);
+    for (int j = 0; j < kVPTG; ++j) {
+        const unsigned i = (unsigned)(j * kTG + tid);
         const unsigned long long c = ((unsigned long long)okey(x[j]) << 32) | (unsigned long long)(0xffffffffu - i);
         best = c > best ? c : best;
     }
@@ -329,11 +423,11 @@ __global__ __launch_bounds__(kT) void greedy_kernel(
     const int tok = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
     float mm = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kVPT; ++j) mm = fmaxf(mm, x[j]);
+    for (int j = 0; j < kVPTG; ++j) mm = fmaxf(mm, x[j]);
     const float mx = block_max_f(mm, &red);
     float s = 0.f;
 #pragma unroll
-    for (int j = 0; j < kVPT; ++j) s += (x[j] == -INFINITY) ? 0.f : expf(x[j] - mx);
+    for (int j = 0; j < kVPTG; ++j) s += (x[j] == -INFINITY) ? 0.f : expf(x[j] - mx);
     const float Z = block_sum_f(s, &red);
     if (tid == 0) {
         out_tok[row] = tok;
@@ -388,7 +482,7 @@ hipError_t launch_sample(int M, int V, const void* logits, int64_t ld, int rule,
                          const uint8_t* active, uint64_t seed, const int64_t* rng_key,
                          const int32_t* rng_ctr, int64_t* out_tok, float* out_logp, hipStream_t st)
 {
-    hipLaunchKernelGGL(greedy_kernel<LT>, dim3(M), dim3(kT), 0, st, M, V, (const LT*)logits, ld, max_valid_id,
+    hipLaunchKernelGGL(greedy_kernel<LT>, dim3(M), dim3(kTG), 0, st, M, V, (const LT*)logits, ld, max_valid_id,
                        temperature, active, out_tok, out_logp);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -422,3 +516,4 @@ hipError_t launch_rep_penalty(int M, int V, float* logits, int64_t ld, float pen
 }
 
 int sampler_max_vocab() { return kT * kVPT; }
+static_assert(kT * kVPT == kTG * kVPTG, "both kernels cover the same vocabulary");

@@ -112,6 +112,30 @@ def test_sampled_distribution(gpu_device, case):
     assert stat < chi2.ppf(0.999, max(dof, 1)), f"chi2 {stat:.1f} dof {dof}"
 
 
+@pytest.mark.parametrize("rule,top_p,top_k", [(osm.RULE_BATCH, 0.95, 0), (osm.RULE_SINGLE, 0.9, 0),
+                                               (osm.RULE_BATCH, 0.9, 3000), (osm.RULE_SINGLE, 1.0, 20000)])
+def test_flat_rows_kept_set(gpu_device, rule, top_p, top_k):
+    """Rows like a random-init model's (logits ~N(0, 1)): tens of thousands of
+    tokens share the probability, so every level of the threshold search sees
+    crowded bins.  Every draw lies in the oracle's kept set, and the draws reach
+    across it (the largest drawn rank is near the kept set's size)."""
+    print(f"[case] flat row rule={rule} p={top_p} k={top_k}", flush=True)
+    g = torch.Generator().manual_seed(31)
+    row = torch.randn(V, generator=g)
+    n = 8192
+    tok, lp = draws(gpu_device, row, n, temperature=1.0, top_p=top_p, top_k=top_k, rule=rule, max_valid_id=65529)
+    dist = osm.distribution(row, temperature=1.0, top_p=top_p, top_k=top_k, max_valid_id=65529, rule=rule)
+    kept = dist > 0
+    assert bool(kept[tok].all()), "a draw fell outside the kept set"
+    order = torch.argsort(row[:65530], descending=True)
+    rank = torch.empty(65530, dtype=torch.long)
+    rank[order] = torch.arange(65530)
+    assert int(rank[tok].max()) > 0.9 * int(kept.sum())
+    for i in range(0, n, 509):
+        t = int(tok[i])
+        assert abs(float(lp[i]) - osm.logp(dist, t, rule)) < 1e-4
+
+
 def test_bias_and_ban(gpu_device):
     print("[case] logit bias and ban", flush=True)
     row = peaked_row(7)
