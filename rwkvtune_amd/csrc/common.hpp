@@ -99,6 +99,19 @@ __device__ __forceinline__ float dpp_xor2(float x) {
 __device__ __forceinline__ float dpp_xor1(float x) {
     return __builtin_amdgcn_update_dpp(0.0f, x, 0xb1, 0xf, 0xf, false);
 }
+// Value of lane l ^ 16 / l ^ 32 (l = lane in the wave) by gfx950's
+// v_permlane16_swap / v_permlane32_swap with both operands x: the first swaps
+// odd 16-lane rows of its first operand with even rows of its second, so the
+// partner is the first result in odd rows and the second in even rows; the
+// second does the same for the upper and lower 32 lanes.
+__device__ __forceinline__ float lane_xor16(float x) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+}
+__device__ __forceinline__ float lane_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+}
 
 // Reduce-scatter over the 16 lanes of a DPP row.  Every lane of the row holds
 // 16 partial sums p[0..15]; on return, lane c of the row holds

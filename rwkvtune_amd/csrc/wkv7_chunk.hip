@@ -341,7 +341,6 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int KP = 72;  // bf16 row stride of planes whose K is 64 (144 B)
 constexpr int TQ = 40;  // bf16 row stride of planes whose K is 32 (80 B)
-constexpr int LWS = 72; // float row stride of the log-decay table
 
 struct __attribute__((aligned(16))) ChunkLds2 {
     uint16_t Rt[2][L][KP], At[2][L][KP], Kh[2][L][KP], Bh[2][L][KP];  // rows t, K = key j
@@ -352,9 +351,9 @@ struct __attribute__((aligned(16))) ChunkLds2 {
     float Sf[NH][SP];   // float32 state [i][j]
     float X[NH][TP];    // S a~^T + V^T A_ak  [i][t]
     float Aab[L][TP];   // [s][t], zero for s >= t
-    float LW[L][LWS];   // per-token log-decay, then its inclusive prefix  [t][j]
-    float tot[4][NH];
-    float DL[NH];
+    float tot[4][NH];   // per wave: log2-decay sums over its 8 tokens  [w][j]
+    float DL[NH];       // decay over the whole chunk
+    alignas(16) int slow[4];  // per wave: a token of the chunk decays below the floor
 };
 
 __device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
@@ -392,21 +391,21 @@ __device__ __forceinline__ bf16x8_t frag(const uint16_t* plane, int stride, int 
     return *reinterpret_cast<const bf16x8_t*>(plane + (row0 + (lane & 31)) * stride + k0 + 8 * (lane >> 5));
 }
 
+// Token-major planes ([row][t] with TQ stride: VT, KbT, BbT) keep their 16-byte
+// groups of 8 tokens XOR-swizzled by row bits 4-5.  Phase A's transposing stores
+// (a wave writes 4 consecutive words into each of 16 rows 4 apart) then reach 64
+// distinct banks instead of 16; a fragment read covers 16 consecutive rows with
+// one swizzle, so reads stay conflict-free.
+__device__ __forceinline__ int tswz(int row, int t) { return row * TQ + ((((t >> 3) ^ (row >> 4)) & 3) << 3) + (t & 7); }
+
+__device__ __forceinline__ bf16x8_t fragT(const uint16_t* plane, int row0, int k0, int lane) {
+    return *reinterpret_cast<const bf16x8_t*>(plane + tswz(row0 + (lane & 31), k0 + 8 * (lane >> 5)));
+}
+
 __device__ __forceinline__ f32x16 mfma3(f32x16 acc, bf16x8_t a0, bf16x8_t a1, bf16x8_t b0, bf16x8_t b1) {
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc, 0, 0, 0);
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc, 0, 0, 0);
-}
-
-// acc += A[rows a0..a0+31][K] . B[rows b0..b0+31][K]^T on hi/lo planes
-__device__ __forceinline__ f32x16 mma32(f32x16 acc, const uint16_t* A, int as, int aplane, int ar0,
-                                        const uint16_t* B, int bs, int bplane, int br0, int K, int lane) {
-    for (int k0 = 0; k0 < K; k0 += 16) {
-        const bf16x8_t a0 = frag(A, as, ar0, k0, lane), a1 = frag(A + aplane, as, ar0, k0, lane);
-        const bf16x8_t b0 = frag(B, bs, br0, k0, lane), b1 = frag(B + bplane, bs, br0, k0, lane);
-        acc = mfma3(acc, a0, a1, b0, b1);
-    }
-    return acc;
 }
 
 // Store accumulator C (= M^T of the stored matrix M) as hi/lo planes of M:
@@ -424,7 +423,7 @@ __device__ __forceinline__ void store_planes_T(uint16_t* P, int stride, int plan
     }
 }
 
-constexpr int RT_PLANE = L * KP, S_PLANE = NH * KP, T64_PLANE = NH * TQ, T32_PLANE = L * TQ;
+constexpr int RT_PLANE = L * KP, S_PLANE = NH * KP, T32_PLANE = L * TQ;
 
 // The 16-bit kernel keeps log-decays in base 2, so every exponential is one
 // v_exp_f32 (about 1 ulp for the arguments here, all >= -58).  Their accuracy is
@@ -480,7 +479,8 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
         }
     }
 
-    // phase-A mapping: tokens 2*tp, 2*tp+1 of the chunk, channels 4*c4 .. +3
+    // phase-A mapping: tokens 2*tp, 2*tp+1 of the chunk, channels 4*c4 .. +3; the 16
+    // lanes of a row read one 128-byte token row of the head
     const int tp = tid >> 4, c4 = tid & 15, j0 = 4 * c4;
     uint2 raw[6][2];  // r, w, k, v, a, b of this thread's two tokens (zero past the end)
     auto fetch = [&](int t0c) {
@@ -501,57 +501,59 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
 
     for (int t0 = tb; t0 < te; t0 += L) {
         const int n = min(L, te - t0);
-        // ---- A1: log-decay of the chunk, strong-decay test ----------------------
+        // ---- A1: log2-decays of the thread's two tokens, their prefix over the chunk
+        // (pair sums scanned over the wave's 4 lane rows = tokens 8w .. 8w+7 by lane
+        // swaps, then the four wave totals through LDS), strong-decay test ---------
         bool slow = false;
+        f32x4 lw[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
             const int t = 2 * tp + e;
             const f32x4 wv = unpack4<IO>(raw[1][e]);
-            f32x4 lw;  // log2 of the decay exp(-exp(w))
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 const float x = t < n ? -ex2(wv[c] * kLog2e) * kLog2e : 0.f;
                 slow |= !(x >= kLog2DecayFloor);
-                lw[c] = x;
+                lw[e][c] = x;
             }
-            *reinterpret_cast<f32x4*>(&sm.LW[t][j0]) = lw;
         }
-        const bool any_slow = __syncthreads_or(slow) != 0;
+        f32x4 inc, exc;  // inclusive / exclusive prefix of the pair sums over the wave's 4 rows
+        const int g = lane >> 4;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const float x = lw[0][c] + lw[1][c];
+            const float p1 = lane_xor16(x);  // row g ^ 1
+            const float p2 = lane_xor32(x + p1);  // rows (g ^ 2) & 2 and + 1
+            exc[c] = (g >= 2 ? p2 : 0.f) + ((g & 1) ? p1 : 0.f);
+            inc[c] = exc[c] + x;
+        }
+        if (g == 3) *reinterpret_cast<f32x4*>(&sm.tot[wave][j0]) = inc;
+        const bool wave_slow = __ballot(slow) != 0;
+        if (lane == 0) sm.slow[wave] = wave_slow ? 1 : 0;
+        __syncthreads();
+        const int4 sl = *reinterpret_cast<const int4*>(sm.slow);
+        const bool any_slow = (sl.x | sl.y | sl.z | sl.w) != 0;
 
         if (!any_slow) {
-            // ---- A2: inclusive prefix over the chunk per key (4 segments of 8) ----
+            // ---- A2: scaled operands as hi/lo planes ------------------------------
             {
-                const int seg = tid >> 6, j = lane;
-                float pre[8], acc = 0.f;
-#pragma unroll
-                for (int u = 0; u < 8; ++u) {
-                    acc += sm.LW[8 * seg + u][j];
-                    pre[u] = acc;
-                }
-                sm.tot[seg][j] = acc;
-                __syncthreads();
-                float off = 0.f, all = 0.f;
+                f32x4 base = {0.f, 0.f, 0.f, 0.f}, all = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    const float tq = sm.tot[q][j];
-                    off += q < seg ? tq : 0.f;
+                    const f32x4 tq = *reinterpret_cast<const f32x4*>(&sm.tot[q][j0]);
+                    if (q < wave) base += tq;
                     all += tq;
                 }
-#pragma unroll
-                for (int u = 0; u < 8; ++u) sm.LW[8 * seg + u][j] = pre[u] + off;
-                if (seg == 0) sm.DL[j] = ex2(all);
-                __syncthreads();
-            }
-            // ---- A3: scaled operands as hi/lo planes ------------------------------
-            {
+                if (tp == 0) *reinterpret_cast<f32x4*>(&sm.DL[j0]) = f32x4{ex2(all.x), ex2(all.y), ex2(all.z), ex2(all.w)};
+                const f32x4 ld_before = base + exc;  // log2 D of the token before 2tp
+                const f32x4 ld_first = ld_before + lw[0];
                 f32x4 vv[2], kb[2], bb[2];
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
                     const int t = 2 * tp + e;
-                    const f32x4 ld = *reinterpret_cast<const f32x4*>(&sm.LW[t][j0]);
-                    const f32x4 ldm = t > 0 ? *reinterpret_cast<const f32x4*>(&sm.LW[t > 0 ? t - 1 : 0][j0])
-                                            : f32x4{0.f, 0.f, 0.f, 0.f};
-                    const f32x4 ldl = *reinterpret_cast<const f32x4*>(&sm.LW[L - 1][j0]);
+                    const f32x4 ld = e == 0 ? ld_first : ld_first + lw[1];
+                    const f32x4 ldm = e == 0 ? ld_before : ld_first;
+                    const f32x4 ldl = all;
                     const f32x4 rv = unpack4<IO>(raw[0][e]), kv = unpack4<IO>(raw[2][e]);
                     const f32x4 av = unpack4<IO>(raw[4][e]), bv = unpack4<IO>(raw[5][e]);
                     vv[e] = unpack4<IO>(raw[3][e]);
@@ -587,14 +589,14 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                     const int j = j0 + c;
                     uint32_t hi, lo;
                     split2(vv[0][c], vv[1][c], hi, lo);
-                    *reinterpret_cast<uint32_t*>(&sm.VT[0][j][2 * tp]) = hi;
-                    *reinterpret_cast<uint32_t*>(&sm.VT[1][j][2 * tp]) = lo;
+                    *reinterpret_cast<uint32_t*>(&sm.VT[0][0][0] + tswz(j, 2 * tp)) = hi;
+                    *reinterpret_cast<uint32_t*>(&sm.VT[1][0][0] + tswz(j, 2 * tp)) = lo;
                     split2(kb[0][c], kb[1][c], hi, lo);
-                    *reinterpret_cast<uint32_t*>(&sm.KbT[0][j][2 * tp]) = hi;
-                    *reinterpret_cast<uint32_t*>(&sm.KbT[1][j][2 * tp]) = lo;
+                    *reinterpret_cast<uint32_t*>(&sm.KbT[0][0][0] + tswz(j, 2 * tp)) = hi;
+                    *reinterpret_cast<uint32_t*>(&sm.KbT[1][0][0] + tswz(j, 2 * tp)) = lo;
                     split2(bb[0][c], bb[1][c], hi, lo);
-                    *reinterpret_cast<uint32_t*>(&sm.BbT[0][j][2 * tp]) = hi;
-                    *reinterpret_cast<uint32_t*>(&sm.BbT[1][j][2 * tp]) = lo;
+                    *reinterpret_cast<uint32_t*>(&sm.BbT[0][0][0] + tswz(j, 2 * tp)) = hi;
+                    *reinterpret_cast<uint32_t*>(&sm.BbT[1][0][0] + tswz(j, 2 * tp)) = lo;
                 }
             }
         }
@@ -688,8 +690,12 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
         // ---- C: X^T += A_ak^T V (waves 0/1); state tiles start (waves 2/3) --------
         f32x16 accS0 = zero16, accS1 = zero16;  // waves 2/3: S^T tiles (j tile 0 / 1, i tile wave-2)
         if (wave < 2) {
-            accX = mma32(accX, &sm.AakT[0][0][0], TQ, T32_PLANE, 0, &sm.VT[0][0][0], TQ, T64_PLANE, 32 * wave, L,
-                         lane);
+            for (int k0 = 0; k0 < L; k0 += 16) {
+                const bf16x8_t a0 = frag(&sm.AakT[0][0][0], TQ, 0, k0, lane), a1 = frag(&sm.AakT[1][0][0], TQ, 0, k0, lane);
+                const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * wave, k0, lane);
+                const bf16x8_t v1 = fragT(&sm.VT[1][0][0], 32 * wave, k0, lane);
+                accX = mfma3(accX, a0, a1, v0, v1);
+            }
             // X[i][t]: lane holds i = 32*wave + l%32, t = 8g + 4(l/32) + 0..3
             const int i = 32 * wave + (lane & 31);
 #pragma unroll
@@ -714,10 +720,10 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
             }
             // S^T[j][i] += kbar_j . v_i over the chunk's tokens
             for (int k0 = 0; k0 < L; k0 += 16) {
-                const bf16x8_t v0 = frag(&sm.VT[0][0][0], TQ, 32 * ir, k0, lane);
-                const bf16x8_t v1 = frag(&sm.VT[1][0][0], TQ, 32 * ir, k0, lane);
-                const bf16x8_t k00 = frag(&sm.KbT[0][0][0], TQ, 0, k0, lane), k01 = frag(&sm.KbT[1][0][0], TQ, 0, k0, lane);
-                const bf16x8_t k10 = frag(&sm.KbT[0][0][0], TQ, 32, k0, lane), k11 = frag(&sm.KbT[1][0][0], TQ, 32, k0, lane);
+                const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * ir, k0, lane);
+                const bf16x8_t v1 = fragT(&sm.VT[1][0][0], 32 * ir, k0, lane);
+                const bf16x8_t k00 = fragT(&sm.KbT[0][0][0], 0, k0, lane), k01 = fragT(&sm.KbT[1][0][0], 0, k0, lane);
+                const bf16x8_t k10 = fragT(&sm.KbT[0][0][0], 32, k0, lane), k11 = fragT(&sm.KbT[1][0][0], 32, k0, lane);
                 accS0 = mfma3(accS0, k00, k01, v0, v1);
                 accS1 = mfma3(accS1, k10, k11, v0, v1);
             }
@@ -725,20 +731,39 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
         __syncthreads();
 
         // ---- triangular solve: SA[i][t] = X[i][t] + sum_{u<t} SA[i][u] A_ab[u][t] -----
+        // Lane q of row i owns tokens t = 4m + q.  Every LDS operand is read before
+        // the dependency chain starts (the lane's 8 X values up front, the Aab rows of
+        // each group of 4 tokens as 16-byte reads issued one group ahead), so a step is only FMAs, two DPP
+        // adds and a select; the newest SA value enters each sum last.
         {
             const int i = tid >> 2, q = tid & 3;
-            float sq[8];  // SA[i][4m + q]
+            float sq[8], xq[8];  // SA[i][4m + q], X[i][4m + q]
 #pragma unroll
-            for (int m = 0; m < 8; ++m) sq[m] = 0.f;
+            for (int m = 0; m < 8; ++m) {
+                sq[m] = 0.f;
+                xq[m] = sm.X[i][4 * m + q];
+            }
+            f32x4 av[L / 4], nx[L / 4];  // Aab[4m + q][4g .. 4g+3] of this group / the next
+            av[0] = *reinterpret_cast<const f32x4*>(&sm.Aab[q][0]);
 #pragma unroll
-            for (int t = 0; t < L; ++t) {
-                float part = 0.f;
+            for (int g = 0; g < L / 4; ++g) {
+                if (g + 1 < L / 4) {
 #pragma unroll
-                for (int m = 0; m < (t + 3) / 4; ++m) part = fmaf(sq[m], sm.Aab[4 * m + q][t], part);
-                part += dpp_xor1(part);
-                part += dpp_xor2(part);
-                const float sat = sm.X[i][t] + part;
-                sq[t >> 2] = q == (t & 3) ? sat : sq[t >> 2];
+                    for (int m = 0; m <= g + 1; ++m)
+                        nx[m] = *reinterpret_cast<const f32x4*>(&sm.Aab[4 * m + q][4 * (g + 1)]);
+                }
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float part = 0.f;
+#pragma unroll
+                    for (int m = 0; m < (4 * g + e + 3) / 4; ++m) part = fmaf(sq[m], av[m][e], part);
+                    part += dpp_xor1(part);
+                    part += dpp_xor2(part);
+                    sq[g] = q == e ? xq[g] + part : sq[g];
+                }
+#pragma unroll
+                for (int m = 0; m < L / 4; ++m)
+                    if (m <= g + 1) av[m] = nx[m];
             }
 #pragma unroll
             for (int m = 0; m < 8; ++m) split1(sq[m], sm.SA[0][i][4 * m + q], sm.SA[1][i][4 * m + q]);
@@ -752,8 +777,8 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                 const bf16x8_t q0 = frag(&sm.BrkT[0][0][0], TQ, 0, k0, lane), q1 = frag(&sm.BrkT[1][0][0], TQ, 0, k0, lane);
                 const bf16x8_t s0 = frag(&sm.SA[0][0][0], TQ, 32 * wave, k0, lane);
                 const bf16x8_t s1 = frag(&sm.SA[1][0][0], TQ, 32 * wave, k0, lane);
-                const bf16x8_t v0 = frag(&sm.VT[0][0][0], TQ, 32 * wave, k0, lane);
-                const bf16x8_t v1 = frag(&sm.VT[1][0][0], TQ, 32 * wave, k0, lane);
+                const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * wave, k0, lane);
+                const bf16x8_t v1 = fragT(&sm.VT[1][0][0], 32 * wave, k0, lane);
                 accY = mfma3(accY, p0, p1, s0, s1);
                 accY = mfma3(accY, q0, q1, v0, v1);
             }
@@ -775,8 +800,8 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
             for (int k0 = 0; k0 < L; k0 += 16) {
                 const bf16x8_t s0 = frag(&sm.SA[0][0][0], TQ, 32 * ir, k0, lane);
                 const bf16x8_t s1 = frag(&sm.SA[1][0][0], TQ, 32 * ir, k0, lane);
-                const bf16x8_t b00 = frag(&sm.BbT[0][0][0], TQ, 0, k0, lane), b01 = frag(&sm.BbT[1][0][0], TQ, 0, k0, lane);
-                const bf16x8_t b10 = frag(&sm.BbT[0][0][0], TQ, 32, k0, lane), b11 = frag(&sm.BbT[1][0][0], TQ, 32, k0, lane);
+                const bf16x8_t b00 = fragT(&sm.BbT[0][0][0], 0, k0, lane), b01 = fragT(&sm.BbT[1][0][0], 0, k0, lane);
+                const bf16x8_t b10 = fragT(&sm.BbT[0][0][0], 32, k0, lane), b11 = fragT(&sm.BbT[1][0][0], 32, k0, lane);
                 accS0 = mfma3(accS0, b00, b01, s0, s1);
                 accS1 = mfma3(accS1, b10, b11, s0, s1);
             }
