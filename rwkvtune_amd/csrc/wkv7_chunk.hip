@@ -642,91 +642,85 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
             continue;
         }
 
-        // ---- B: two 32x32 tiles per wave, K = 64 over keys -------------------------
+        // ---- B: two 32x32 tiles per wave, K = 64 over keys, sharing one operand:
+        //   wave 0: X^T (value tile 0) and A_ab,   wave 1: X^T (value tile 1) and A_ak,
+        //   wave 2: Y^T (value tile 0) and B_rb,   wave 3: Y^T (value tile 1) and B_rk,
+        // where X^T[t][i] = a~_t . S_i, Y^T[t][i] = r~_t . S_i, A_ab[s][t] = b^_s . a~_t,
+        // A_ak[s][t] = k^_s . a~_t (s < t), B_rb[s][t] = b^_s . r~_t, B_rk[s][t] = k^_s . r~_t (s <= t)
         const f32x16 zero16 = {0.f};
-        f32x16 accX = zero16, accY = zero16;  // waves 0/1: X^T, Y^T of value rows 32*wave..
-        if (wave < 2) {
-            // X^T[t][i] = a~_t . S_i,  Y^T[t][i] = r~_t . S_i   (i in tile `wave`)
+        const int vt = wave & 1;                  // value tile of X^T / Y^T
+        f32x16 accXY = zero16;                    // waves 0/1: X^T, waves 2/3: Y^T
+        {
+            const uint16_t* Q = wave < 2 ? &sm.At[0][0][0] : &sm.Rt[0][0][0];
+            const uint16_t* P = (wave & 1) ? &sm.Kh[0][0][0] : &sm.Bh[0][0][0];
+            f32x16 c1 = zero16;
             for (int k0 = 0; k0 < NH; k0 += 16) {
-                const bf16x8_t s0 = frag(&sm.Sp[0][0][0], KP, 32 * wave, k0, lane);
-                const bf16x8_t s1 = frag(&sm.Sp[1][0][0], KP, 32 * wave, k0, lane);
-                const bf16x8_t a0 = frag(&sm.At[0][0][0], KP, 0, k0, lane), a1 = frag(&sm.At[1][0][0], KP, 0, k0, lane);
-                const bf16x8_t r0 = frag(&sm.Rt[0][0][0], KP, 0, k0, lane), r1 = frag(&sm.Rt[1][0][0], KP, 0, k0, lane);
-                accX = mfma3(accX, a0, a1, s0, s1);
-                accY = mfma3(accY, r0, r1, s0, s1);
+                const bf16x8_t s0 = frag(&sm.Sp[0][0][0], KP, 32 * vt, k0, lane);
+                const bf16x8_t s1 = frag(&sm.Sp[1][0][0], KP, 32 * vt, k0, lane);
+                const bf16x8_t q0 = frag(Q, KP, 0, k0, lane), q1 = frag(Q + RT_PLANE, KP, 0, k0, lane);
+                const bf16x8_t p0 = frag(P, KP, 0, k0, lane), p1 = frag(P + RT_PLANE, KP, 0, k0, lane);
+                accXY = mfma3(accXY, q0, q1, s0, s1);
+                c1 = mfma3(c1, p0, p1, q0, q1);
             }
-        } else {
-            // wave 2: A_ab[s][t] = b^_s . a~_t and B_rb[s][t] = b^_s . r~_t  (shared b^)
-            // wave 3: A_ak[s][t] = k^_s . a~_t and B_rk[s][t] = k^_s . r~_t  (shared k^)
-            const uint16_t* Pq = wave == 2 ? &sm.Bh[0][0][0] : &sm.Kh[0][0][0];
-            f32x16 c1 = zero16, c2 = zero16;
-            for (int k0 = 0; k0 < NH; k0 += 16) {
-                const bf16x8_t p0 = frag(Pq, KP, 0, k0, lane), p1 = frag(Pq + RT_PLANE, KP, 0, k0, lane);
-                const bf16x8_t a0 = frag(&sm.At[0][0][0], KP, 0, k0, lane), a1 = frag(&sm.At[1][0][0], KP, 0, k0, lane);
-                const bf16x8_t r0 = frag(&sm.Rt[0][0][0], KP, 0, k0, lane), r1 = frag(&sm.Rt[1][0][0], KP, 0, k0, lane);
-                c1 = mfma3(c1, p0, p1, a0, a1);
-                c2 = mfma3(c2, p0, p1, r0, r1);
-            }
-            // masks: lane holds [s = 8g + 4(l/32) + e][t = l%32]
+            // lane holds [s = 8g + 4(l/32) + e][t = l%32]
             const int tcol = lane & 31;
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int srow = 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
-                c1[q] = srow < tcol ? c1[q] : 0.f;   // A_ab / A_ak: s < t
-                c2[q] = srow <= tcol ? c2[q] : 0.f;  // B_rb / B_rk: s <= t
+                const bool keep = wave < 2 ? srow < tcol : srow <= tcol;
+                c1[q] = keep ? c1[q] : 0.f;
             }
-            if (wave == 2) {
+            if (wave == 0) {
 #pragma unroll
                 for (int q = 0; q < 16; ++q)
                     sm.Aab[8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)][tcol] = c1[q];
-                store_planes_T(&sm.BrbT[0][0][0], TQ, T32_PLANE, 0, 0, c2, lane);
             } else {
-                store_planes_T(&sm.AakT[0][0][0], TQ, T32_PLANE, 0, 0, c1, lane);
-                store_planes_T(&sm.BrkT[0][0][0], TQ, T32_PLANE, 0, 0, c2, lane);
+                uint16_t* out = wave == 1 ? &sm.AakT[0][0][0] : wave == 2 ? &sm.BrbT[0][0][0] : &sm.BrkT[0][0][0];
+                store_planes_T(out, TQ, T32_PLANE, 0, 0, c1, lane);
             }
         }
         __syncthreads();
 
-        // ---- C: X^T += A_ak^T V (waves 0/1); state tiles start (waves 2/3) --------
-        f32x16 accS0 = zero16, accS1 = zero16;  // waves 2/3: S^T tiles (j tile 0 / 1, i tile wave-2)
+        // ---- C: X^T += A_ak^T V (waves 0/1); every wave starts one state tile ------
         if (wave < 2) {
             for (int k0 = 0; k0 < L; k0 += 16) {
                 const bf16x8_t a0 = frag(&sm.AakT[0][0][0], TQ, 0, k0, lane), a1 = frag(&sm.AakT[1][0][0], TQ, 0, k0, lane);
                 const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * wave, k0, lane);
                 const bf16x8_t v1 = fragT(&sm.VT[1][0][0], 32 * wave, k0, lane);
-                accX = mfma3(accX, a0, a1, v0, v1);
+                accXY = mfma3(accXY, a0, a1, v0, v1);
             }
             // X[i][t]: lane holds i = 32*wave + l%32, t = 8g + 4(l/32) + 0..3
             const int i = 32 * wave + (lane & 31);
 #pragma unroll
             for (int g = 0; g < 4; ++g)
                 *reinterpret_cast<f32x4*>(&sm.X[i][8 * g + 4 * (lane >> 5)]) =
-                    f32x4{accX[4 * g], accX[4 * g + 1], accX[4 * g + 2], accX[4 * g + 3]};
-        } else {
-            const int ir = wave - 2;               // value-row tile
+                    f32x4{accXY[4 * g], accXY[4 * g + 1], accXY[4 * g + 2], accXY[4 * g + 3]};
+        }
+        {
+            // S^T tile (value rows 32*ir.., keys 32*jt..) = (S D_L)^T + kbar^T V, back into Sf;
+            // lane holds S[i = 32*ir + l%32][j = 32*jt + 8g + 4(l/32) + 0..3]
+            const int ir = wave >> 1, jt = wave & 1;
             const int i = 32 * ir + (lane & 31);
+            f32x16 acc;
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int jo = 8 * g + 4 * (lane >> 5);
-                const f32x4 s0 = *reinterpret_cast<const f32x4*>(&sm.Sf[i][jo]);
-                const f32x4 s1 = *reinterpret_cast<const f32x4*>(&sm.Sf[i][32 + jo]);
-                const f32x4 d0 = *reinterpret_cast<const f32x4*>(&sm.DL[jo]);
-                const f32x4 d1 = *reinterpret_cast<const f32x4*>(&sm.DL[32 + jo]);
+                const int jo = 32 * jt + 8 * g + 4 * (lane >> 5);
+                const f32x4 sv = *reinterpret_cast<const f32x4*>(&sm.Sf[i][jo]);
+                const f32x4 dv = *reinterpret_cast<const f32x4*>(&sm.DL[jo]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    accS0[4 * g + e] = s0[e] * d0[e];
-                    accS1[4 * g + e] = s1[e] * d1[e];
-                }
+                for (int e = 0; e < 4; ++e) acc[4 * g + e] = sv[e] * dv[e];
             }
-            // S^T[j][i] += kbar_j . v_i over the chunk's tokens
             for (int k0 = 0; k0 < L; k0 += 16) {
                 const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * ir, k0, lane);
                 const bf16x8_t v1 = fragT(&sm.VT[1][0][0], 32 * ir, k0, lane);
-                const bf16x8_t k00 = fragT(&sm.KbT[0][0][0], 0, k0, lane), k01 = fragT(&sm.KbT[1][0][0], 0, k0, lane);
-                const bf16x8_t k10 = fragT(&sm.KbT[0][0][0], 32, k0, lane), k11 = fragT(&sm.KbT[1][0][0], 32, k0, lane);
-                accS0 = mfma3(accS0, k00, k01, v0, v1);
-                accS1 = mfma3(accS1, k10, k11, v0, v1);
+                const bf16x8_t k0p = fragT(&sm.KbT[0][0][0], 32 * jt, k0, lane);
+                const bf16x8_t k1p = fragT(&sm.KbT[1][0][0], 32 * jt, k0, lane);
+                acc = mfma3(acc, k0p, k1p, v0, v1);
             }
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<f32x4*>(&sm.Sf[i][32 * jt + 8 * g + 4 * (lane >> 5)]) =
+                    f32x4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
         }
         __syncthreads();
 
@@ -770,33 +764,23 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
         }
         __syncthreads();
 
-        // ---- D: Y^T += B_rb^T SA + B_rk^T V (waves 0/1); S^T += bbar SA (waves 2/3) --
+        // ---- D: S^T += bbar^T SA (waves 0/1, value rows 32*wave..);
+        //         Y^T += B_rb^T SA + B_rk^T V (waves 2/3, value tile wave - 2) -------------
         if (wave < 2) {
-            for (int k0 = 0; k0 < L; k0 += 16) {
-                const bf16x8_t p0 = frag(&sm.BrbT[0][0][0], TQ, 0, k0, lane), p1 = frag(&sm.BrbT[1][0][0], TQ, 0, k0, lane);
-                const bf16x8_t q0 = frag(&sm.BrkT[0][0][0], TQ, 0, k0, lane), q1 = frag(&sm.BrkT[1][0][0], TQ, 0, k0, lane);
-                const bf16x8_t s0 = frag(&sm.SA[0][0][0], TQ, 32 * wave, k0, lane);
-                const bf16x8_t s1 = frag(&sm.SA[1][0][0], TQ, 32 * wave, k0, lane);
-                const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * wave, k0, lane);
-                const bf16x8_t v1 = fragT(&sm.VT[1][0][0], 32 * wave, k0, lane);
-                accY = mfma3(accY, p0, p1, s0, s1);
-                accY = mfma3(accY, q0, q1, v0, v1);
-            }
-            // y[t0 + t][32*wave + l%32], t = 8g + 4(l/32) + e
-            IO* yb = y + (size_t)t0 * C + h * NH + 32 * wave + (lane & 31);
-            if (n == L) {
+            const int ir = wave;
+            const int i = 32 * ir + (lane & 31);
+            f32x16 accS0, accS1;  // lane holds S[i][j = 32*jt + 8g + 4(l/32) + 0..3], jt = 0 / 1
 #pragma unroll
-                for (int q = 0; q < 16; ++q)
-                    yb[(8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * C] = tr::from_f32(accY[q]);
-            } else {
+            for (int g = 0; g < 4; ++g) {
+                const int jo = 8 * g + 4 * (lane >> 5);
+                const f32x4 s0 = *reinterpret_cast<const f32x4*>(&sm.Sf[i][jo]);
+                const f32x4 s1 = *reinterpret_cast<const f32x4*>(&sm.Sf[i][32 + jo]);
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const int t = 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
-                    if (t < n) yb[t * C] = tr::from_f32(accY[q]);
+                for (int e = 0; e < 4; ++e) {
+                    accS0[4 * g + e] = s0[e];
+                    accS1[4 * g + e] = s1[e];
                 }
             }
-        } else {
-            const int ir = wave - 2;
             for (int k0 = 0; k0 < L; k0 += 16) {
                 const bf16x8_t s0 = frag(&sm.SA[0][0][0], TQ, 32 * ir, k0, lane);
                 const bf16x8_t s1 = frag(&sm.SA[1][0][0], TQ, 32 * ir, k0, lane);
@@ -805,8 +789,6 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                 accS0 = mfma3(accS0, b00, b01, s0, s1);
                 accS1 = mfma3(accS1, b10, b11, s0, s1);
             }
-            // lane holds S[i = 32*ir + l%32][j = 32*jt + 8g + 4(l/32) + 0..3]
-            const int i = 32 * ir + (lane & 31);
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int jo = 8 * g + 4 * (lane >> 5);
@@ -817,8 +799,32 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
             }
             store_planes_T(&sm.Sp[0][0][0], KP, S_PLANE, 32 * ir, 0, accS0, lane);
             store_planes_T(&sm.Sp[0][0][0], KP, S_PLANE, 32 * ir, 32, accS1, lane);
+        } else {
+            for (int k0 = 0; k0 < L; k0 += 16) {
+                const bf16x8_t p0 = frag(&sm.BrbT[0][0][0], TQ, 0, k0, lane), p1 = frag(&sm.BrbT[1][0][0], TQ, 0, k0, lane);
+                const bf16x8_t q0 = frag(&sm.BrkT[0][0][0], TQ, 0, k0, lane), q1 = frag(&sm.BrkT[1][0][0], TQ, 0, k0, lane);
+                const bf16x8_t s0 = frag(&sm.SA[0][0][0], TQ, 32 * vt, k0, lane);
+                const bf16x8_t s1 = frag(&sm.SA[1][0][0], TQ, 32 * vt, k0, lane);
+                const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * vt, k0, lane);
+                const bf16x8_t v1 = fragT(&sm.VT[1][0][0], 32 * vt, k0, lane);
+                accXY = mfma3(accXY, p0, p1, s0, s1);
+                accXY = mfma3(accXY, q0, q1, v0, v1);
+            }
+            // y[t0 + t][32*vt + l%32], t = 8g + 4(l/32) + e
+            IO* yb = y + (size_t)t0 * C + h * NH + 32 * vt + (lane & 31);
+            if (n == L) {
+#pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    yb[(8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * C] = tr::from_f32(accXY[q]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const int t = 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
+                    if (t < n) yb[t * C] = tr::from_f32(accXY[q]);
+                }
+            }
         }
-        // No barrier here: the next chunk's first LDS writes (LW) touch nothing
+        // No barrier here: the next chunk's first LDS writes (tot, slow) touch nothing
         // read in phase D, and its barriers precede every other write.
     }
     __syncthreads();
