@@ -681,7 +681,7 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
         }
         __syncthreads();
 
-        // ---- C: X^T += A_ak^T V (waves 0/1); every wave starts one state tile ------
+        // ---- C: X^T += A_ak^T V (waves 0/1) ---------------------------------------
         if (wave < 2) {
             for (int k0 = 0; k0 < L; k0 += 16) {
                 const bf16x8_t a0 = frag(&sm.AakT[0][0][0], TQ, 0, k0, lane), a1 = frag(&sm.AakT[1][0][0], TQ, 0, k0, lane);
@@ -696,10 +696,22 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                 *reinterpret_cast<f32x4*>(&sm.X[i][8 * g + 4 * (lane >> 5)]) =
                     f32x4{accXY[4 * g], accXY[4 * g + 1], accXY[4 * g + 2], accXY[4 * g + 3]};
         }
+        __syncthreads();
+
+        // ---- triangular solve: SA[i][t] = X[i][t] + sum_{u<t} SA[i][u] A_ab[u][t] -----
+        // Lane q of row i owns tokens t = 4m + q.  Every LDS operand is read before
+        // the dependency chain starts (the lane's 8 X values up front, the Aab rows of
+        // each group of 4 tokens as 16-byte reads issued one group ahead), so a step is only FMAs, two DPP
+        // adds and a select; the newest SA value enters each sum last.  Every wave first
+        // issues one state tile's start on the matrix cores (straight-line code in the
+        // same block as the solve, so its MFMAs overlap the solve's dependency chain).
+        // S^T tile (value rows 32*ir.., keys 32*jt..) = (S D_L)^T + kbar^T V; lane holds
+        // S[i = 32*ir + l%32][j = 32*jt + 8g + 4(l/32) + 0..3]; stored to Sf after the solve
+        const int ir_t = wave >> 1, jt_t = wave & 1;
+        f32x16 tile;
+        bf16x8_t tv[2][2], tk[2][2];  // v and kbar fragments of the tile's two k steps (hi, lo)
         {
-            // S^T tile (value rows 32*ir.., keys 32*jt..) = (S D_L)^T + kbar^T V, back into Sf;
-            // lane holds S[i = 32*ir + l%32][j = 32*jt + 8g + 4(l/32) + 0..3]
-            const int ir = wave >> 1, jt = wave & 1;
+            const int ir = ir_t, jt = jt_t;
             const int i = 32 * ir + (lane & 31);
             f32x16 acc;
 #pragma unroll
@@ -710,25 +722,24 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
 #pragma unroll
                 for (int e = 0; e < 4; ++e) acc[4 * g + e] = sv[e] * dv[e];
             }
-            for (int k0 = 0; k0 < L; k0 += 16) {
-                const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * ir, k0, lane);
-                const bf16x8_t v1 = fragT(&sm.VT[1][0][0], 32 * ir, k0, lane);
-                const bf16x8_t k0p = fragT(&sm.KbT[0][0][0], 32 * jt, k0, lane);
-                const bf16x8_t k1p = fragT(&sm.KbT[1][0][0], 32 * jt, k0, lane);
-                acc = mfma3(acc, k0p, k1p, v0, v1);
-            }
 #pragma unroll
-            for (int g = 0; g < 4; ++g)
-                *reinterpret_cast<f32x4*>(&sm.Sf[i][32 * jt + 8 * g + 4 * (lane >> 5)]) =
-                    f32x4{acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
+            for (int ks = 0; ks < 2; ++ks) {
+                tv[ks][0] = fragT(&sm.VT[0][0][0], 32 * ir, 16 * ks, lane);
+                tv[ks][1] = fragT(&sm.VT[1][0][0], 32 * ir, 16 * ks, lane);
+                tk[ks][0] = fragT(&sm.KbT[0][0][0], 32 * jt, 16 * ks, lane);
+                tk[ks][1] = fragT(&sm.KbT[1][0][0], 32 * jt, 16 * ks, lane);
+            }
+            tile = acc;
         }
-        __syncthreads();
-
-        // ---- triangular solve: SA[i][t] = X[i][t] + sum_{u<t} SA[i][u] A_ab[u][t] -----
-        // Lane q of row i owns tokens t = 4m + q.  Every LDS operand is read before
-        // the dependency chain starts (the lane's 8 X values up front, the Aab rows of
-        // each group of 4 tokens as 16-byte reads issued one group ahead), so a step is only FMAs, two DPP
-        // adds and a select; the newest SA value enters each sum last.
+        // the tile's six MFMAs, one per group of the solve, in mfma3's order per k step
+        // (lo.hi, hi.lo, hi.hi); the scheduling barrier keeps each in its group
+        auto tile_mfma = [&](int m) {
+            const int ks = m / 3, part = m % 3;
+            const bf16x8_t a = part == 0 ? tk[ks][1] : tk[ks][0];
+            const bf16x8_t b = part == 1 ? tv[ks][1] : tv[ks][0];
+            tile = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, tile, 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        };
         {
             const int i = tid >> 2, q = tid & 3;
             float sq[8], xq[8];  // SA[i][4m + q], X[i][4m + q]
@@ -746,6 +757,7 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                     for (int m = 0; m <= g + 1; ++m)
                         nx[m] = *reinterpret_cast<const f32x4*>(&sm.Aab[4 * m + q][4 * (g + 1)]);
                 }
+                if (g >= 1 && g <= 6) tile_mfma(g - 1);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float part = 0.f;
@@ -761,6 +773,13 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
             }
 #pragma unroll
             for (int m = 0; m < 8; ++m) split1(sq[m], sm.SA[0][i][4 * m + q], sm.SA[1][i][4 * m + q]);
+        }
+        {
+            const int i = 32 * ir_t + (lane & 31);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<f32x4*>(&sm.Sf[i][32 * jt_t + 8 * g + 4 * (lane >> 5)]) =
+                    f32x4{tile[4 * g], tile[4 * g + 1], tile[4 * g + 2], tile[4 * g + 3]};
         }
         __syncthreads();
 
