@@ -350,7 +350,7 @@ struct __attribute__((aligned(16))) ChunkLds2 {
     uint16_t SA[2][NH][TQ];                                           // rows i, K = t
     float Sf[NH][SP];   // float32 state [i][j]
     float X[NH][TP];    // S a~^T + V^T A_ak  [i][t]
-    float Aab[L][TP];   // [s][t], zero for s >= t
+    float AT[L][TP];    // A_ab transposed: [t][s], zero for s >= t
     float tot[4][NH];   // per wave: log2-decay sums over its 8 tokens  [w][j]
     float DL[NH];       // decay over the whole chunk
     alignas(16) int slow[4];  // per wave: a token of the chunk decays below the floor
@@ -431,6 +431,16 @@ constexpr int RT_PLANE = L * KP, S_PLANE = NH * KP, T32_PLANE = L * TQ;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLog2DecayFloor = kLogDecayFloor * kLog2e;
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// lane e of each quad, to all four lanes (quad_perm eeee); e is a constant after unrolling
+__device__ __forceinline__ float quad_bcast(float x, int e) {
+    switch (e) {
+    case 0: return __builtin_amdgcn_mov_dpp(x, 0x00, 0xf, 0xf, false);
+    case 1: return __builtin_amdgcn_mov_dpp(x, 0x55, 0xf, 0xf, false);
+    case 2: return __builtin_amdgcn_mov_dpp(x, 0xaa, 0xf, 0xf, false);
+    default: return __builtin_amdgcn_mov_dpp(x, 0xff, 0xf, 0xf, false);
+    }
+}
 
 // hi / lo bf16 parts of one value (hardware round-to-nearest-even)
 __device__ __forceinline__ void split1(float x, uint16_t& hi, uint16_t& lo) {
@@ -672,8 +682,9 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
             }
             if (wave == 0) {
 #pragma unroll
-                for (int q = 0; q < 16; ++q)
-                    sm.Aab[8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)][tcol] = c1[q];
+                for (int g = 0; g < 4; ++g)
+                    *reinterpret_cast<f32x4*>(&sm.AT[tcol][8 * g + 4 * (lane >> 5)]) =
+                        f32x4{c1[4 * g], c1[4 * g + 1], c1[4 * g + 2], c1[4 * g + 3]};
             } else {
                 uint16_t* out = wave == 1 ? &sm.AakT[0][0][0] : wave == 2 ? &sm.BrbT[0][0][0] : &sm.BrkT[0][0][0];
                 store_planes_T(out, TQ, T32_PLANE, 0, 0, c1, lane);
@@ -699,12 +710,15 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
         __syncthreads();
 
         // ---- triangular solve: SA[i][t] = X[i][t] + sum_{u<t} SA[i][u] A_ab[u][t] -----
-        // Lane q of row i owns tokens t = 4m + q.  Every LDS operand is read before
-        // the dependency chain starts (the lane's 8 X values up front, the Aab rows of
-        // each group of 4 tokens as 16-byte reads issued one group ahead), so a step is only FMAs, two DPP
-        // adds and a select; the newest SA value enters each sum last.  Every wave first
-        // issues one state tile's start on the matrix cores (straight-line code in the
-        // same block as the solve, so its MFMAs overlap the solve's dependency chain).
+        // Right-looking: lane q of row i keeps running sums for its targets t = 4m + q.
+        // At step t the owner lane (q = t % 4) finishes sa_t, a quad broadcast hands it
+        // to the other three lanes, and every lane pushes sa_t A_ab[t][4m + q] into its
+        // later sums (which start from X); the dependency chain per step is one DPP
+        // move and one FMA, the other FMAs fill its gaps.  Operands are read before the chain: the
+        // lane's 8 X values up front, the transposed A_ab rows one group of 4 tokens
+        // ahead as 16-byte reads.  Every wave also issues one state tile's start on the
+        // matrix cores (straight-line code in the same block as the solve, so its MFMAs
+        // overlap the chain).
         // S^T tile (value rows 32*ir.., keys 32*jt..) = (S D_L)^T + kbar^T V; lane holds
         // S[i = 32*ir + l%32][j = 32*jt + 8g + 4(l/32) + 0..3]; stored to Sf after the solve
         const int ir_t = wave >> 1, jt_t = wave & 1;
@@ -742,37 +756,33 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
         };
         {
             const int i = tid >> 2, q = tid & 3;
-            float sq[8], xq[8];  // SA[i][4m + q], X[i][4m + q]
+            // pq[m]: X[i][4m + q] plus the terms pushed so far; it is SA[i][4m + q] from the
+            // step of token 4m + q on (later pushes into it multiply A_ab entries that are 0)
+            float pq[8];
 #pragma unroll
-            for (int m = 0; m < 8; ++m) {
-                sq[m] = 0.f;
-                xq[m] = sm.X[i][4 * m + q];
-            }
-            f32x4 av[L / 4], nx[L / 4];  // Aab[4m + q][4g .. 4g+3] of this group / the next
-            av[0] = *reinterpret_cast<const f32x4*>(&sm.Aab[q][0]);
+            for (int m = 0; m < 8; ++m) pq[m] = sm.X[i][4 * m + q];
+            f32x4 av[L / 4], nx[L / 4];  // AT[4m + q][4g .. 4g+3] for m >= g: this group / the next
+#pragma unroll
+            for (int m = 0; m < L / 4; ++m) av[m] = *reinterpret_cast<const f32x4*>(&sm.AT[4 * m + q][0]);
 #pragma unroll
             for (int g = 0; g < L / 4; ++g) {
                 if (g + 1 < L / 4) {
 #pragma unroll
-                    for (int m = 0; m <= g + 1; ++m)
-                        nx[m] = *reinterpret_cast<const f32x4*>(&sm.Aab[4 * m + q][4 * (g + 1)]);
+                    for (int m = g + 1; m < L / 4; ++m)
+                        nx[m] = *reinterpret_cast<const f32x4*>(&sm.AT[4 * m + q][4 * (g + 1)]);
                 }
                 if (g >= 1 && g <= 6) tile_mfma(g - 1);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float part = 0.f;
+                    const float sat = quad_bcast(pq[g], e);  // sa_t, t = 4g + e, from lane e
 #pragma unroll
-                    for (int m = 0; m < (4 * g + e + 3) / 4; ++m) part = fmaf(sq[m], av[m][e], part);
-                    part += dpp_xor1(part);
-                    part += dpp_xor2(part);
-                    sq[g] = q == e ? xq[g] + part : sq[g];
+                    for (int m = g; m < L / 4; ++m) pq[m] = fmaf(sat, av[m][e], pq[m]);
                 }
 #pragma unroll
-                for (int m = 0; m < L / 4; ++m)
-                    if (m <= g + 1) av[m] = nx[m];
+                for (int m = g + 1; m < L / 4; ++m) av[m] = nx[m];
             }
 #pragma unroll
-            for (int m = 0; m < 8; ++m) split1(sq[m], sm.SA[0][i][4 * m + q], sm.SA[1][i][4 * m + q]);
+            for (int m = 0; m < 8; ++m) split1(pq[m], sm.SA[0][i][4 * m + q], sm.SA[1][i][4 * m + q]);
         }
         {
             const int i = 32 * ir_t + (lane & 31);
