@@ -26,6 +26,8 @@
 // exact token-serial update instead, so every input gives the recurrence's result.
 #include "common.hpp"
 
+#include <type_traits>
+
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -408,6 +410,17 @@ __device__ __forceinline__ f32x16 mfma3(f32x16 acc, bf16x8_t a0, bf16x8_t a1, bf
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc, 0, 0, 0);
 }
 
+// mfma3 with a B operand that has no lo part when V_HI_ONLY (the skipped term is 0)
+template <bool V_HI_ONLY>
+__device__ __forceinline__ f32x16 mfma_v(f32x16 acc, bf16x8_t a0, bf16x8_t a1, bf16x8_t b0, bf16x8_t b1) {
+    if constexpr (V_HI_ONLY) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0, acc, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc, 0, 0, 0);
+    } else {
+        return mfma3(acc, a0, a1, b0, b1);
+    }
+}
+
 // Store accumulator C (= M^T of the stored matrix M) as hi/lo planes of M:
 // lane l holds M[l%32][8g + 4*(l/32) + 0..3] in acc[4g .. 4g+3].
 __device__ __forceinline__ void store_planes_T(uint16_t* P, int stride, int plane, int row0, int col0,
@@ -458,6 +471,9 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
     IO* __restrict__ y)
 {
     typedef io_traits<IO> tr;
+    // bf16 inputs are exact as bf16 MFMA operands: V (unscaled) has no lo plane, and
+    // the products with V skip their hi.lo term
+    constexpr bool kVExact = std::is_same<IO, bf16_t>::value;
     __shared__ ChunkLds2 sm;
     const int unit = blockIdx.x;
     const int s = unit / H;
@@ -554,26 +570,27 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                     if (q < wave) base += tq;
                     all += tq;
                 }
-                if (tp == 0) *reinterpret_cast<f32x4*>(&sm.DL[j0]) = f32x4{ex2(all.x), ex2(all.y), ex2(all.z), ex2(all.w)};
+                const f32x4 DLv = {ex2(all.x), ex2(all.y), ex2(all.z), ex2(all.w)};  // D_L
+                if (tp == 0) *reinterpret_cast<f32x4*>(&sm.DL[j0]) = DLv;
                 const f32x4 ld_before = base + exc;  // log2 D of the token before 2tp
                 const f32x4 ld_first = ld_before + lw[0];
-                f32x4 vv[2], kb[2], bb[2];
+                f32x4 vv[2], kb[2], bb[2], Dprev;
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
                     const int t = 2 * tp + e;
                     const f32x4 ld = e == 0 ? ld_first : ld_first + lw[1];
-                    const f32x4 ldm = e == 0 ? ld_before : ld_first;
-                    const f32x4 ldl = all;
                     const f32x4 rv = unpack4<IO>(raw[0][e]), kv = unpack4<IO>(raw[2][e]);
                     const f32x4 av = unpack4<IO>(raw[4][e]), bv = unpack4<IO>(raw[5][e]);
                     vv[e] = unpack4<IO>(raw[3][e]);
                     f32x4 rt, at, kh, bh;
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
-                        const float iD = ex2(-ld[c]);
-                        const float ratio = ex2(ldl[c] - ld[c]);
-                        rt[c] = rv[c] * ex2(ld[c]);
-                        at[c] = av[c] * ex2(ldm[c]);
+                        const float Dt = ex2(ld[c]), iD = ex2(-ld[c]);
+                        const float Dtm1 = e == 0 ? ex2(ld_before[c]) : Dprev[c];
+                        const float ratio = DLv[c] * iD;  // D_L / D_t
+                        Dprev[c] = Dt;
+                        rt[c] = rv[c] * Dt;
+                        at[c] = av[c] * Dtm1;
                         kh[c] = kv[c] * iD;
                         bh[c] = bv[c] * iD;
                         kb[e][c] = kv[c] * ratio;
@@ -598,9 +615,17 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                 for (int c = 0; c < 4; ++c) {
                     const int j = j0 + c;
                     uint32_t hi, lo;
-                    split2(vv[0][c], vv[1][c], hi, lo);
-                    *reinterpret_cast<uint32_t*>(&sm.VT[0][0][0] + tswz(j, 2 * tp)) = hi;
-                    *reinterpret_cast<uint32_t*>(&sm.VT[1][0][0] + tswz(j, 2 * tp)) = lo;
+                    if constexpr (kVExact) {
+                        // the raw bf16 bits of channel j for tokens 2tp, 2tp+1 (no lo plane)
+                        const uint32_t w0 = c < 2 ? raw[3][0].x : raw[3][0].y;
+                        const uint32_t w1 = c < 2 ? raw[3][1].x : raw[3][1].y;
+                        hi = (c & 1) ? ((w0 >> 16) | (w1 & 0xffff0000u)) : ((w0 & 0xffffu) | (w1 << 16));
+                        *reinterpret_cast<uint32_t*>(&sm.VT[0][0][0] + tswz(j, 2 * tp)) = hi;
+                    } else {
+                        split2(vv[0][c], vv[1][c], hi, lo);
+                        *reinterpret_cast<uint32_t*>(&sm.VT[0][0][0] + tswz(j, 2 * tp)) = hi;
+                        *reinterpret_cast<uint32_t*>(&sm.VT[1][0][0] + tswz(j, 2 * tp)) = lo;
+                    }
                     split2(kb[0][c], kb[1][c], hi, lo);
                     *reinterpret_cast<uint32_t*>(&sm.KbT[0][0][0] + tswz(j, 2 * tp)) = hi;
                     *reinterpret_cast<uint32_t*>(&sm.KbT[1][0][0] + tswz(j, 2 * tp)) = lo;
@@ -697,8 +722,8 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
             for (int k0 = 0; k0 < L; k0 += 16) {
                 const bf16x8_t a0 = frag(&sm.AakT[0][0][0], TQ, 0, k0, lane), a1 = frag(&sm.AakT[1][0][0], TQ, 0, k0, lane);
                 const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * wave, k0, lane);
-                const bf16x8_t v1 = fragT(&sm.VT[1][0][0], 32 * wave, k0, lane);
-                accXY = mfma3(accXY, a0, a1, v0, v1);
+                const bf16x8_t v1 = kVExact ? v0 : fragT(&sm.VT[1][0][0], 32 * wave, k0, lane);
+                accXY = mfma_v<kVExact>(accXY, a0, a1, v0, v1);
             }
             // X[i][t]: lane holds i = 32*wave + l%32, t = 8g + 4(l/32) + 0..3
             const int i = 32 * wave + (lane & 31);
@@ -739,7 +764,7 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 tv[ks][0] = fragT(&sm.VT[0][0][0], 32 * ir, 16 * ks, lane);
-                tv[ks][1] = fragT(&sm.VT[1][0][0], 32 * ir, 16 * ks, lane);
+                tv[ks][1] = kVExact ? tv[ks][0] : fragT(&sm.VT[1][0][0], 32 * ir, 16 * ks, lane);
                 tk[ks][0] = fragT(&sm.KbT[0][0][0], 32 * jt, 16 * ks, lane);
                 tk[ks][1] = fragT(&sm.KbT[1][0][0], 32 * jt, 16 * ks, lane);
             }
@@ -749,6 +774,7 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
         // (lo.hi, hi.lo, hi.hi); the scheduling barrier keeps each in its group
         auto tile_mfma = [&](int m) {
             const int ks = m / 3, part = m % 3;
+            if (kVExact && part == 1) return;  // hi(kbar) . lo(v) = 0
             const bf16x8_t a = part == 0 ? tk[ks][1] : tk[ks][0];
             const bf16x8_t b = part == 1 ? tv[ks][1] : tv[ks][0];
             tile = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, tile, 0, 0, 0);
@@ -835,9 +861,9 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                 const bf16x8_t s0 = frag(&sm.SA[0][0][0], TQ, 32 * vt, k0, lane);
                 const bf16x8_t s1 = frag(&sm.SA[1][0][0], TQ, 32 * vt, k0, lane);
                 const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * vt, k0, lane);
-                const bf16x8_t v1 = fragT(&sm.VT[1][0][0], 32 * vt, k0, lane);
+                const bf16x8_t v1 = kVExact ? v0 : fragT(&sm.VT[1][0][0], 32 * vt, k0, lane);
                 accXY = mfma3(accXY, p0, p1, s0, s1);
-                accXY = mfma3(accXY, q0, q1, v0, v1);
+                accXY = mfma_v<kVExact>(accXY, q0, q1, v0, v1);
             }
             // y[t0 + t][32*vt + l%32], t = 8g + 4(l/32) + e
             IO* yb = y + (size_t)t0 * C + h * NH + 32 * vt + (lane & 31);
