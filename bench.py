@@ -193,12 +193,14 @@ def wkv_decode_leg(dev, iters=800, pools_n=8):
 
 # chunked prefill (L = 32 tokens, N = 64): contraction flops per (chunk, head) of the
 # matrix form - A_ab, A_ak, B_rb, B_rk (4 x L*L*N), S a~^T and S r~^T (2 x N*L*N),
-# V^T A_ak (N*L*L), SA B_rb + V^T B_rk (2 x N*L*L), SA bbar + V^T kbar (2 x N*L*N);
-# executed as 3 bf16 MFMA products each for bf16/fp16 I/O (hi/lo operand split)
+# V^T A_ak (N*L*L), SA B_rb + V^T B_rk (2 x N*L*L), SA bbar + V^T kbar (2 x N*L*N).
+# Executed as bf16 MFMA part products on hi/lo operand splits: 3 per contraction, 2 for
+# the three products with V when the inputs are bf16 (V is exact in bf16: no lo part)
 CHUNK_L = 32
+PREFILL_V_FLOPS_PER_CHUNK_HEAD = 2 * (2 * N * CHUNK_L * CHUNK_L + N * CHUNK_L * N)
 PREFILL_FLOPS_PER_CHUNK_HEAD = 2 * (4 * CHUNK_L * CHUNK_L * N + 2 * N * CHUNK_L * N + N * CHUNK_L * CHUNK_L
                                     + 2 * N * CHUNK_L * CHUNK_L + 2 * N * CHUNK_L * N)
-MFMA_PARTS = 3
+PREFILL_MFMA_FLOPS_PER_CHUNK_HEAD = 3 * PREFILL_FLOPS_PER_CHUNK_HEAD - PREFILL_V_FLOPS_PER_CHUNK_HEAD
 PEAK_BF16_TFLOPS = 2500.0      # MI355X dense bf16 MFMA
 PREFILL_BYTES_PER_HEAD_TOKEN = 7 * N * 2        # r, w, k, v, a, b in, y out (bf16)
 STATE_BYTES_PER_SEQ_HEAD = 2 * N * N * 4        # fp32 state read + write
@@ -239,7 +241,7 @@ def prefill_leg(dev, iters=20, chunk_len=64):
     flops = chunks * PREFILL_FLOPS_PER_CHUNK_HEAD
     nbytes = total * H * PREFILL_BYTES_PER_HEAD_TOKEN + len(lens) * H * STATE_BYTES_PER_SEQ_HEAD
     alg_tf = flops / (us * 1e-6) / 1e12
-    mfma_tf = alg_tf * MFMA_PARTS
+    mfma_tf = chunks * PREFILL_MFMA_FLOPS_PER_CHUNK_HEAD / (us * 1e-6) / 1e12
     gbs = nbytes / (us * 1e-6) / 1e9
     return {"kernel": "wkv7_chunk_kernel<bf16>", "tokens": total, "seqs": len(lens), "H": H,
             "us_per_launch": us, "tokens_per_s": total / (us * 1e-6), "algorithmic_TFLOPs": alg_tf,
