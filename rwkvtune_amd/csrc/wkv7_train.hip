@@ -60,6 +60,7 @@ __global__ __launch_bounds__(TH) void wkv7_train_fwd_kernel(
     // [buffer][array][token of the segment][j]: arrays r, decay, k, a, b, v
     constexpr int NA = 6;
     __shared__ __attribute__((aligned(16))) float in[2][NA][SEG][NH];
+    __shared__ __attribute__((aligned(16))) float out[2][SEG][NH];  // y, sa of the segment [t][i]
     const int bh = blockIdx.x;
     const int bb = bh / H, hh = bh - bb * H;
     const int tid = threadIdx.x;
@@ -80,15 +81,18 @@ __global__ __launch_bounds__(TH) void wkv7_train_fwd_kernel(
     }
 
     // staging of a segment: flat element f = tid + TH m (m < NL) is element
-    // f % 64 of token f / 64 % 16 of array f / 1024
+    // f % 64 of token f / 64 % 16 of array f / 1024.  The loads read raw values from
+    // rows clamped to T - 1 (no condition on a load, so they stay in flight together);
+    // the staging turns tokens past T into zero inputs with decay 1, which leave the
+    // state unchanged, so every segment runs all 16 tokens without a branch.
     constexpr int NL = NA * SEG * NH / TH;
-    float xr[NL];
+    IO xr[NL];
     auto fetch = [&](int c) {
 #pragma unroll
         for (int m = 0; m < NL; ++m) {
             const int f = tid + TH * m, arr = f >> 10, t = c * SEG + ((f >> 6) & (SEG - 1)), e = f & 63;
             const IO* sp = arr == 0 ? r : arr == 1 ? w : arr == 2 ? k : arr == 3 ? a : arr == 4 ? b : v;
-            xr[m] = t < T ? tr::to_f32(sp[(((size_t)bb * T + t) * H + hh) * NH + e]) : 0.f;
+            xr[m] = sp[(((size_t)bb * T + min(t, T - 1)) * H + hh) * NH + e];
         }
     };
     const int nseg = (T + SEG - 1) / SEG;
@@ -97,14 +101,16 @@ __global__ __launch_bounds__(TH) void wkv7_train_fwd_kernel(
         const int buf = c & 1;
 #pragma unroll
         for (int m = 0; m < NL; ++m) {
-            const int f = tid + TH * m, arr = f >> 10;
-            in[buf][arr][(f >> 6) & (SEG - 1)][f & 63] = arr == 1 ? expf(-expf(xr[m])) : xr[m];
+            const int f = tid + TH * m, arr = f >> 10, u = (f >> 6) & (SEG - 1);
+            const bool ok = c * SEG + u < T;
+            const float x = tr::to_f32(xr[m]);
+            in[buf][arr][u][f & 63] = arr == 1 ? (ok ? expf(-expf(x)) : 1.f) : (ok ? x : 0.f);
         }
         __syncthreads();
         if (c + 1 < nseg) fetch(c + 1);
-        const int n = min(SEG, T - c * SEG);
-        for (int u = 0; u < n; ++u) {
-            const int t = c * SEG + u;
+        float yk[SEG / TPR], sk[SEG / TPR];  // y, sa of tokens q + 8m of the segment (this lane's row)
+#pragma unroll
+        for (int u = 0; u < SEG; ++u) {
             const float* rr = in[buf][0][u] + j0;
             const float* dec = in[buf][1][u] + j0;
             const float* kk = in[buf][2][u] + j0;
@@ -126,17 +132,31 @@ __global__ __launch_bounds__(TH) void wkv7_train_fwd_kernel(
                 if (jj & 1) y2 = fmaf(sv, rr[jj], y2); else y1 = fmaf(sv, rr[jj], y1);
             }
             const float yi = row_sum(y1 + y2);
-            const size_t o = (((size_t)bb * T + t) * H + hh) * NH + i;
-            if (q == 0) {
-                y[o] = tr::from_f32(yi);
-                sa_out[o] = sa;
-            }
+            yk[u / TPR] = q == u % TPR ? yi : yk[u / TPR];
+            sk[u / TPR] = q == u % TPR ? sa : sk[u / TPR];
+        }
+#pragma unroll
+        for (int m = 0; m < SEG / TPR; ++m) {
+            out[0][q + TPR * m][i] = yk[m];
+            out[1][q + TPR * m][i] = sk[m];
         }
         // the state after the segment's last token
         float* p = ckpt + (((size_t)bh * nck + c) * NH + i) * NH + j0;
 #pragma unroll
         for (int cc = 0; cc < JPT / 4; ++cc)
             *reinterpret_cast<f32x4*>(p + 4 * cc) = f32x4{S[4 * cc], S[4 * cc + 1], S[4 * cc + 2], S[4 * cc + 3]};
+        __syncthreads();
+        // y and sa of the segment's tokens, each token's 64 rows contiguous
+        const int n = min(SEG, T - c * SEG);
+#pragma unroll
+        for (int m = 0; m < SEG * NH / TH; ++m) {
+            const int e = tid + TH * m, u = e >> 6, ii = e & 63;
+            if (u < n) {
+                const size_t o = (((size_t)bb * T + c * SEG + u) * H + hh) * NH + ii;
+                y[o] = tr::from_f32(out[0][u][ii]);
+                sa_out[o] = out[1][u][ii];
+            }
+        }
     }
     if (s_out != nullptr) {
         // every thread read its part of s0 at the start, so s_out may alias s0
@@ -160,10 +180,11 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
 {
     typedef io_traits<IO> tr;
     // [buffer][array][token of the segment][j]: arrays r, decay, k, v, a, b, dy,
-    // sa, log-decay (-exp(w_raw))
-    constexpr int NA = 9;
+    // sa, log-decay (-exp(w_raw)), inverse decay
+    constexpr int NA = 10;
     __shared__ __attribute__((aligned(16))) float in[2][NA][SEG][NH];
     __shared__ __attribute__((aligned(16))) float dsa_sh[2][NH];
+    __shared__ __attribute__((aligned(16))) float gout[6][SEG][NH];  // dr, dw, dk, dv, db, da [t][i]
     const int bh = blockIdx.x;
     const int bb = bh / H, hh = bh - bb * H;
     const int tid = threadIdx.x;
@@ -182,12 +203,13 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
 #pragma unroll
         for (int jj = 0; jj < JPT; ++jj) dS[jj] = dST[jj] = 0.f;
     }
-#pragma unroll
-    for (int jj = 0; jj < JPT; ++jj) sT[jj] = 0.f;
 
     // staging of a segment: flat element f = tid + TH m (m < NL) is element
     // f % 64 of token f / 64 % 16 of input array f / 1024 (r, w, k, v, a, b, dy,
-    // sa); w also yields the log-decay array
+    // sa); w also yields the log-decay and inverse-decay arrays.  Rows past T are
+    // loaded clamped and staged as zero inputs with decay 1, which leave the state,
+    // its gradient and every carried sum unchanged, so each segment runs all 16
+    // tokens without a branch.
     constexpr int NL = 8 * SEG * NH / TH;
     float xr[NL];
     auto fetch = [&](int c) {
@@ -204,33 +226,42 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
             }
         }
     };
+    float ckn[JPT];  // S[j][i] after segment c (its checkpoint), loaded one segment ahead
+    auto fetch_ck = [&](int c) {
+        const float* p = ckpt + ((size_t)bh * nck + c) * NH * NH;
+#pragma unroll
+        for (int jj = 0; jj < JPT; ++jj) ckn[jj] = p[(j0 + jj) * NH + i];
+    };
     const int nseg = (T + SEG - 1) / SEG;
     fetch(nseg - 1);
-    int par = 0;  // dsa_sh buffer of the current token
+    fetch_ck(nseg - 1);
     for (int c = nseg - 1; c >= 0; --c) {
         const int buf = c & 1;
 #pragma unroll
         for (int m = 0; m < NL; ++m) {
             const int f = tid + TH * m, arr = f >> 10, u = (f >> 6) & (SEG - 1), e = f & 63;
+            const bool ok = c * SEG + u < T;
             if (arr == 1) {
-                const float lw = -expf(xr[m]);
-                in[buf][1][u][e] = expf(lw);
+                const float lw = ok ? -expf(xr[m]) : 0.f;
+                const float wd = expf(lw);
+                in[buf][1][u][e] = wd;
                 in[buf][8][u][e] = lw;
+                in[buf][9][u][e] = 1.0f / wd;
             } else {
-                in[buf][arr][u][e] = xr[m];
+                in[buf][arr][u][e] = ok ? xr[m] : 0.f;
             }
         }
-        __syncthreads();
-        if (c > 0) fetch(c - 1);
-        // S after the segment's last token
-        {
-            const float* p = ckpt + ((size_t)bh * nck + c) * NH * NH;
 #pragma unroll
-            for (int jj = 0; jj < JPT; ++jj) sT[jj] = p[(j0 + jj) * NH + i];
+        for (int jj = 0; jj < JPT; ++jj) sT[jj] = ckn[jj];
+        __syncthreads();
+        if (c > 0) {
+            fetch(c - 1);
+            fetch_ck(c - 1);
         }
-        const int n = min(SEG, T - c * SEG);
-        for (int u = n - 1; u >= 0; --u) {
-            const int t = c * SEG + u;
+        float keep[6][SEG / TPR];  // dr, dw, dk, dv, db, da of tokens q + 8m (this lane's row)
+#pragma unroll
+        for (int u = SEG - 1; u >= 0; --u) {
+            const int par = (SEG - 1 - u) & 1;  // dsa_sh buffer of this token
             const float* rr = in[buf][0][u];
             const float* dec = in[buf][1][u];
             const float* kk = in[buf][2][u];
@@ -247,7 +278,7 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
             }
             const float g = row_sum(g1 + g2);
             const float ri = rr[i], ki = kk[i], bi = bv[i], dyi = dyv[i], ai = aa[i], wi = dec[i];
-            const float iwi = 1.0f / wi;
+            const float iwi = in[buf][9][u][i];
             float gw = 0.f, gk = 0.f, gv = 0.f, gsa = 0.f, gb = 0.f;
 #pragma unroll
             for (int jj = 0; jj < JPT; ++jj) {
@@ -266,15 +297,14 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
             gv = row_sum(gv);
             gsa = row_sum(gsa);
             gb = row_sum(gb);
-            const size_t o = (((size_t)bb * T + t) * H + hh) * NH + i;
-            if (q == 0) {
-                dr[o] = tr::from_f32(g);
-                dw[o] = tr::from_f32(gw * wi * in[buf][8][u][i]);
-                dk[o] = tr::from_f32(gk);
-                dv[o] = tr::from_f32(gv);
-                db[o] = tr::from_f32(gb);
-                dsa_sh[par][i] = gsa;
-            }
+            const int ku = u / TPR;
+            const bool mine = q == u % TPR;
+            keep[0][ku] = mine ? g : keep[0][ku];
+            keep[1][ku] = mine ? gw * wi * in[buf][8][u][i] : keep[1][ku];
+            keep[2][ku] = mine ? gk : keep[2][ku];
+            keep[3][ku] = mine ? gv : keep[3][ku];
+            keep[4][ku] = mine ? gb : keep[4][ku];
+            dsa_sh[par][i] = gsa;  // the row's 8 lanes store the same value
             // one barrier per token: dsa_sh alternates, so the next token's write
             // goes to the other buffer, read by nobody until after this barrier
             __syncthreads();
@@ -286,14 +316,33 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
                 a2 = fmaf(sT[jj + 1], ds[j0 + jj + 1], a2);
             }
             const float ga = row_sum(a1 + a2);
-            if (q == 0) da[o] = tr::from_f32(ga);
+            keep[5][ku] = mine ? ga : keep[5][ku];
 #pragma unroll
             for (int jj = 0; jj < JPT; ++jj) {
                 const int j = j0 + jj;
                 dS[jj] = fmaf(dS[jj], dec[j], gsa * aa[j]);
                 dST[jj] = fmaf(dST[jj], wi, ai * ds[j]);
             }
-            par ^= 1;
+        }
+#pragma unroll
+        for (int x = 0; x < 6; ++x)
+#pragma unroll
+            for (int m = 0; m < SEG / TPR; ++m) gout[x][q + TPR * m][i] = keep[x][m];
+        __syncthreads();
+        // the segment's gradients, each token's 64 values contiguous
+        const int n = min(SEG, T - c * SEG);
+#pragma unroll
+        for (int m = 0; m < SEG * NH / TH; ++m) {
+            const int e = tid + TH * m, u = e >> 6, ii = e & 63;
+            if (u < n) {
+                const size_t o = (((size_t)bb * T + c * SEG + u) * H + hh) * NH + ii;
+                dr[o] = tr::from_f32(gout[0][u][ii]);
+                dw[o] = tr::from_f32(gout[1][u][ii]);
+                dk[o] = tr::from_f32(gout[2][u][ii]);
+                dv[o] = tr::from_f32(gout[3][u][ii]);
+                db[o] = tr::from_f32(gout[4][u][ii]);
+                da[o] = tr::from_f32(gout[5][u][ii]);
+            }
         }
     }
     if (ds0 != nullptr) {
