@@ -45,25 +45,43 @@ __device__ __forceinline__ int elem_of(int j, int tid) { return (j / kGroup) * k
 __device__ __forceinline__ int owner_of(int i) { return (i % kStride) / kGroup; }
 __device__ __forceinline__ int slot_of(int i) { return (i / kStride) * kGroup + (i % kGroup); }
 
-// the row's values with entries past vmax (banned ids and padding) as -inf;
-// whole in-range groups of an aligned row are read with one 16-byte load
-// (two for float32)
+// the row's values with entries past vmax (banned ids and padding) as -inf.  No
+// load depends on a condition (a conditional load is waited on where it stands,
+// which serialises the row's loads): on an aligned row with V % 8 == 0 every group
+// of 8 is wholly inside the row or wholly past it, and is one 16-byte load (two for
+// float32) of the group or, past the row, of group 0; otherwise every element is
+// one load from an index clamped to the row.  The masks are selects afterwards.
 template <typename LT>
-__device__ __forceinline__ void load_row(const LT* lg, int vmax, float (&x)[kVPT]) {
+__device__ __forceinline__ void load_row(const LT* lg, int V, int vmax, float (&x)[kVPT]) {
     typedef io_traits<LT> tr;
     const int tid = threadIdx.x;
-    const bool vec = (((uintptr_t)lg) & 15) == 0;
+    if ((((uintptr_t)lg) & 15) == 0 && V % kGroup == 0) {
+        f32x4 a[kVPT / kGroup], b[kVPT / kGroup];
 #pragma unroll
-    for (int c = 0; c < kVPT / kGroup; ++c) {
-        const int i0 = c * kStride + tid * kGroup;
-        if (vec && i0 + kGroup - 1 <= vmax) {
-            const f32x4 a = tr::load4(lg + i0), b = tr::load4(lg + i0 + 4);
-            x[c * kGroup + 0] = a.x; x[c * kGroup + 1] = a.y; x[c * kGroup + 2] = a.z; x[c * kGroup + 3] = a.w;
-            x[c * kGroup + 4] = b.x; x[c * kGroup + 5] = b.y; x[c * kGroup + 6] = b.z; x[c * kGroup + 7] = b.w;
-        } else {
+        for (int c = 0; c < kVPT / kGroup; ++c) {
+            const int i0 = c * kStride + tid * kGroup;
+            const LT* p = lg + (i0 < V ? i0 : 0);
+            a[c] = tr::load4(p);
+            b[c] = tr::load4(p + 4);
+        }
 #pragma unroll
-            for (int e = 0; e < kGroup; ++e)
-                x[c * kGroup + e] = (i0 + e <= vmax) ? tr::to_f32(lg[i0 + e]) : -INFINITY;
+        for (int c = 0; c < kVPT / kGroup; ++c) {
+            const int i0 = c * kStride + tid * kGroup;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x[c * kGroup + e] = i0 + e <= vmax ? a[c][e] : -INFINITY;
+                x[c * kGroup + 4 + e] = i0 + 4 + e <= vmax ? b[c][e] : -INFINITY;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int c = 0; c < kVPT / kGroup; ++c) {
+#pragma unroll
+            for (int e = 0; e < kGroup; ++e) {
+                const int i = c * kStride + tid * kGroup + e;
+                const float v = tr::to_f32(lg[i < V ? i : V - 1]);
+                x[c * kGroup + e] = i <= vmax ? v : -INFINITY;
+            }
         }
     }
 }
@@ -252,7 +270,7 @@ __global__ __launch_bounds__(kT) void sample_kernel(
     const float temp = temperature[row];
     if (!(temp >= 1e-6f)) return;  // greedy rows belong to greedy_kernel
     float x[kVPT];
-    load_row(lg, vmax, x);  // banned and padding: -inf
+    load_row(lg, V, vmax, x);  // banned and padding: -inf
     // temperature (a multiply by its reciprocal: within an ulp of the division),
     // then logit bias (clamped), core.py:86-95
     if (temp != 1.0f) {
@@ -409,7 +427,8 @@ __global__ __launch_bounds__(kTG) void greedy_kernel(
 #pragma unroll
     for (int j = 0; j < kVPTG; ++j) {
         const int i = j * kTG + tid;
-        x[j] = (i <= vmax) ? tr::to_f32(lg[i]) : -INFINITY;
+        const float v = tr::to_f32(lg[i < V ? i : V - 1]);  // unconditional load (see load_row)
+        x[j] = i <= vmax ? v : -INFINITY;
     }
     // padding is -inf at the highest indices, so it never wins a tie
     unsigned long long best = 0;
