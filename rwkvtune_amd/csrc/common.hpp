@@ -99,6 +99,37 @@ __device__ __forceinline__ float dpp_xor2(float x) {
 __device__ __forceinline__ float dpp_xor1(float x) {
     return __builtin_amdgcn_update_dpp(0.0f, x, 0xb1, 0xf, 0xf, false);
 }
+// Sum of n float4 planes p[0], p[stride], ..., p[(n-1) stride] in plane order.
+// n = 1..8 run unrolled, every load issued before the first add (a loop with a
+// run-time count waits for each load before issuing the next).
+template <int N>
+__device__ __forceinline__ f32x4 sum_planes_n(const float* p, int64_t stride) {
+    f32x4 t[N];
+#pragma unroll
+    for (int q = 0; q < N; ++q) t[q] = *reinterpret_cast<const f32x4*>(p + q * stride);
+    f32x4 v = t[0];
+#pragma unroll
+    for (int q = 1; q < N; ++q) v += t[q];
+    return v;
+}
+__device__ __forceinline__ f32x4 sum_planes(const float* p, int64_t stride, int n) {
+    switch (n) {
+    case 1: return sum_planes_n<1>(p, stride);
+    case 2: return sum_planes_n<2>(p, stride);
+    case 3: return sum_planes_n<3>(p, stride);
+    case 4: return sum_planes_n<4>(p, stride);
+    case 5: return sum_planes_n<5>(p, stride);
+    case 6: return sum_planes_n<6>(p, stride);
+    case 7: return sum_planes_n<7>(p, stride);
+    case 8: return sum_planes_n<8>(p, stride);
+    default: {
+        f32x4 v = *reinterpret_cast<const f32x4*>(p);
+        for (int q = 1; q < n; ++q) v += *reinterpret_cast<const f32x4*>(p + q * stride);
+        return v;
+    }
+    }
+}
+
 // Value of lane l ^ 16 / l ^ 32 (l = lane in the wave) by gfx950's
 // v_permlane16_swap / v_permlane32_swap with both operands x: the first swaps
 // odd 16-lane rows of its first operand with even rows of its second, so the

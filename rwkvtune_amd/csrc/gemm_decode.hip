@@ -332,8 +332,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(GemmBatch batch, const
     if (P.splits <= 1 || e >= total) return;
     const float* base = ws + P.ws_off + e;
     if ((P.N & 3) == 0) {  // 4 elements of one row
-        f32x4 v = *reinterpret_cast<const f32x4*>(base);
-        for (int s = 1; s < P.splits; ++s) v += *reinterpret_cast<const f32x4*>(base + s * total);
+        const f32x4 v = sum_planes(base, total, P.splits);
         const int row = (int)(e / P.N), col = (int)(e % P.N);
 #pragma unroll
         for (int c = 0; c < 4; ++c) P.C[(int64_t)row * P.ldc + col + c] = f32_to_bf16(epi_fn(P.epi, v[c]));

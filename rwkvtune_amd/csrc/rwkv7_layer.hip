@@ -107,9 +107,7 @@ template <> struct vec4io<f16_t> {
 template <typename IO>
 __device__ __forceinline__ f32x4 add_term(const ResidualSrc<IO>& src, int64_t row, int C, int c) {
     if (src.parts != nullptr) {
-        const float* p = src.parts + row * C + 4 * c;
-        f32x4 v = *reinterpret_cast<const f32x4*>(p);
-        for (int q = 1; q < src.n_parts; ++q) v += *reinterpret_cast<const f32x4*>(p + q * src.part_stride);
+        const f32x4 v = sum_planes(src.parts + row * C + 4 * c, src.part_stride, src.n_parts);
         if constexpr (sizeof(IO) == 4) return v;
         IO t[4];
         vec4io<IO>::store(t, v);
