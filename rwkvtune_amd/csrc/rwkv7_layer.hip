@@ -145,9 +145,7 @@ struct RowRegs {
 // residual of row m into registers (emb lookup or x_in + add)
 template <typename IO, int NV, int TH>
 __device__ __forceinline__ void load_row(const ResidualSrc<IO>& src, int m, int C4, RowRegs<IO, NV>& r) {
-    // loads from clamped chunks, masked after (a conditional load is waited on where it stands)
     const int t = threadIdx.x;
-    const f32x4 z = {0.f, 0.f, 0.f, 0.f};
     if (src.tokens != nullptr) {
         const int64_t tk = src.tokens[m];
         const bool ok = tk >= 0 && tk < src.vocab;
@@ -155,18 +153,19 @@ __device__ __forceinline__ void load_row(const ResidualSrc<IO>& src, int m, int 
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
             const int c = t + j * TH;
-            const f32x4 v = vec4io<IO>::load(e + 4 * (c < C4 ? c : 0));
-            r.v[j] = c < C4 && ok ? v : z;
+            f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            r.v[j] = (c < C4 && ok) ? vec4io<IO>::load(e + 4 * c) : z;
         }
     } else {
         const float* x = src.x_in + (size_t)m * C4 * 4;
         const bool has_add = src.add != nullptr || src.parts != nullptr;
 #pragma unroll
         for (int j = 0; j < NV; ++j) {
-            const int c = t + j * TH, cc = c < C4 ? c : 0;
-            f32x4 a = *reinterpret_cast<const f32x4*>(x + 4 * cc);
-            if (has_add) a += add_term(src, m, 4 * C4, cc);
-            r.v[j] = c < C4 ? a : z;
+            const int c = t + j * TH;
+            f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            f32x4 a = (c < C4) ? *reinterpret_cast<const f32x4*>(x + 4 * c) : z;
+            if (has_add && c < C4) a += add_term(src, m, 4 * C4, c);
+            r.v[j] = a;
         }
     }
 }
@@ -251,52 +250,39 @@ __global__ __launch_bounds__(TH) void shift_mix_kernel(
     };
     const IO* e_cur = src.tokens != nullptr ? emb_row(m) : nullptr;
     const IO* e_prv = (src.tokens != nullptr && !first) ? emb_row(m - 1) : nullptr;
-    // chunk c of the residual of `row` (embedding lookup, or x_in + add); chunks past
-    // the row read chunk 0 and return zero (no load depends on a condition: such a
-    // load is waited on where it stands)
+    // chunk c of the residual of `row` (embedding lookup, or x_in + add)
     auto resid = [&](int row, const IO* e, int c) -> f32x4 {
-        const int cc = c < C4 ? c : 0;
-        f32x4 a;
-        if (src.tokens != nullptr) {
-            const f32x4 v = vec4io<IO>::load((e != nullptr ? e : src.emb) + 4 * cc);
-            a = e != nullptr ? v : z;
-        } else {
-            a = *reinterpret_cast<const f32x4*>(src.x_in + (size_t)row * C + 4 * cc);
-            if (src.add != nullptr || src.parts != nullptr) a += add_term(src, row, C, cc);
-        }
-        return c < C4 ? a : z;
-    };
-    auto ld4 = [&](const float* base, int c) -> f32x4 {
-        return *reinterpret_cast<const f32x4*>(base + 4 * (c < C4 ? c : 0));
+        if (c >= C4) return z;
+        if (src.tokens != nullptr) return e != nullptr ? vec4io<IO>::load(e + 4 * c) : z;
+        f32x4 a = *reinterpret_cast<const f32x4*>(src.x_in + (size_t)row * C + 4 * c);
+        if (src.add != nullptr || src.parts != nullptr) a += add_term(src, row, C, c);
+        return a;
     };
 
-    // Every operand is loaded up front - the LayerNorm parameters, the mix
-    // coefficients and the slot's x_prev first, then the row and the previous row
-    // (whose split-K planes are summed as they arrive) - into plain register
-    // arrays, so their latencies overlap.  Chunks past the row are never used.
+    // Every operand is loaded up front - the row, the previous row (or the
+    // slot's x_prev), the LayerNorm parameters and the mix coefficients - into
+    // plain register arrays, so their latencies overlap.
     // (with two chunks per thread in 1024-thread blocks - at most 128 registers -
     // the mix coefficients are read at use instead: their registers would spill)
     constexpr bool kPreMix = NV == 1 || TH < 1024;
     constexpr int NVM = kPreMix ? NV : 1;
     const float* pp = prev_pool + (size_t)(slot < 0 ? 0 : slot) * C;
-    f32x4 cur[NV], prv[NV], pv[NV], lw[NV], lb[NV], mu[NMIX][NVM];
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-        const int c = t + j * TH;
-        lw[j] = ld4(ln_w, c);
-        lb[j] = ld4(ln_b, c);
-        if constexpr (kPreMix) {
-#pragma unroll
-            for (int q = 0; q < NMIX; ++q) mu[q][j] = ld4(mix + (size_t)q * C, c);
-        }
-        pv[j] = z;
-        if (first) pv[j] = ld4(pp, c);  // the slot's x_prev (a sequence's first row only)
-    }
+    f32x4 cur[NV], prv[NV], lw[NV], lb[NV], mu[NMIX][NVM];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = t + j * TH;
         cur[j] = resid(m, e_cur, c);
-        prv[j] = first ? (c < C4 && slot >= 0 ? pv[j] : z) : resid(m - 1, e_prv, c);
+        if (first)
+            prv[j] = (c < C4 && slot >= 0) ? *reinterpret_cast<const f32x4*>(pp + 4 * c) : z;
+        else
+            prv[j] = resid(m - 1, e_prv, c);
+        lw[j] = c < C4 ? *reinterpret_cast<const f32x4*>(ln_w + 4 * c) : z;
+        lb[j] = c < C4 ? *reinterpret_cast<const f32x4*>(ln_b + 4 * c) : z;
+        if constexpr (kPreMix) {
+#pragma unroll
+            for (int q = 0; q < NMIX; ++q)
+                mu[q][j] = c < C4 ? *reinterpret_cast<const f32x4*>(mix + (size_t)q * C + 4 * c) : z;
+        }
     }
     // ln0 on the residual (layer 0); the previous row needs it too
     if (src.ln0_w != nullptr) ln_regs<NV, TH>(cur, prv, !first, C4, src.ln0_w, src.ln0_b, red);
