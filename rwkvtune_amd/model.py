@@ -325,13 +325,14 @@ class _LayerPack:
                 self.lora_down[i, :, :dn.shape[1]] = dn.detach()
                 self.lora_up[i, :up.shape[0], :] = up.detach()
         # decode-GEMM weights of bf16 models, packed: r / k / v, the LoRA downs
-        # and ups as [out][in] matrices, the FFN key and value
+        # and ups as [out][in] matrices, the output projection, the FFN key and value
         self.gp = {}
         if att.w1.dtype == torch.bfloat16:
             with torch.no_grad():
                 self.gp = {"r": PackedWeight(att.receptance.weight.detach()),
                            "k": PackedWeight(att.key.weight.detach()),
                            "v": PackedWeight(att.value.weight.detach()),
+                           "o": PackedWeight(att.output.weight.detach()),
                            "fk": PackedWeight(ffn.key.weight.detach()),
                            "fv": PackedWeight(ffn.value.weight.detach())}
                 names = ("w1", "a1", "g1", "w2", "a2", "g2") + (() if self.layer0 else ("v1", "v2"))
@@ -353,9 +354,12 @@ class RWKV7Model(nn.Module):
         # decode rows of a bf16 model run their projections on the library's
         # grouped MFMA GEMM over packed weights: r, k, v and the LoRA downs (tanh /
         # sigmoid fused) in one launch, the LoRA ups in one, the FFN key (relu^2
-        # fused) and value; the output projection and the head stay library GEMMs
-        # (faster there at these shapes, measured)
+        # fused) and value, the output projection (split-K planes summed by the
+        # next row kernel); the head stays a library GEMM (faster there, measured)
         self.use_grouped_gemm = True
+        # decode: output projection on the grouped GEMM's split-K planes (summed by
+        # the next row kernel) instead of the library GEMM
+        self.use_grouped_output = True
         self._lora_h = {}
 
     # -- bookkeeping ---------------------------------------------------------
@@ -594,9 +598,15 @@ class RWKV7Model(nn.Module):
                 wkv_ops.wkv7_prefill(kv, seq_slot, cu_seqlens, *ops.unbind(0), y=y)
                 _lib.call("rwkv7_tmix_post", code, M, H, P(y), P(ops[0]), P(ops[2]), P(ops[3]), P(g),
                           pk.tparams, P(o), st)
-            att_out = self._lin(o, att.output.weight)
+            if grouped and self.use_grouped_output:
+                # the output projection's K-range partials, summed by the next shift_mix
+                att_out, att_parts = self._gemm_partials(M, o, pk.gp["o"], st)
+                att_stride = M * C
+            else:
+                att_out, att_parts, att_stride = self._lin(o, att.output.weight), 0, 0
             # residual + attention -> ln2 -> FFN shift/lerp
-            _lib.call("rwkv7_shift_mix", code, M, C, P(x_res), P(att_out), 0, 0, None, None, 0, None, None,
+            _lib.call("rwkv7_shift_mix", code, M, C, P(x_res), P(att_out), att_parts, att_stride, None, None, 0,
+                      None, None,
                       P(x_mid), P(pk.ln2[0]), P(pk.ln2[1]), P(fx), S, P(row_slot), P(row_last), 1,
                       P(pk.mixk), P(xk_ffn), st)
             if grouped:
