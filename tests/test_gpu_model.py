@@ -138,10 +138,14 @@ def test_cfg1_greedy_token_ids_identical(gpu_device):
     assert torch.equal(gpu_tok, ref_tok)
 
 
-def test_grouped_gemm_decode_path(gpu_device):
-    """The optional grouped MFMA GEMM decode path matches the fp64 oracle too."""
-    print("[case] grouped-GEMM decode path", flush=True)
+@pytest.mark.parametrize("grouped_output", [True, False])
+def test_grouped_gemm_decode_path(gpu_device, grouped_output):
+    """The optional grouped MFMA GEMM decode path matches the fp64 oracle too, with
+    the output projection as split-K planes summed by the next row kernel or as a
+    library GEMM."""
+    print(f"[case] grouped-GEMM decode path (output projection on planes: {grouped_output})", flush=True)
     m = tiny(torch.bfloat16, seed=14)
+    m.use_grouped_output = grouped_output
     sd = om.cast_state_dict(m.state_dict(), torch.float64)
     g = torch.Generator().manual_seed(3)
     idx = torch.randint(0, V, (5, 6), generator=g)
