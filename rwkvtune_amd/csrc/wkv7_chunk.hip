@@ -328,10 +328,18 @@ __global__ __launch_bounds__(256) void wkv7_chunk_kernel(
 // ===========================================================================
 // bf16 / fp16 I/O: the same chunk algebra with every MFMA operand stored once,
 // at production, as bf16 hi + lo planes in LDS (x = hi + lo + e, |e| <= 2^-17 |x|),
-// and three v_mfma_f32_32x32x16_bf16 per product step (hi.hi + hi.lo + lo.hi).
+// and three v_mfma_f32_32x32x16_bf16 per product step (hi.hi + hi.lo + lo.hi;
+// two for the products with V when the inputs are bf16, exact as bf16 operands).
 // The per-product error (~2^-16) leaves y ~5e-5 of its rms from the exact
 // recurrence and the state ~5e-6 relative, well inside the bf16 / fp16 output
 // rounding; the float32 kernel above keeps the three-part split instead.
+//
+// One 256-thread block per (sequence, head), one block per CU (~144 KB of LDS).
+// Per chunk: phase A turns the prefetched inputs into the scaled operand planes
+// (log-decay prefix in registers, one barrier); phase B gives each wave one
+// state product (X^T or Y^T of a value tile) and one intra-chunk matrix; phase C
+// adds V^T A_ak to X; the right-looking triangular solve (quad broadcasts) runs
+// with each wave's state-tile MFMAs interleaved; phase D finishes Y and S.
 //
 // 32x32x16 operand layout: lane l supplies row (l % 32) of A (and of B^T) at
 // k = 8*(l/32) .. +7; accumulator q of lane l is C[8*(q/4) + 4*(l/32) + q%4][l%32].
