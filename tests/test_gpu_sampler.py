@@ -192,3 +192,43 @@ def test_repetition_penalty(gpu_device):
     torch.cuda.synchronize()
     ref = osm.repetition_penalty(logits, [h + q for h, q in zip(hists, gen)], 1.3)
     assert torch.allclose(d.cpu().double(), ref, rtol=1e-6, atol=1e-6)
+
+
+@pytest.mark.parametrize("Vs,dtype,offset", [(1000, torch.bfloat16, 0), (1003, torch.bfloat16, 0),
+                                              (1003, torch.float32, 0), (1000, torch.bfloat16, 1)])
+def test_small_vocab_rows(gpu_device, Vs, dtype, offset):
+    """Rows shorter than the kernel's 65,536-entry layout: V a multiple of 8 on an
+    aligned row (16-byte group loads, groups past the row masked), V not a multiple
+    of 8 and rows that are not 16-byte aligned (one load per entry).  Greedy equals
+    the oracle's argmax; every top-p draw lies in the oracle's kept set, with the
+    oracle's log-probability."""
+    print(f"[case] small vocab V={Vs} {dtype} offset={offset}", flush=True)
+    g = torch.Generator().manual_seed(Vs + offset)
+    row = torch.randn(Vs, generator=g) - 6.0
+    idx = torch.randperm(Vs, generator=g)[:20]
+    row[idx] = torch.randn(20, generator=g) * 1.5
+    row = row.to(dtype).float()  # the values the kernel sees
+    n = 2048
+    # rows of a [n, Vs + offset] buffer viewed from column `offset` (misaligned when offset > 0)
+    store = torch.zeros(n, Vs + offset, dtype=dtype)
+    store[:, offset:] = row.to(dtype)
+    logits = store.to(gpu_device)[:, offset:]
+    for temp, top_p in ((0.0, 1.0), (1.0, 0.9)):
+        buf = dsm.SamplerBuffers(n, gpu_device)
+        buf.set_uniform(temp, top_p, 0)
+        buf.rng_key.fill_(7)
+        buf.rng_ctr.copy_(torch.arange(n, dtype=torch.int32, device=gpu_device))
+        tok = torch.empty(n, dtype=torch.int64, device=gpu_device)
+        lp = torch.empty(n, dtype=torch.float32, device=gpu_device)
+        dsm.sample_rows(logits, buf, rule=osm.RULE_BATCH, max_valid_id=None, seed=1, out_tok=tok, out_logp=lp)
+        torch.cuda.synchronize()
+        tok, lp = tok.cpu(), lp.cpu()
+        if temp == 0.0:
+            t, l = osm.greedy(row, max_valid_id=None)
+            assert bool((tok == t).all()) and float((lp - l).abs().max()) < 1e-4
+        else:
+            dist = osm.distribution(row, temperature=1.0, top_p=top_p, top_k=0, max_valid_id=None,
+                                    rule=osm.RULE_BATCH)
+            assert bool((dist[tok] > 0).all()), "a draw fell outside the kept set"
+            for i in range(0, n, 97):
+                assert abs(float(lp[i]) - osm.logp(dist, int(tok[i]), osm.RULE_BATCH)) < 1e-4
