@@ -161,3 +161,26 @@ def test_infctx_raw_module(gpu_device):
     assert torch.equal(y, y2.detach()) and torch.equal(s, s2.detach())
     for got, ref in zip(grads, [x.grad for x in leaves] + [st.grad]):
         assert torch.equal(got, ref)
+
+
+def test_train_kernels_fp16(gpu_device):
+    """The fp16 instantiation of both kernels: inputs rounded to fp16 first, the
+    oracle on the rounded values in float64; y and the gradients (fp16 outputs)
+    within 2e-3 of their largest magnitude, sa and the checkpoints (float32) within
+    1e-4.  T = 37 ends in a partial segment."""
+    print("[case] train kernels fp16 T=37", flush=True)
+    B, T, H = 2, 37, 2
+    xs = [x.half() for x in inputs(B, T, H, -6.0, -1.0, seed=41)]
+    g = torch.Generator().manual_seed(42)
+    dy = torch.randn(B, T, H, 64, generator=g).half()
+    r, w, k, v, a, b = (x.float() for x in xs)
+    y_o, sa_o, ck_o, _ = otr.train_forward(r, w, k, v, a, b)
+    grads_o = otr.train_backward(r, w, k, v, a, b, dy.float(), ck_o, sa_o)
+    rd, wd, kd, vd, ad, bd = (x.to(gpu_device).contiguous() for x in xs)
+    y, ck, sa = ops._train_forward(wd, rd, kd, vd, ad, bd)
+    dw, dr, dk, dv, da, db, _ = ops._train_backward(wd, rd, kd, vd, ad, bd, dy.to(gpu_device), ck, sa)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.float16
+    assert close(y, y_o, 2e-3) and close(sa, sa_o, 1e-4) and close(ck, ck_o, 1e-4)
+    for name, got, ref in zip(("dr", "dw", "dk", "dv", "da", "db"), (dr, dw, dk, dv, da, db), grads_o[:6]):
+        assert got.dtype == torch.float16 and close(got, ref, 2e-3), name
