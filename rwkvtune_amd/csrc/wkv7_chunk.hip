@@ -364,6 +364,7 @@ struct __attribute__((aligned(16))) ChunkLds2 {
     float tot[4][NH];   // per wave: log2-decay sums over its 8 tokens  [w][j]
     float DL[NH];       // decay over the whole chunk
     alignas(16) int slow[4];  // per wave: a token of the chunk decays below the floor
+    int pick;                 // the block's sequence (ragged batches, longest first)
 };
 
 __device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
@@ -484,11 +485,35 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
     constexpr bool kVExact = std::is_same<IO, bf16_t>::value;
     __shared__ ChunkLds2 sm;
     const int unit = blockIdx.x;
-    const int s = unit / H;
-    const int h = unit - s * H;
+    const int h = unit % H;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
+
+    // Ragged batches run longest sequence first: block group r takes the r-th
+    // longest sequence (ties by index, so every sequence is taken once), and the
+    // longest chains of chunks start earliest instead of stretching the launch's
+    // tail.  The lengths are ranked from LDS (the X buffer, unused until phase C).
+    int s = unit / H;
+    if (cu_seqlens != nullptr) {
+        const int nseq = (int)(gridDim.x / (unsigned)H);
+        if (nseq <= NH * TP) {
+            int* lens = reinterpret_cast<int*>(&sm.X[0][0]);
+            for (int c = tid; c < nseq; c += 256) lens[c] = cu_seqlens[c + 1] - cu_seqlens[c];
+            __syncthreads();
+            for (int c = tid; c < nseq; c += 256) {
+                const int len = lens[c];
+                int rank = 0;
+                for (int d = 0; d < nseq; ++d) {
+                    const int l2 = lens[d];
+                    rank += (l2 > len || (l2 == len && d < c)) ? 1 : 0;
+                }
+                if (rank == s) sm.pick = c;
+            }
+            __syncthreads();
+            s = sm.pick;
+        }
+    }
 
     const int tb = cu_seqlens != nullptr ? cu_seqlens[s] : s * T_uniform;
     const int te = cu_seqlens != nullptr ? cu_seqlens[s + 1] : tb + T_uniform;
