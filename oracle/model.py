@@ -16,9 +16,18 @@ The WKV recurrence is ``oracle.wkv7``: ``wkv7_cpu`` (the reference CPU operator,
 
 Pinning (tests/test_oracle_model.py): the float32 and float64 statements agree;
 prefill(T) equals T single-token steps; batch rows are independent; a layer with
-zeroed output projections is the identity on the residual stream; the LoRA and
-mix formulas are checked term by term against hand-computed special cases
-(decay softplus form, value-residual at sigmoid = 0/1, kk normalisation).
+zeroed output projections is the identity on the residual stream; one token
+from a zero state gives S = v k^T and a GroupNorm closed form.  Each term of the
+layer is then isolated on an otherwise transparent layer (identity projections,
+no shift, no LoRA, gate 1) and checked against values known by hand: the decay
+exp(-exp(-softplus(-w0) - 0.5)) at w0 = +30, 0, -30 over two tokens; the value
+residual at sigmoid = 1 and 0 (v_first taken, own value kept); the delta rule
+b = kk * a removing the fraction a of a unit state along kk (a = 1/2, 1/4); the
+key update k (1 + (a - 1) k_a) = 3/4 k; the bonus |x|^2 x; the token-shift
+direction (mix 1 reads the previous token); relu(x)^2 of the channel mix at
+six points and its shift.  Swapping the decay sign, the value-residual
+direction, b = kk for kk * a, relu for relu^2, the shift direction, the bonus
+axis or the gate's sigmoid placement each fails at least one of these.
 """
 
 from __future__ import annotations

@@ -17,6 +17,14 @@ the first token included.
 Greedy decoding (temperature 0) makes both deterministic, which is what the
 parity tests compare.  Sampled decoding uses ``torch.multinomial`` on the rule's
 distribution (``oracle.sampler.distribution``); it is only used for timing.
+
+Pinning (tests/test_oracle_rollout.py): every greedy path equals its prompt
+decoded alone by ``oracle.model.greedy_generate`` (no fork, no lockstep batch),
+cut by the stop rule - with duplicate prompts, per-path caps (cap 1 giving two
+tokens in GRPO), an EOS that ends some paths mid-way and one that ends a
+scheduler sequence on its first token; the lockstep loop runs exactly until the
+longest path ends.  A wrong cap comparison, a lost state write-back, a fork
+from the wrong prompt or a dropped EOS check each fails one of them.
 """
 
 from __future__ import annotations

@@ -137,3 +137,209 @@ def test_first_token_time_mix_closed_form():
     var_y = (kr ** 2) * (vc ** 2).mean(-1, keepdim=True)
     expect = kr * vc / torch.sqrt(var_y + 64e-5)
     assert torch.allclose(y.view(H, N), expect, rtol=1e-9, atol=1e-9)
+
+
+# ---------------------------------------------------------------------------
+# Closed forms that each isolate one term of the time mix / channel mix.  The
+# layer is first made transparent (identity projections, no token shift in the
+# mixes, zero LoRA downs, gate 1, no delta-rule or bonus term, identity
+# GroupNorm affine), then one term at a time is switched on at values whose
+# result is known by hand.  A slip in that term (a sign, a swapped lerp, a
+# dropped square or factor) fails the corresponding test.
+# ---------------------------------------------------------------------------
+
+def _transparent(sd, i, C):
+    p = f"blocks.{i}.att."
+    eye = torch.eye(C, dtype=torch.float64)
+    for n in ("receptance", "key", "value", "output"):
+        sd[p + n + ".weight"] = eye.clone()
+    for n in ("x_r", "x_w", "x_k", "x_v", "x_a", "x_g"):
+        sd[p + n] = torch.zeros_like(sd[p + n])
+    for n in ("w1", "a1", "g1") + (("v1",) if i > 0 else ()):
+        sd[p + n] = torch.zeros_like(sd[p + n])
+    # g = sigmoid(0) @ g2 with every g2 entry 2 / rank: g = 1 on every channel
+    sd[p + "g2"] = torch.full_like(sd[p + "g2"], 2.0 / sd[p + "g2"].shape[0])
+    for n in ("k_k", "k_a", "r_k", "a0"):
+        sd[p + n] = torch.zeros_like(sd[p + n])
+    sd[p + "w0"] = torch.full_like(sd[p + "w0"], -30.0)   # decay exp(-exp(-softplus(30) - .5)) = 1 - 6e-14
+    sd[p + "ln_x.weight"] = torch.ones(C, dtype=torch.float64)
+    sd[p + "ln_x.bias"] = torch.zeros(C, dtype=torch.float64)
+    return p
+
+
+def _run_time_mix(sd, i, x, v_first=None, S0=None):
+    cfg = om.config_of(sd)
+    B, T, C = x.shape
+    st = om.init_state(cfg, B)[i]
+    kv = st["att_kv"] if S0 is None else S0
+    return om.time_mix(sd, i, cfg, x, v_first, st["att_x_prev"], kv, torch.float64)
+
+
+def test_decay_softplus_form_closed_form():
+    """w = -softplus(-(w0 + w_lora)) - 0.5 with the decay exp(-exp(w)) applied by
+    the recurrence (model.py:227, wkv7s.cu:27).  With k_k = 0 (kk = 0: no
+    delta-rule term) and w1 = 0 (w_lora = 0), two tokens from a zero state leave
+    S = v1 k1^T diag(d) + v2 k2^T, with d known in closed form at three w0:
+      w0 = +30:  softplus(-30) ~ 0       -> d = exp(-e^-0.5)          = 0.5452392...
+      w0 =   0:  softplus(0) = ln 2      -> d = exp(-e^-0.5 / 2)      = 0.7384031...
+      w0 = -30:  softplus(30) ~ 30       -> d = exp(-e^-30.5) ~ 1."""
+    sd = tiny_sd(11, L=1)
+    C = 256
+    p = _transparent(sd, 0, C)
+    pattern = torch.tensor([30.0, 0.0, -30.0], dtype=torch.float64)
+    sd[p + "w0"] = pattern.repeat(C // 3 + 1)[:C].reshape(sd[p + "w0"].shape)
+    d_of = {30.0: math.exp(-math.exp(-0.5)), 0.0: math.exp(-math.exp(-0.5) / 2), -30.0: 1.0}
+    assert abs(d_of[30.0] - 0.5452392) < 1e-7 and abs(d_of[0.0] - 0.7384031) < 1e-7
+    d = torch.tensor([d_of[float(w)] for w in sd[p + "w0"].reshape(C)], dtype=torch.float64)
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(1, 2, C, generator=g, dtype=torch.float64)
+    _, _, _, S = _run_time_mix(sd, 0, x)
+    H = C // N
+    x1, x2, dh = x[0, 0].view(H, N), x[0, 1].view(H, N), d.view(H, N)
+    expect = x1[:, :, None] * (x1 * dh)[:, None, :] + x2[:, :, None] * x2[:, None, :]
+    assert torch.allclose(S[0], expect, rtol=1e-11, atol=1e-11)
+
+
+def test_value_residual_at_sigmoid_saturation():
+    """v <- v + (v_first - v) * sigmoid(v0 + v_lora) on layers > 0
+    (model.py:215-218): v0 = +40 (sigmoid = 1) takes v_first, v0 = -40
+    (sigmoid = 0) keeps the layer's own value.  One token from a zero state
+    gives S = v k^T, so row i of each head's state is v_i times k."""
+    sd = tiny_sd(13, L=2)
+    C = 256
+    H = C // N
+    p = _transparent(sd, 1, C)
+    v0 = torch.tensor([40.0 if (c // N) % 2 == 0 else -40.0 for c in range(C)], dtype=torch.float64)
+    sd[p + "v0"] = v0.reshape(sd[p + "v0"].shape)
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(1, 1, C, generator=g, dtype=torch.float64)
+    u = torch.randn(1, 1, C, generator=g, dtype=torch.float64)   # v_first from layer 0
+    _, vf, _, S = _run_time_mix(sd, 1, x, v_first=u)
+    assert vf is u
+    v_expect = torch.where(v0 > 0, u[0, 0], x[0, 0]).view(H, N)
+    k = x[0, 0].view(H, N)
+    assert torch.allclose(S[0], v_expect[:, :, None] * k[:, None, :], rtol=1e-12, atol=1e-12)
+
+
+def test_layer0_value_becomes_v_first():
+    sd = tiny_sd(15, L=2)
+    C = 256
+    _transparent(sd, 0, C)
+    g = torch.Generator().manual_seed(16)
+    x = torch.randn(1, 3, C, generator=g, dtype=torch.float64)
+    _, vf, _, _ = _run_time_mix(sd, 0, x)
+    assert torch.allclose(vf, x, rtol=0, atol=0)   # value projection = identity, no shift
+
+
+def test_delta_rule_uses_kk_times_a():
+    """The WKV call is WKV(r, w, k, v, -kk, kk*a) (model.py:246-247).  With the
+    value projection at zero (v = 0), a1 = 0 (a = sigmoid(a0)), decay 1, k_k = 1
+    and a token whose key is e_0 in every head (kk = e_0), one step from S0 = I
+    gives S1 = I - a_0 e_0 e_0^T: the delta rule removes the fraction a of the
+    state along kk.  Heads take a0 = 0 (a = 1/2) and a0 = ln(1/3) (a = 1/4):
+    S1[0, 0] = 1/2 and 3/4; every other entry stays that of I."""
+    sd = tiny_sd(17, L=1)
+    C = 256
+    H = C // N
+    p = _transparent(sd, 0, C)
+    sd[p + "value.weight"] = torch.zeros(C, C, dtype=torch.float64)
+    sd[p + "k_k"] = torch.ones_like(sd[p + "k_k"])
+    a0 = torch.tensor([0.0 if (c // N) % 2 == 0 else math.log(1.0 / 3.0) for c in range(C)], dtype=torch.float64)
+    sd[p + "a0"] = a0.reshape(sd[p + "a0"].shape)
+    x = torch.zeros(1, 1, C, dtype=torch.float64)
+    x[0, 0, ::N] = 3.0
+    S0 = torch.eye(N, dtype=torch.float64).expand(1, H, N, N).clone()
+    _, _, _, S = _run_time_mix(sd, 0, x, S0=S0)
+    expect = S0.clone()
+    for h in range(H):
+        expect[0, h, 0, 0] = 0.5 if h % 2 == 0 else 0.75
+    assert torch.allclose(S, expect, rtol=0, atol=1e-12)
+
+
+def test_key_update_by_a():
+    """k <- k * (1 + (a - 1) * k_a) (model.py:225): a = 1/2 (a0 = 0), k_a = 1/2
+    scales the key by 3/4, so one token from a zero state gives S = (3/4) v k^T."""
+    sd = tiny_sd(18, L=1)
+    C = 256
+    H = C // N
+    p = _transparent(sd, 0, C)
+    sd[p + "k_a"] = torch.full_like(sd[p + "k_a"], 0.5)
+    g = torch.Generator().manual_seed(19)
+    x = torch.randn(1, 1, C, generator=g, dtype=torch.float64)
+    _, _, _, S = _run_time_mix(sd, 0, x)
+    xv = x[0, 0].view(H, N)
+    assert torch.allclose(S[0], 0.75 * xv[:, :, None] * xv[:, None, :], rtol=1e-12, atol=1e-12)
+
+
+def test_bonus_term():
+    """out += (sum_head r * k * r_k) * v (model.py:267-268): with the GroupNorm
+    affine at zero only the bonus reaches the output; r = k = v = x and r_k = 1
+    give out_head = |x_head|^2 x_head."""
+    sd = tiny_sd(20, L=1)
+    C = 256
+    H = C // N
+    p = _transparent(sd, 0, C)
+    sd[p + "r_k"] = torch.ones_like(sd[p + "r_k"])
+    sd[p + "ln_x.weight"] = torch.zeros(C, dtype=torch.float64)
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(1, 1, C, generator=g, dtype=torch.float64)
+    y, _, _, _ = _run_time_mix(sd, 0, x)
+    xh = x[0, 0].view(H, N)
+    assert torch.allclose(y[0, 0].view(H, N), (xh * xh).sum(-1, keepdim=True) * xh, rtol=1e-12, atol=1e-12)
+
+
+def test_token_shift_lerp_direction():
+    """x_mix = x + (x_prev - x) * mix (model.py:196-208): mix = 1 feeds the
+    previous token.  With x_r = 1 and everything else transparent, token 2's
+    receptance is token 1, so y_2 = GroupNorm(S_2 x_1) with S_2 = x_1 x_1^T +
+    x_2 x_2^T; and mix = 0 (x_r = 0) reads x_2 itself."""
+    sd = tiny_sd(22, L=1)
+    C = 256
+    H = C // N
+    p = _transparent(sd, 0, C)
+    g = torch.Generator().manual_seed(23)
+    x = torch.randn(1, 2, C, generator=g, dtype=torch.float64)
+    x1, x2 = x[0, 0].view(H, N), x[0, 1].view(H, N)
+    S2 = x1[:, :, None] * x1[:, None, :] + x2[:, :, None] * x2[:, None, :]
+
+    def gn(y):
+        yc = y - y.mean(-1, keepdim=True)
+        return yc / torch.sqrt((yc ** 2).mean(-1, keepdim=True) + 64e-5)
+
+    for mix, rvec in ((1.0, x1), (0.0, x2)):
+        sd[p + "x_r"] = torch.full_like(sd[p + "x_r"], mix)
+        y, _, x_last, _ = _run_time_mix(sd, 0, x)
+        assert torch.allclose(x_last, x[:, -1], rtol=0, atol=0)
+        y2 = torch.einsum("hij,hj->hi", S2, rvec)
+        assert torch.allclose(y[0, 1].view(H, N), gn(y2), rtol=1e-9, atol=1e-9)
+
+
+def test_channel_mix_relu_squared_and_shift():
+    """FFN = value(relu(key(x + (x_prev - x) * x_k))^2) (model.py:315-338).  With
+    key = [I; 0] and value = [I, 0] the output is relu(input)^2 per channel, at
+    hand-evaluated points: -2 -> 0, -0.5 -> 0, 0 -> 0, 0.5 -> 0.25, 2 -> 4,
+    3 -> 9.  x_k = 0 reads the token, x_k = 1 the previous token."""
+    sd = tiny_sd(24, L=1)
+    C = 256
+    p = "blocks.0.ffn."
+    key = torch.zeros(4 * C, C, dtype=torch.float64)
+    key[:C] = torch.eye(C, dtype=torch.float64)
+    val = torch.zeros(C, 4 * C, dtype=torch.float64)
+    val[:, :C] = torch.eye(C, dtype=torch.float64)
+    sd[p + "key.weight"], sd[p + "value.weight"] = key, val
+    table = {-2.0: 0.0, -0.5: 0.0, 0.0: 0.0, 0.5: 0.25, 2.0: 4.0, 3.0: 9.0}
+    pts = torch.tensor(list(table), dtype=torch.float64).repeat(C // 6 + 1)[:C]
+    want = torch.tensor([table[float(v)] for v in pts], dtype=torch.float64)
+    g = torch.Generator().manual_seed(25)
+    other = torch.randn(C, generator=g, dtype=torch.float64)
+    # x_k = 0: the token's own value
+    sd[p + "x_k"] = torch.zeros_like(sd[p + "x_k"])
+    out, last = om.channel_mix(sd, 0, pts.view(1, 1, C), other.view(1, C))
+    assert torch.allclose(out[0, 0], want, rtol=0, atol=1e-14)
+    assert torch.equal(last[0], pts)
+    # x_k = 1: the previous token (x_prev for the first, token 1 for token 2)
+    sd[p + "x_k"] = torch.ones_like(sd[p + "x_k"])
+    seq = torch.stack([other, pts]).view(1, 2, C)
+    out, _ = om.channel_mix(sd, 0, seq, pts.view(1, C))
+    assert torch.allclose(out[0, 0], want, rtol=0, atol=1e-14)
+    assert torch.allclose(out[0, 1], torch.clamp(other, min=0) ** 2, rtol=1e-14, atol=1e-14)
