@@ -63,13 +63,14 @@ if ROOT not in sys.path:
 
 import torch  # noqa: E402
 
+from rwkvtune_amd.workloads import MAX_VALID_ID, cfg4_workload, cfg5_workload  # noqa: E402
+
 PEAK_HBM_GBS = 8000.0          # MI355X datasheet HBM3E bandwidth
 METRIC = "rollout tokens/s (RWKV7-1.5B, 512 seqs); WKV7 decode HBM GB/s vs peak"
 N = 64
 # algorithmic bytes per (slot, head) unit of one decode step
 WKV_BYTES_PER_UNIT = 2 * N * N * 4 + 6 * N * 2 + N * 2          # state r+w, 6 bf16 inputs, bf16 y
 TMIX_BYTES_PER_UNIT = 2 * N * N * 4 + 7 * N * 2 + N * 4 + N * 2  # state r+w, 7 bf16 inputs, fp32 v_first, bf16 out
-MAX_VALID_ID = 65529
 
 
 def log(msg):
@@ -86,16 +87,6 @@ class NullTokenizer:
 
     def decode(self, ids):
         return ""
-
-
-def cfg4_workload(seed=4):
-    g = torch.Generator().manual_seed(seed)
-    lens = torch.randint(256, 2049, (64,), generator=g).tolist()
-    prompts = [torch.randint(1, MAX_VALID_ID + 1, (L,), generator=g).tolist() for L in lens]
-    # Geometric(p = 1/300) on {1, 2, ...}, capped at 512
-    u = torch.rand(64 * 8, generator=g, dtype=torch.float64)
-    caps = torch.clamp(torch.ceil(torch.log1p(-u) / torch.log1p(torch.tensor(-1.0 / 300))), 1, 512)
-    return prompts, [int(c) for c in caps]
 
 
 def time_launches(fn, n_iter, stream):
@@ -128,16 +119,6 @@ def copy_reference(dev, n_bytes=256 * 32 * 64 * 64 * 4, reps=8):
         dst.copy_(src)
     torch.cuda.synchronize()
     return n_bytes
-
-
-def cfg5_workload(seed=5):
-    """cfg5: 128 random 2048-token prompts; per-sequence stop length
-    ~ Geometric(mean 600) capped at 1024."""
-    g = torch.Generator().manual_seed(seed)
-    prompts = [torch.randint(1, MAX_VALID_ID + 1, (2048,), generator=g).tolist() for _ in range(128)]
-    u = torch.rand(128, generator=g, dtype=torch.float64)
-    caps = torch.clamp(torch.ceil(torch.log1p(-u) / torch.log1p(torch.tensor(-1.0 / 600))), 1, 1024)
-    return prompts, [int(c) for c in caps]
 
 
 def tmix_decode_leg(dev, iters=480, S=256, H=32, L=24):

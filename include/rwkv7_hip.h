@@ -273,8 +273,10 @@ int rwkv7_gemm_pack(const void *B, int64_t ldb, int N, int K, void *out, void *s
  * active (uint8 [M], nullable): rows with 0 are skipped.  Draws use a
  * counter-based hash of (seed, rng_key[m], rng_ctr[m]).  rule 1 =
  * TokenSampler.sample (rwkvtune/inference/core.py:40-137), rule 0 =
- * TokenSampler.sample_batch (core.py:142-236); see sampler.hip for the exact
- * rules.  Replaces both methods' torch op chains (softmax, sort, cumsum,
+ * TokenSampler.sample_batch (core.py:142-236), rule 2 =
+ * GenerationMixin.generate (rwkvtune/models/generation_mixin.py:180-211:
+ * top-k, then top-p only when 0 < top_p < 1, keeping the crossing token); see
+ * sampler.hip for the exact rules.  Replaces both methods' torch op chains (softmax, sort, cumsum,
  * multinomial, gather) and their per-sequence .item() synchronisations.
  */
 int rwkv7_sample(int dtype, int64_t M, int64_t V, const void *logits, int64_t ld, int rule,

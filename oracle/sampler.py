@@ -10,6 +10,11 @@
     RULE_BATCH = ``TokenSampler.sample_batch`` (``core.py:142-236``): top_k keeps
     the k largest logits, then top_p keeps the sorted prefix with cumsum <= p and
     always the first entry (``:214-228``); softmax over what is kept.
+    RULE_MIXIN = ``GenerationMixin.generate`` (``rwkvtune/models/generation_mixin.py:
+    180-211``): softmax; top_k > 0 keeps the k most probable and renormalises;
+    then, only when 0 < top_p < 1, the sorted entries whose preceding cumulative
+    sum is <= p (the shifted ``cumsum > p`` mask: the crossing entry is kept, the
+    first always) and renormalises.  No id ban (the caller passes none).
 ``logp(...)``          the log-probability the reference returns for a token.
 ``greedy(...)``        argmax of the banned logits (first index on ties) and its
     log_softmax (``core.py:80-83, 184-188``).
@@ -28,6 +33,7 @@ import torch
 
 RULE_BATCH = 0
 RULE_SINGLE = 1
+RULE_MIXIN = 2
 
 
 def _prep(logits, temperature, logit_bias, max_valid_id):
@@ -49,6 +55,21 @@ def distribution(logits, temperature=1.0, top_p=1.0, top_k=0, logit_bias=None,
     x = _prep(logits, temperature, logit_bias, max_valid_id)
     V = x.shape[-1]
     order = torch.sort(-x, stable=True).indices  # descending, ties by index
+    if rule == RULE_MIXIN:
+        probs = torch.softmax(x, -1)
+        if top_k > 0:
+            kept = torch.zeros(V, dtype=torch.float64)
+            kept[order[:min(top_k, V)]] = probs[order[:min(top_k, V)]]
+            probs = kept / kept.sum()
+        if 0.0 < top_p < 1.0:
+            o2 = torch.sort(-probs, stable=True).indices
+            cs = torch.cumsum(probs[o2], 0)
+            remove = torch.zeros(V, dtype=torch.bool)
+            remove[1:] = cs[:-1] > top_p
+            kept = probs.clone()
+            kept[o2[remove]] = 0.0
+            probs = kept / kept.sum()
+        return probs
     if rule == RULE_SINGLE:
         probs = torch.softmax(x, -1)
         if not torch.isfinite(probs).all():
@@ -83,7 +104,7 @@ def distribution(logits, temperature=1.0, top_p=1.0, top_k=0, logit_bias=None,
 
 def logp(dist, token, rule):
     p = float(dist[token])
-    if rule == RULE_SINGLE:
+    if rule in (RULE_SINGLE, RULE_MIXIN):
         return float(torch.log(torch.tensor(p + 1e-10, dtype=torch.float64)))
     return float(torch.log(torch.tensor(p, dtype=torch.float64)))
 

@@ -373,7 +373,8 @@ extern "C" int rwkv7_sample(int dtype, int64_t M, int64_t V, const void* logits,
     if (M < 0 || M > kMaxInt || V <= 0 || V > sampler_max_vocab() || ld < V)
         return fail(RWKV7_ERR_INVALID, "rwkv7_sample: bad sizes M=%lld V=%lld ld=%lld (V <= %d)", (long long)M,
                     (long long)V, (long long)ld, sampler_max_vocab());
-    if (rule != 0 && rule != 1) return fail(RWKV7_ERR_INVALID, "rwkv7_sample: rule must be 0 (batch) or 1 (single)");
+    if (rule < 0 || rule > 2)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_sample: rule must be 0 (batch), 1 (single) or 2 (generate)");
     if (M == 0) return ok();
     if (!logits || !temperature || !top_p || !top_k || !rng_key || !rng_ctr || !out_tok || !out_logp)
         return fail(RWKV7_ERR_INVALID, "rwkv7_sample: null pointer");

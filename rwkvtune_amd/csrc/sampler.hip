@@ -13,6 +13,10 @@
 //   * RULE_BATCH (TokenSampler.sample_batch, core.py:142-236): top_k keeps the k
 //     largest logits, then top_p keeps the sorted prefix with cumsum <= top_p and
 //     always the first token (core.py:214-228); logp = log_softmax(filtered)[token].
+//   * RULE_MIXIN (GenerationMixin.generate, rwkvtune/models/generation_mixin.py:
+//     188-211): top_k keeps the k largest, then - only when 0 < top_p < 1 - the
+//     renormalised nucleus up to and including the crossing token (the shifted
+//     cumsum > top_p mask); logp = log(renormalised p + 1e-10).
 //
 // Design: one 1024-thread block per row; the row (V <= 65536) lives in registers,
 // 64 values per thread, read with 16-byte loads (layout at load_row).  A token is the bit pattern of
@@ -36,7 +40,7 @@ constexpr int kTG = 1024, kVPTG = 64;
 constexpr int kWMax = 16;  // waves of the larger block
 constexpr int kBins = 1024;  // radix bins per level (one per thread)
 
-enum { RULE_BATCH = 0, RULE_SINGLE = 1 };
+enum { RULE_BATCH = 0, RULE_SINGLE = 1, RULE_MIXIN = 2 };
 
 // Row layout in registers: thread t holds x[8c + e] = element 8192 c + 8 t + e
 // (c < 8, e < 8), so each group of 8 is one 16-byte load of a 16-bit row.
@@ -331,7 +335,8 @@ __global__ __launch_bounds__(kT) void sample_kernel(
         for (int j = 0; j < kVPT; ++j) sk += key[j] >= lo ? __uint_as_float(key[j]) : 0.f;
         W = block_sum_f(sk, &red);
     }
-    const bool nucleus = !uniform && p < 1.0f && (rule == RULE_BATCH || k <= 0);
+    const bool nucleus = !uniform && p < 1.0f &&
+                         (rule == RULE_BATCH || (rule == RULE_MIXIN && p > 0.f) || (rule == RULE_SINGLE && k <= 0));
     if (nucleus) {
         // the key of the token whose inclusion crosses p: the highest K' with
         // mass(key >= max(K', lo)) > p * mass(key >= lo), in fixed point
@@ -343,9 +348,9 @@ __global__ __launch_bounds__(kT) void sample_kernel(
         const uint32_t b3 = radix_level<false>(key, lo, 0, (b1 << 10) | b2, false, above, target, 0.f, bins, wsum,
                                                &pick_bin, &pick_val);
         const uint32_t K = (b1 << 20) | (b2 << 10) | b3;
-        // RULE_SINGLE keeps the crossing token, RULE_BATCH stops before it but
-        // always keeps the most probable token (q = 1)
-        uint32_t nlo = (rule == RULE_SINGLE) ? K : K + 1u;
+        // RULE_SINGLE and RULE_MIXIN keep the crossing token, RULE_BATCH stops
+        // before it but always keeps the most probable token (q = 1)
+        uint32_t nlo = (rule == RULE_BATCH) ? K + 1u : K;
         const uint32_t top = __float_as_uint(1.0f);
         if (nlo > top) nlo = top;
         lo = nlo > lo ? nlo : lo;
@@ -370,7 +375,10 @@ __global__ __launch_bounds__(kT) void sample_kernel(
     for (int j = 0; j < kVPT; ++j) tm += key[j] >= lo ? __uint_as_float(key[j]) : 0.f;
     if (tid == 0) pick = -1;
     const float acc = block_incl_scan(tm, fsum);  // [before, acc) of consecutive threads tile [0, total)
-    if (tid == kT - 1) fsum[0] = acc;             // total (fsum is free once every thread has its offset)
+    // every wave reads fsum[0 .. w-1] at the end of the scan: wait for all of
+    // them before fsum[0] is reused for the total
+    __syncthreads();
+    if (tid == kT - 1) fsum[0] = acc;             // total
     __syncthreads();
     const float total = fsum[0];
     const float target = u * total;
@@ -400,7 +408,7 @@ __global__ __launch_bounds__(kT) void sample_kernel(
             if (j == slot_of(tok)) kq = key[j];
         const float q = __uint_as_float(kq);
         out_tok[row] = tok;
-        out_logp[row] = (rule == RULE_SINGLE) ? logf(q / W + 1e-10f) : logf(q) - logf(W);
+        out_logp[row] = (rule == RULE_BATCH) ? logf(q) - logf(W) : logf(q / W + 1e-10f);
     }
 }
 

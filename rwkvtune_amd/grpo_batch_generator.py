@@ -17,6 +17,11 @@ Semantics kept from the reference:
   * results: ``completions`` (decoded strings), ``completion_ids`` (LongTensor
     ``[B*G, max_len]``, 0-padded, on the model's device), ``masks`` (bool).
 
+``model`` may be an ``rwkvtune_amd.RWKV7Model`` or any module with the
+reference model's parameter names - the trainer's own model: its parameters
+are used in place (``as_hip_model``) and parameter updates between calls are
+picked up without any call from the trainer.
+
 Differences, on purpose: decoding runs on the GPU slot table
 (``rwkvtune_amd.engine``) with ``max_decode_batch_size`` slots (all paths when
 -1, capped at 1024) and continuous refill instead of a shrinking lockstep batch;
@@ -37,6 +42,7 @@ import torch
 
 from ._common import decode_tokens, dedupe, max_valid_token_id
 from .engine import RolloutEngine
+from .model import as_hip_model
 from .sampler import RULE_BATCH, RULE_SINGLE, TokenSampler
 
 
@@ -44,6 +50,9 @@ class GRPOBatchGenerator:
     def __init__(self, model, tokenizer, chunk_size: int = 2048, max_prefill_batch_size: int = -1,
                  max_decode_batch_size: int = -1, eos_token_id: Optional[int] = None, *, verbose: bool = True):
         self.model = model
+        # the caller's module (e.g. GRPOTrainer's training model) runs through a
+        # wrapper that shares its parameters; packed copies follow their updates
+        self._hip = as_hip_model(model)
         self.tokenizer = tokenizer
         self.device = next(model.parameters()).device
         self.dtype = next(model.parameters()).dtype
@@ -52,8 +61,8 @@ class GRPOBatchGenerator:
         self.max_decode_batch_size = max_decode_batch_size
         self.eos_token_id = eos_token_id
         self.sampler = TokenSampler
-        self.n_layer = model.config.n_layer
-        self.n_embd = model.config.n_embd
+        self.n_layer = self._hip.config.n_layer
+        self.n_embd = self._hip.config.n_embd
         self.verbose = verbose
         mv = max_valid_token_id(tokenizer)
         if mv is not None:
@@ -65,7 +74,7 @@ class GRPOBatchGenerator:
     def _engine(self, slots: int) -> RolloutEngine:
         eng = self._engines.get(slots)
         if eng is None:
-            eng = RolloutEngine(self.model, slots, eos_token_id=self.eos_token_id,
+            eng = RolloutEngine(self._hip, slots, eos_token_id=self.eos_token_id,
                                 max_valid_id=TokenSampler._max_valid_token_id)
             self._engines = {slots: eng}
         return eng

@@ -28,6 +28,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import weakref
 from dataclasses import dataclass, field
 from typing import List, Optional, Sequence
 
@@ -276,68 +277,111 @@ class PackedWeight:
         n = _lib.load().rwkv7_gemm_packed_elems(self.N, self.K)
         if n < 0:
             raise ValueError("rwkv7_gemm_packed_elems: " + _lib.load().rwkv7_last_error().decode())
-        w = weight if weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0 else weight.contiguous()
         self.t = torch.empty(n, dtype=torch.bfloat16, device=weight.device)
+        self.pack(weight)
+
+    def pack(self, weight: torch.Tensor):
+        """(Re)write the packed copy from ``weight`` (same shape) into the same buffer."""
+        if tuple(weight.shape) != (self.N, self.K):
+            raise ValueError(f"repack of a {self.N} x {self.K} weight from {tuple(weight.shape)}")
+        w = weight if weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0 else weight.contiguous()
         _lib.call("rwkv7_gemm_pack", _lib.ptr(w), w.stride(0), self.N, self.K, _lib.ptr(self.t),
                   _lib.stream_of(self.t))
 
 
 class _LayerPack:
-    """float32 copies of one layer's per-channel parameters, laid out for the kernels."""
+    """float32 copies of one layer's per-channel parameters, laid out for the
+    kernels, and (bf16 models) the packed decode-GEMM weights.  ``refresh``
+    rewrites every copy from the current parameters into the same buffers, so
+    kernel argument pointers (and the pointer table ``tparams``) stay valid."""
 
     def __init__(self, blk: RWKV7Block, C: int):
-        att, ffn = blk.att, blk.ffn
-
-        def f32(t):
-            return t.detach().reshape(-1).to(torch.float32).contiguous()
-
+        self.C = C
         self.layer0 = blk.layer_id == 0
-        self.use_ln0 = self.layer0 and not blk.skip_ln0
-        self.ln0 = (f32(blk.ln0.weight), f32(blk.ln0.bias)) if self.use_ln0 else None
-        self.ln1 = (f32(blk.ln1.weight), f32(blk.ln1.bias))
-        self.ln2 = (f32(blk.ln2.weight), f32(blk.ln2.bias))
+        self.gp = {}
+        self._fill(blk, alloc=True)
+
+    def refresh(self, blk: RWKV7Block):
+        self._fill(blk, alloc=False)
+
+    @staticmethod
+    def _f32(t):
+        return t.detach().reshape(-1).to(torch.float32).contiguous()
+
+    def _set(self, name, value, alloc):
+        if alloc:
+            setattr(self, name, value)
+        else:
+            getattr(self, name).copy_(value)
+
+    def _fill(self, blk: RWKV7Block, alloc: bool):
+        att, ffn = blk.att, blk.ffn
+        C = self.C
+        f32 = self._f32
+        use_ln0 = self.layer0 and not blk.skip_ln0
+        if alloc:
+            self.use_ln0 = use_ln0
+        elif use_ln0 != self.use_ln0:
+            raise RuntimeError("skip_ln0 changed: rebuild the packs")
+        if use_ln0:
+            self._set("ln0_w", f32(blk.ln0.weight), alloc)
+            self._set("ln0_b", f32(blk.ln0.bias), alloc)
+        self.ln0 = (self.ln0_w, self.ln0_b) if use_ln0 else None
+        for nm, ln in (("ln1", blk.ln1), ("ln2", blk.ln2)):
+            self._set(nm + "_w", f32(ln.weight), alloc)
+            self._set(nm + "_b", f32(ln.bias), alloc)
+        self.ln1 = (self.ln1_w, self.ln1_b)
+        self.ln2 = (self.ln2_w, self.ln2_b)
         # seven mixes, in the order the projections consume them: r, k, v (one
         # batched GEMM), then the LoRA inputs w, a, g, v (one batched GEMM)
-        self.mix7 = torch.stack([f32(getattr(att, n)) for n in ("x_r", "x_k", "x_v", "x_w", "x_a", "x_g", "x_v")])
-        self.mixk = f32(ffn.x_k).reshape(1, C)
-        zero = torch.zeros(C, dtype=torch.float32, device=self.mix7.device)
-        self.tvecs = [f32(att.w0), f32(att.a0), f32(att.v0) if not self.layer0 else zero,
-                      f32(att.k_k), f32(att.k_a), f32(att.r_k), f32(att.ln_x.weight), f32(att.ln_x.bias)]
-        ptrs = [t.data_ptr() for t in self.tvecs]
-        if self.layer0:
-            ptrs[2] = 0
-        self.tparams = (ctypes.c_void_p * 8)(*ptrs)
+        self._set("mix7", torch.stack([f32(getattr(att, n)) for n in ("x_r", "x_k", "x_v", "x_w", "x_a", "x_g",
+                                                                        "x_v")]), alloc)
+        self._set("mixk", f32(ffn.x_k).reshape(1, C), alloc)
+        dev = self.mix7.device
+        zero = torch.zeros(C, dtype=torch.float32, device=dev)
+        tv = [f32(att.w0), f32(att.a0), f32(att.v0) if not self.layer0 else zero,
+              f32(att.k_k), f32(att.k_a), f32(att.r_k), f32(att.ln_x.weight), f32(att.ln_x.bias)]
+        if alloc:
+            self.tvecs = tv
+            ptrs = [t.data_ptr() for t in self.tvecs]
+            if self.layer0:
+                ptrs[2] = 0
+            self.tparams = (ctypes.c_void_p * 8)(*ptrs)
+        else:
+            for dst, src in zip(self.tvecs, tv):
+                dst.copy_(src)
         # Batched projection weights ([batch][in][out], contiguous: the right
         # operand of a batched GEMM must not be a transposed view): r/k/v, and the
         # LoRA pairs zero-padded to a common rank D (padded down-columns give 0,
         # whose activation meets zero up-rows, so padding adds nothing).
         with torch.no_grad():
-            self.w_rkv = torch.stack([att.receptance.weight.detach().t(), att.key.weight.detach().t(),
-                                      att.value.weight.detach().t()]).contiguous()
+            self._set("w_rkv", torch.stack([att.receptance.weight.detach().t(), att.key.weight.detach().t(),
+                                            att.value.weight.detach().t()]).contiguous(), alloc)
             downs = [att.w1, att.a1, att.g1] + ([] if self.layer0 else [att.v1])
             ups = [att.w2, att.a2, att.g2] + ([] if self.layer0 else [att.v2])
-            D = max(d.shape[1] for d in downs)
-            D = (D + 31) // 32 * 32
-            dt = att.w1.dtype
-            self.lora_down = torch.zeros((len(downs), C, D), dtype=dt, device=att.w1.device)
-            self.lora_up = torch.zeros((len(ups), D, C), dtype=dt, device=att.w1.device)
+            if alloc:
+                D = max(d.shape[1] for d in downs)
+                D = (D + 31) // 32 * 32
+                dt = att.w1.dtype
+                self.lora_down = torch.zeros((len(downs), C, D), dtype=dt, device=att.w1.device)
+                self.lora_up = torch.zeros((len(ups), D, C), dtype=dt, device=att.w1.device)
             for i, (dn, up) in enumerate(zip(downs, ups)):
                 self.lora_down[i, :, :dn.shape[1]] = dn.detach()
                 self.lora_up[i, :up.shape[0], :] = up.detach()
         # decode-GEMM weights of bf16 models, packed: r / k / v, the LoRA downs
         # and ups as [out][in] matrices, the output projection, the FFN key and value
-        self.gp = {}
         if att.w1.dtype == torch.bfloat16:
             with torch.no_grad():
-                self.gp = {"r": PackedWeight(att.receptance.weight.detach()),
-                           "k": PackedWeight(att.key.weight.detach()),
-                           "v": PackedWeight(att.value.weight.detach()),
-                           "o": PackedWeight(att.output.weight.detach()),
-                           "fk": PackedWeight(ffn.key.weight.detach()),
-                           "fv": PackedWeight(ffn.value.weight.detach())}
+                mats = {"r": att.receptance.weight, "k": att.key.weight, "v": att.value.weight,
+                        "o": att.output.weight, "fk": ffn.key.weight, "fv": ffn.value.weight}
                 names = ("w1", "a1", "g1", "w2", "a2", "g2") + (() if self.layer0 else ("v1", "v2"))
                 for n in names:
-                    self.gp[n] = PackedWeight(getattr(att, n).detach().t().contiguous())
+                    mats[n] = getattr(att, n).detach().t().contiguous()
+                for n, wt in mats.items():
+                    if alloc:
+                        self.gp[n] = PackedWeight(wt.detach())
+                    else:
+                        self.gp[n].pack(wt.detach())
 
 
 class RWKV7Model(nn.Module):
@@ -351,6 +395,8 @@ class RWKV7Model(nn.Module):
         self.ln_out = nn.LayerNorm(config.n_embd)
         self.head = nn.Linear(config.n_embd, config.vocab_size, bias=False)
         self._packs = None
+        self._packs_key = None
+        self._packs_struct = None
         # decode rows of a bf16 model run their projections on the library's
         # grouped MFMA GEMM over packed weights: r, k, v and the LoRA downs (tanh /
         # sigmoid fused) in one launch, the LoRA ups in one, the FFN key (relu^2
@@ -365,7 +411,8 @@ class RWKV7Model(nn.Module):
     # -- bookkeeping ---------------------------------------------------------
 
     def invalidate(self):
-        """Drop cached float32 parameter packs (call after changing parameters)."""
+        """Drop the cached parameter packs; the next forward rebuilds them.  (Not
+        needed after in-place parameter updates, which ``packs`` detects.)"""
         self._packs = None
 
     def _apply(self, fn, *args, **kwargs):
@@ -404,14 +451,37 @@ class RWKV7Model(nn.Module):
             raise RuntimeError("RWKV7Model runs on the HIP library only; move it to a GPU device first")
         _lib.load()
 
+    def _param_key(self):
+        """(data_ptr, version) of every parameter: an in-place update (an
+        optimizer step, ``copy_``, ``mul_`` ...) bumps the version, a move or
+        reassignment changes the pointer."""
+        return tuple((p.data_ptr(), p._version) for p in self.parameters())
+
+    def _struct_key(self):
+        return (tuple((p.device, p.dtype, tuple(p.shape)) for p in self.parameters()),
+                tuple(b.skip_ln0 for b in self.blocks))
+
     def packs(self):
-        if self._packs is None:
-            self._check_device()
-            C = self.config.n_embd
-            with torch.no_grad():
+        """The kernels' parameter packs, rebuilt or refreshed whenever a parameter
+        changed since they were made (no ``invalidate()`` needed after an
+        optimizer step that updates the parameters in place)."""
+        key = self._param_key()
+        if self._packs is not None and key == self._packs_key:
+            return self._packs
+        self._check_device()
+        C = self.config.n_embd
+        with torch.no_grad():
+            if self._packs is not None and self._struct_key() == self._packs_struct:
+                for pk, b in zip(self._packs, self.blocks):
+                    pk.refresh(b)
+                self._ln_out[0].copy_(self.ln_out.weight.detach().float())
+                self._ln_out[1].copy_(self.ln_out.bias.detach().float())
+            else:
                 self._packs = [_LayerPack(b, C) for b in self.blocks]
                 self._ln_out = (self.ln_out.weight.detach().float().contiguous(),
                                 self.ln_out.bias.detach().float().contiguous())
+                self._packs_struct = self._struct_key()
+        self._packs_key = key
         return self._packs
 
     def init_state(self, batch_size: int):
@@ -705,6 +775,129 @@ class RWKV7Model(nn.Module):
         return logits.view(B, keep, -1)
 
 
+    @torch.no_grad()
+    def generate(self, input_ids: Optional[torch.Tensor] = None, inputs: Optional[torch.Tensor] = None,
+                 max_new_tokens: Optional[int] = None, max_length: Optional[int] = None,
+                 min_length: Optional[int] = None, do_sample: bool = True, temperature: float = 1.0,
+                 top_k: int = 0, top_p: float = 1.0, repetition_penalty: float = 1.0,
+                 num_return_sequences: int = 1, eos_token_id=None, pad_token_id: Optional[int] = None,
+                 token_ban: Optional[Sequence[int]] = None, return_dict_in_generate: bool = False,
+                 output_scores: bool = False, initial_states=None, seed: Optional[int] = None, **kwargs):
+        """Transformers-style generation with the semantics of the reference's
+        ``GenerationMixin.generate`` (``rwkvtune/models/generation_mixin.py:33-225``):
+
+        * ``input_ids`` ``[B, T]`` or ``[T]``; ``num_return_sequences`` repeats each
+          row; ``max_new_tokens``, else ``max_length - T``, else 512 new tokens;
+        * ``do_sample=False`` or ``temperature == 0`` is greedy argmax over the
+          whole vocabulary (no id ban); otherwise temperature, ``token_ban`` (-inf),
+          top-k and then, when 0 < top_p < 1, the nucleus keeping the crossing
+          token (sampler rule 2); the repetition penalty counts every occurrence in
+          the row's input and generated ids;
+        * a row stops counting as unfinished when it emits an id of
+          ``eos_token_id`` (an int or a list); generation ends when every row has,
+          finished rows keep generating until then, as in the reference;
+        * returns ``[B * num_return_sequences, T + generated]`` int64 (the input
+          included), or ``{"sequences": ...}`` with ``return_dict_in_generate``.
+
+        The prompt is prefilled in one ragged call and each new token is one
+        pooled decode step; sampling is the device sampler (draws from its
+        counter-based stream, keyed by ``seed``), so sampled tokens follow the
+        reference's distribution, not ``torch.multinomial``'s stream.
+        ``min_length``, ``pad_token_id`` and ``output_scores`` are accepted and,
+        as in the reference, unused."""
+        from .sampler import RULE_MIXIN, SamplerBuffers, TokenSampler, repetition_penalty_, sample_rows
+        self._check_device()
+        if input_ids is None:
+            input_ids = inputs
+        if input_ids is None:
+            raise ValueError("Must provide input_ids or inputs parameter")
+        if input_ids.dim() == 1:
+            input_ids = input_ids.unsqueeze(0)
+        B, T = input_ids.shape
+        if T == 0:
+            raise ValueError("generate needs at least one input token per row")
+        if max_new_tokens is not None:
+            n_new = int(max_new_tokens)
+        elif max_length is not None:
+            n_new = int(max_length) - T
+        else:
+            n_new = 512
+        if eos_token_id is None:
+            eos_token_id = getattr(self.config, "eos_token_id", None)
+        eos = [] if eos_token_id is None else ([int(eos_token_id)] if isinstance(eos_token_id, int)
+                                               else [int(e) for e in eos_token_id])
+        if not do_sample:
+            temperature, top_p, top_k = 1.0, 0.0, 0
+        greedy = (not do_sample) or temperature == 0
+        if num_return_sequences > 1:
+            input_ids = input_ids.repeat_interleave(num_return_sequences, dim=0)
+            B = B * num_return_sequences
+        dev = self.device
+        cfg = self.config
+        ids = input_ids.to(device=dev, dtype=torch.int64)
+        if n_new <= 0:
+            return {"sequences": ids.clone()} if return_dict_in_generate else ids.clone()
+        pool = StatePool(cfg, B, dev)
+        if initial_states is not None:
+            if len(initial_states) != cfg.n_layer:
+                raise ValueError(f"expected {cfg.n_layer} layer states, got {len(initial_states)}")
+            for l, st in enumerate(initial_states):
+                pool.att_x[l].copy_(st["att_x_prev"].reshape(B, -1))
+                pool.kv[l].copy_(st["att_kv"].reshape(pool.kv[l].shape))
+                pool.ffn_x[l].copy_(st["ffn_x_prev"].reshape(B, -1))
+        slot, last, cu, seq_slot = self._meta_uniform(B, T, dev)
+        last_rows = (torch.arange(B, device=dev, dtype=torch.int32) * T + (T - 1)).contiguous()
+        logits = self.forward_pooled(ids.reshape(-1).contiguous(), slot, last, pool, decode=(T == 1),
+                                     cu_seqlens=cu, seq_slot=seq_slot, logit_rows=last_rows)
+        width = T + n_new
+        out = torch.zeros((B, width), dtype=torch.int64, device=dev)
+        out[:, :T] = ids
+        use_pen = repetition_penalty is not None and repetition_penalty != 1.0 and repetition_penalty > 0
+        if use_pen:
+            hist = torch.zeros((B, width), dtype=torch.int32, device=dev)
+            hist[:, :T] = ids.to(torch.int32)
+            h_start = torch.arange(B, dtype=torch.int64, device=dev) * width
+            h_len = torch.empty(B, dtype=torch.int32, device=dev)
+        ban = None
+        if token_ban is not None and len(token_ban) > 0:
+            ban = torch.tensor([int(t) for t in token_ban], dtype=torch.int64, device=dev)
+        eos_t = torch.tensor(eos, dtype=torch.int64, device=dev) if eos else None
+        unfinished = torch.ones(B, dtype=torch.bool, device=dev)
+        buf = SamplerBuffers(B, dev)
+        buf.set_uniform(0.0 if greedy else float(temperature), float(top_p), int(top_k))
+        call_key = TokenSampler._next_key()
+        buf.rng_key.copy_(torch.arange(B, dtype=torch.int64, device=dev) + (call_key << 24))
+        if seed is None:
+            seed = TokenSampler._seed
+        row_slot = torch.arange(B, dtype=torch.int32, device=dev)
+        tok = torch.empty(B, dtype=torch.int64, device=dev)
+        lp = torch.empty(B, dtype=torch.float32, device=dev)
+        done = n_new
+        for step in range(n_new):
+            lg = logits
+            if use_pen:
+                lg = lg.float()
+                h_len.fill_(T + step)
+                repetition_penalty_(lg, float(repetition_penalty), hist.view(-1), h_start, h_len)
+            if ban is not None:
+                lg = lg.clone() if lg is logits else lg
+                lg[:, ban] = float("-inf")
+            buf.rng_ctr.fill_(step)
+            sample_rows(lg, buf, rule=RULE_MIXIN, max_valid_id=None, seed=seed, out_tok=tok, out_logp=lp)
+            out[:, T + step] = tok
+            if use_pen:
+                hist[:, T + step] = tok.to(torch.int32)
+            if eos_t is not None:
+                unfinished &= ~torch.isin(tok, eos_t)
+                if not bool(unfinished.any()):
+                    done = step + 1
+                    break
+            if step + 1 < n_new:
+                logits = self.forward_pooled(tok, row_slot, row_slot, pool, decode=True)
+        seqs = out[:, :T + done]
+        return {"sequences": seqs} if return_dict_in_generate else seqs
+
+
 def build_model(config: RWKV7Config, dtype=torch.bfloat16, device="cuda", seed: int = 0) -> RWKV7Model:
     """Allocate a model on ``device`` in ``dtype`` and apply the seeded dense init."""
     with torch.device("meta"):
@@ -712,4 +905,73 @@ def build_model(config: RWKV7Config, dtype=torch.bfloat16, device="cuda", seed: 
     m = m.to_empty(device=device)
     m = m.to(dtype)
     init_dense_(m, seed=seed, device=device)
+    return m
+
+
+# ---------------------------------------------------------------------------
+# The caller's own model
+# ---------------------------------------------------------------------------
+
+_HIP_MODELS: "weakref.WeakKeyDictionary[nn.Module, RWKV7Model]" = weakref.WeakKeyDictionary()
+
+
+def _config_of_params(params, src_config=None) -> RWKV7Config:
+    """Architecture of a module carrying the reference's parameter names, read
+    from the parameter shapes (``model.py:34-131, 281-302, 346-365, 421-433``)."""
+    try:
+        V, C = params["emb.weight"].shape
+        L = 1 + max(int(n.split(".")[1]) for n in params if n.startswith("blocks."))
+        dw = params["blocks.0.att.w1"].shape[1]
+        dg = params["blocks.0.att.g1"].shape[1]
+        dv = params["blocks.1.att.v1"].shape[1] if L > 1 else 0
+    except (KeyError, ValueError) as e:
+        raise ValueError(f"not an RWKV-7 module with the reference's parameter names ({e})") from None
+    ctx = int(getattr(src_config, "ctx_len", 1024)) if src_config is not None else 1024
+    return RWKV7Config(n_layer=L, n_embd=int(C), vocab_size=int(V), ctx_len=ctx, dim_att_lora=int(dw),
+                       dim_gate_lora=int(dg), dim_mv_lora=int(dv))
+
+
+def as_hip_model(module: nn.Module) -> RWKV7Model:
+    """An ``RWKV7Model`` running ``module``'s own parameters on the HIP library.
+
+    ``module`` is any ``nn.Module`` with the reference ``RWKV7Model``'s parameter
+    names (``emb.weight``, ``blocks.{i}.att.receptance.weight``, ...) - the
+    training model ``GRPOTrainer`` hands its rollout generator
+    (``rwkvtune/training/grpo/lightning_module.py:708-750``).  The returned model
+    registers the *same* ``Parameter`` objects (nothing is copied), so parameter
+    updates are seen; its packed copies are refreshed when a parameter's version
+    or storage changes.  One wrapper is kept per module.  An ``RWKV7Model`` is
+    returned unchanged.  A module with parameters the architecture does not have
+    (e.g. adapter weights not merged into the base weights) is rejected."""
+    if isinstance(module, RWKV7Model):
+        return module
+    hit = _HIP_MODELS.get(module)
+    if hit is not None:
+        return hit
+    params = dict(module.named_parameters())
+    cfg = _config_of_params(params, getattr(module, "config", None))
+    with torch.device("meta"):
+        m = RWKV7Model(cfg)
+    ours = dict(m.named_parameters())
+    extra = sorted(set(params) - set(ours))
+    missing = sorted(set(ours) - set(params))
+    if extra or missing:
+        raise ValueError(f"{type(module).__name__} does not carry the RWKV-7 parameter set: "
+                         f"missing {missing[:4]}, unexpected {extra[:4]}")
+    devs = {p.device for p in params.values()}
+    if len(devs) != 1:
+        raise ValueError(f"parameters on several devices: {sorted(map(str, devs))}")
+    for name, p in ours.items():
+        src = params[name]
+        if tuple(src.shape) != tuple(p.shape):
+            raise ValueError(f"{name}: shape {tuple(src.shape)}, expected {tuple(p.shape)}")
+        owner, _, leaf = name.rpartition(".")
+        m.get_submodule(owner)._parameters[leaf] = src
+    try:
+        src_block0 = module.get_submodule("blocks.0")
+    except AttributeError:
+        src_block0 = None
+    m.blocks[0].skip_ln0 = bool(getattr(src_block0, "skip_ln0", False))
+    m.train(module.training)
+    _HIP_MODELS[module] = m
     return m

@@ -29,6 +29,7 @@ from . import _lib
 
 RULE_BATCH = 0
 RULE_SINGLE = 1
+RULE_MIXIN = 2   # GenerationMixin.generate (generation_mixin.py:180-211)
 
 
 class SamplerBuffers:

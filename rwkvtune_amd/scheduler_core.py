@@ -35,6 +35,7 @@ import torch
 
 from ._common import dedupe, max_valid_token_id
 from .engine import RolloutEngine
+from .model import as_hip_model
 from .sampler import RULE_SINGLE, TokenSampler
 
 
@@ -86,6 +87,7 @@ class SchedulerCore:
         if state_cache is not None:
             raise NotImplementedError("the prefix state cache is not part of rwkvtune_amd")
         self.model = model
+        self._hip = as_hip_model(model)
         self.tokenizer = tokenizer
         self.device = next(model.parameters()).device
         self.dtype = next(model.parameters()).dtype
@@ -93,9 +95,9 @@ class SchedulerCore:
         self.max_batch_tokens = max_batch_tokens
         self.prefill_chunk_size = prefill_chunk_size
         self.state_cache = None
-        self.n_layer = model.config.n_layer
-        self.n_embd = model.config.n_embd
-        self.head_size = getattr(model.config, "head_size_a", 64)
+        self.n_layer = self._hip.config.n_layer
+        self.n_embd = self._hip.config.n_embd
+        self.head_size = 64
         self.n_head = self.n_embd // self.head_size
         self.sampler = TokenSampler
         mv = max_valid_token_id(tokenizer)
@@ -150,7 +152,7 @@ class SchedulerCore:
         per_step = collections.defaultdict(list)
         slots = max(1, min(self.max_batch_size, 1024))
         for (eos, bias), group in groups.items():
-            eng = RolloutEngine(self.model, min(slots, len(group)), eos_token_id=eos,
+            eng = RolloutEngine(self._hip, min(slots, len(group)), eos_token_id=eos,
                                 max_valid_id=TokenSampler._max_valid_token_id)
             uniq, index = dedupe([s.prompt_tokens for s in group])
             for s in group:

@@ -69,3 +69,30 @@ def cu_seqlens_of(lengths):
     for L in lengths:
         cu.append(cu[-1] + int(L))
     return cu
+
+
+MAX_VALID_ID = 65529  # last id of the reference vocabulary (rwkv_vocab_v20230424.txt)
+
+
+def geometric_caps(n: int, mean: float, cap: int, g: torch.Generator):
+    """``n`` stop lengths ~ Geometric(p = 1/mean) on {1, 2, ...}, clamped to ``cap``."""
+    u = torch.rand(n, generator=g, dtype=torch.float64)
+    caps = torch.clamp(torch.ceil(torch.log1p(-u) / torch.log1p(torch.tensor(-1.0 / mean))), 1, cap)
+    return [int(c) for c in caps]
+
+
+def cfg4_workload(seed: int = 4):
+    """GRPO rollout inputs of the 1.5B benchmark: 64 prompts of U(256, 2048) ids in
+    [1, 65529] and 64 x 8 per-path stop lengths ~ Geometric(mean 300) capped at 512."""
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(256, 2049, (64,), generator=g).tolist()
+    prompts = [torch.randint(1, MAX_VALID_ID + 1, (L,), generator=g).tolist() for L in lens]
+    return prompts, geometric_caps(64 * 8, 300.0, 512, g)
+
+
+def cfg5_workload(seed: int = 5, n: int = 128, prompt_len: int = 2048):
+    """7.2B rollout inputs: ``n`` prompts of ``prompt_len`` random ids and per-sequence
+    stop lengths ~ Geometric(mean 600) capped at 1024."""
+    g = torch.Generator().manual_seed(seed)
+    prompts = [torch.randint(1, MAX_VALID_ID + 1, (prompt_len,), generator=g).tolist() for _ in range(n)]
+    return prompts, geometric_caps(n, 600.0, 1024, g)

@@ -80,6 +80,9 @@ CASES = [
     (osm.RULE_SINGLE, 0.9, 0.6, 0),
     (osm.RULE_SINGLE, 1.0, 0.9, 8),
     (osm.RULE_SINGLE, 1.0, 1.0, 0),
+    (osm.RULE_MIXIN, 1.0, 0.9, 0),
+    (osm.RULE_MIXIN, 0.8, 0.7, 12),
+    (osm.RULE_MIXIN, 1.0, 0.0, 10),
 ]
 
 

@@ -75,3 +75,25 @@ def test_repetition_penalty_per_occurrence():
     x = torch.tensor([[2.0, -2.0, 1.0]])
     out = osm.repetition_penalty(x, [[0, 0, 1, 5]], 2.0)
     assert torch.allclose(out, torch.tensor([[0.5, -4.0, 1.0]], dtype=torch.float64))
+
+
+def test_generate_rule_top_k_then_nucleus_keeping_crossing():
+    """generation_mixin.py:188-211 by hand: probs 0.4, 0.3, 0.2, 0.1.
+    top_k = 3 -> 4/9, 3/9, 2/9; top_p = 0.5 keeps 4/9 (cum 4/9 <= .5) and the
+    crossing 3/9 -> 4/7, 3/7.  top_p = 0 (or 1) applies no nucleus at all; top_k
+    = 0 with top_p = 0.65 keeps .4, .3 (cum before .3 is .4 <= .65) and .2 (cum
+    before is .7 > .65 -> removed): 4/7, 3/7."""
+    x = torch.log(L(0.4, 0.3, 0.2, 0.1))
+    d = osm.distribution(x, top_k=3, top_p=0.5, rule=osm.RULE_MIXIN)
+    assert torch.allclose(d, L(4 / 7, 3 / 7, 0.0, 0.0))
+    for p in (0.0, 1.0):
+        d = osm.distribution(x, top_k=3, top_p=p, rule=osm.RULE_MIXIN)
+        assert torch.allclose(d, L(4 / 9, 3 / 9, 2 / 9, 0.0))
+    d = osm.distribution(x, top_k=0, top_p=0.65, rule=osm.RULE_MIXIN)
+    assert torch.allclose(d, L(4 / 7, 3 / 7, 0.0, 0.0))
+    # no filter: the softmax itself
+    assert torch.allclose(osm.distribution(x, rule=osm.RULE_MIXIN), L(0.4, 0.3, 0.2, 0.1))
+    # temperature 0.5 squares and renormalises the probabilities
+    d = osm.distribution(x, temperature=0.5, rule=osm.RULE_MIXIN)
+    q = L(0.16, 0.09, 0.04, 0.01)
+    assert torch.allclose(d, q / q.sum())
