@@ -234,6 +234,26 @@ int rwkv7_gemm_decode(int64_t M, int count, const void *const *A, const void *co
                       float *workspace, int64_t workspace_floats, void *stream);
 
 /*
+ * rwkv7_gemm_decode without a workspace argument and without any allocation:
+ * split-K partials go to the library's static scratch, a fixed array of
+ * RWKV7_GEMM_SCRATCH_FLOATS floats (8 MiB) that every GPU the library runs on
+ * holds until the process ends.  Problem sets needing more (see
+ * rwkv7_gemm_decode_workspace; every 1.5B / 7.2B decode projection set needs at
+ * most 1.6M floats) return RWKV7_ERR_INVALID.  The scratch needs no clearing
+ * (every range writes all its partials before they are read).  All calls on one
+ * GPU share its scratch, so calls that overlap on one GPU (concurrent streams,
+ * threads) race; calls in one stream's order do not.  The first call on a device
+ * looks up that device's scratch address once.
+ * No counterpart in the reference: this entry point is for callers that cannot
+ * allocate device memory - code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  Results equal rwkv7_gemm_decode's bit for bit.
+ */
+#define RWKV7_GEMM_SCRATCH_FLOATS (1 << 21)
+int rwkv7_gemm_decode_noalloc(int64_t M, int count, const void *const *A, const void *const *B,
+                              void *const *C, const int64_t *lda, const int64_t *ldc,
+                              const int *N, const int *K, const int *epi, void *stream);
+
+/*
  * One problem of rwkv7_gemm_decode (epi 0) without its reduction: the products
  * of the plan's P = rwkv7_gemm_decode_partial_count(M, N, K) K ranges are left in
  * `workspace` as float32 planes [P][M][N] (16-byte aligned, P * M * N floats),

@@ -51,6 +51,7 @@ SIGNATURES = {
     "rwkv7_admit_copy": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64] + [_P] * 6 + [_P]),
     "rwkv7_gemm_decode_workspace": (_I64, [_I64, _I32, _P, _P]),
     "rwkv7_gemm_decode": (_I32, [_I64, _I32] + [_P] * 8 + [_P, _I64, _P]),
+    "rwkv7_gemm_decode_noalloc": (_I32, [_I64, _I32] + [_P] * 8 + [_P]),
     "rwkv7_gemm_decode_partial_count": (_I32, [_I64, _I32, _I32]),
     "rwkv7_gemm_decode_partials": (_I32, [_I64, _P, _P, _I64, _I32, _I32, _P, _I64, _P, _P]),
     "rwkv7_gemm_packed_elems": (_I64, [_I32, _I32]),

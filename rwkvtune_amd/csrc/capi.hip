@@ -615,30 +615,68 @@ extern "C" int64_t rwkv7_gemm_decode_workspace(int64_t M, int count, const int* 
     return gemm_decode_workspace((int)(M > 0 ? M : 1), count, N, K);
 }
 
+namespace {
+// Argument checks shared by rwkv7_gemm_decode and rwkv7_gemm_decode_noalloc;
+// *need_ws receives the split-K floats the problem set needs.
+int check_gemm_decode(const char* fn, int64_t M, int count, const void* const* A, const void* const* B,
+                      void* const* C, const int64_t* lda, const int64_t* ldc, const int* N, const int* K,
+                      const int* epi, int64_t* need_ws) {
+    if (check_gemm_problems(fn, M, count, N, K) != RWKV7_OK) return RWKV7_ERR_INVALID;
+    *need_ws = 0;
+    if (M == 0) return RWKV7_OK;
+    if (!A || !B || !C || !lda || !ldc || !epi) return fail(RWKV7_ERR_INVALID, "%s: null array", fn);
+    int64_t blocks = 0;
+    for (int i = 0; i < count; ++i) {
+        if (!A[i] || !B[i] || !C[i]) return fail(RWKV7_ERR_INVALID, "%s: null pointer in problem %d", fn, i);
+        if (lda[i] < K[i] || ldc[i] < N[i] || (lda[i] % 8) != 0)
+            return fail(RWKV7_ERR_INVALID, "%s: problem %d: lda >= K and %% 8 == 0, ldc >= N required", fn, i);
+        if ((((uintptr_t)A[i]) | ((uintptr_t)B[i])) & 15)
+            return fail(RWKV7_ERR_INVALID, "%s: problem %d: A and packed B must be 16-byte aligned", fn, i);
+        if (epi[i] < 0 || epi[i] > 3) return fail(RWKV7_ERR_INVALID, "%s: problem %d: epi in 0..3", fn, i);
+        blocks += ((M + 31) / 32) * (int64_t)((N[i] + 63) / 64 + 7) * 8;
+    }
+    if (blocks > kMaxInt) return fail(RWKV7_ERR_INVALID, "%s: too many tiles", fn);
+    *need_ws = gemm_decode_workspace((int)M, count, N, K);
+    return RWKV7_OK;
+}
+}  // namespace
+
 extern "C" int rwkv7_gemm_decode(int64_t M, int count, const void* const* A, const void* const* B, void* const* C,
                                  const int64_t* lda, const int64_t* ldc, const int* N, const int* K, const int* epi,
                                  float* workspace, int64_t workspace_floats, void* stream) {
-    if (check_gemm_problems("rwkv7_gemm_decode", M, count, N, K) != RWKV7_OK) return RWKV7_ERR_INVALID;
+    int64_t need_ws = 0;
+    const int rc = check_gemm_decode("rwkv7_gemm_decode", M, count, A, B, C, lda, ldc, N, K, epi, &need_ws);
+    if (rc != RWKV7_OK) return rc;
     if (M == 0) return ok();
-    if (!A || !B || !C || !lda || !ldc || !epi) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: null array");
-    int64_t blocks = 0;
-    for (int i = 0; i < count; ++i) {
-        if (!A[i] || !B[i] || !C[i]) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: null pointer in problem %d", i);
-        if (lda[i] < K[i] || ldc[i] < N[i] || (lda[i] % 8) != 0)
-            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: lda >= K and %% 8 == 0, ldc >= N required", i);
-        if ((((uintptr_t)A[i]) | ((uintptr_t)B[i])) & 15)
-            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: A and packed B must be 16-byte aligned", i);
-        if (epi[i] < 0 || epi[i] > 3)
-            return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: problem %d: epi in 0..3", i);
-        blocks += ((M + 31) / 32) * (int64_t)((N[i] + 63) / 64 + 7) * 8;
-    }
-    if (blocks > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: too many tiles");
-    const int64_t need_ws = gemm_decode_workspace((int)M, count, N, K);
     if (need_ws > 0 && (workspace == nullptr || workspace_floats < need_ws))
         return fail(RWKV7_ERR_INVALID, "rwkv7_gemm_decode: needs a workspace of %lld floats (have %lld)",
                     (long long)need_ws, (long long)workspace_floats);
     return launch_status(launch_gemm_decode((int)M, count, A, B, C, lda, ldc, N, K, epi, workspace,
                                             (hipStream_t)stream),
+                         "gemm_decode_kernel");
+}
+
+hipError_t gemm_scratch(float** out);
+
+extern "C" int rwkv7_gemm_decode_noalloc(int64_t M, int count, const void* const* A, const void* const* B,
+                                         void* const* C, const int64_t* lda, const int64_t* ldc, const int* N,
+                                         const int* K, const int* epi, void* stream) {
+    int64_t need_ws = 0;
+    const int rc = check_gemm_decode("rwkv7_gemm_decode_noalloc", M, count, A, B, C, lda, ldc, N, K, epi, &need_ws);
+    if (rc != RWKV7_OK) return rc;
+    if (M == 0) return ok();
+    if (need_ws > RWKV7_GEMM_SCRATCH_FLOATS)
+        return fail(RWKV7_ERR_INVALID,
+                    "rwkv7_gemm_decode_noalloc: this problem set needs %lld floats of split-K scratch, more than "
+                    "the %lld of the library's static scratch; use rwkv7_gemm_decode with a workspace",
+                    (long long)need_ws, (long long)RWKV7_GEMM_SCRATCH_FLOATS);
+    float* ws = nullptr;
+    if (need_ws > 0) {
+        const hipError_t e = gemm_scratch(&ws);
+        if (e != hipSuccess)
+            return fail(RWKV7_ERR_LAUNCH, "rwkv7_gemm_decode_noalloc: scratch address: %s", hipGetErrorString(e));
+    }
+    return launch_status(launch_gemm_decode((int)M, count, A, B, C, lda, ldc, N, K, epi, ws, (hipStream_t)stream),
                          "gemm_decode_kernel");
 }
 

@@ -45,10 +45,45 @@
 //     launch_gemm_decode_partials, the consumer of the result does.
 // MFMA operand layout (gfx950): lane l supplies row l%32 of A and of B, k =
 // 8*(l/32) .. +7; accumulator q of lane l is C[8*(q/4) + 4*(l/32) + q%4][l%32].
+#include <mutex>
+
 #include "common.hpp"
+#include "rwkv7_hip.h"
 
 // source of the chunks past a K range
 __device__ __attribute__((aligned(16))) uint32_t g_gemm_zero_chunk[4];
+
+// Split-K partials of rwkv7_gemm_decode_noalloc: a fixed array in every GPU's
+// copy of the code object (RWKV7_GEMM_SCRATCH_FLOATS floats, held until the
+// process ends), used instead of a caller workspace.  Host code never passes
+// the array's name to a kernel: that is a host-side stand-in, not a device
+// address.  gemm_scratch() looks up each device's address once, with
+// hipGetSymbolAddress on that device, and every launch takes the looked-up pointer.
+static __device__ __align__(256) float scratch[RWKV7_GEMM_SCRATCH_FLOATS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+// Device address of the current device's scratch array (looked up on the first
+// call on that device).
+hipError_t gemm_scratch(float** out) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return hipSuccess;
+}
 
 namespace {
 
