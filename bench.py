@@ -37,12 +37,21 @@ prefill            chunked WKV7 prefill of cfg3 (64 ragged prompts ~U(64, 2048),
     in one launch; value = prompt tokens/s; roofline = bf16 MFMA rate executed
     (three part products per contraction) against the 2.5 PFLOP/s dense peak.
 
-Both workloads also time the dominant rollout kernel - the fused single-token
-time-mix (``tmix_decode_kernel``: WKV step + decay/LoRA element-wise + GroupNorm /
-bonus / gate) at the rollout's shape (256 slots, H=32) - with HIP events on its
-launch stream, rotating over 24 layer pools (3.2 GB) so no state is served from
-the 256 MB last-level cache; that is the ``roofline`` object.  ``wkv7_decode_cfg2``
-reports the stand-alone WKV kernel the same way (8 pools, 1.07 GB).
+The default line also carries:
+* ``roofline`` - the fused single-token time-mix (``tmix_decode_kernel``: WKV step +
+  decay/LoRA element-wise + GroupNorm / bonus / gate) at the rollout's shape (256
+  slots, H=32), timed with HIP events on its launch stream, rotating over 24 layer
+  pools (3.2 GB) so no state is served from the 256 MB last-level cache; its
+  ``traffic`` is derived from the committed PMC summary
+  ``profiles/tmix_decode_cfg4_shape_pmc.md``;
+* ``roofline_rollout`` - the whole rollout decode step: algorithmic bytes (every
+  decode weight once per step + each live row's state read and written) over the
+  measured decode time;
+* ``gemm_decode`` - the decode projections (five grouped packed-weight GEMM launches
+  per layer) at 256 rows over all 24 layers in turn: weight bytes / time;
+* ``wkv7_decode_cfg2`` / ``wkv7_prefill_cfg3`` - the stand-alone WKV kernels;
+* ``cfg5_rollout`` - one timed 7.2B rollout (the ``cfg5`` workload) after one warm-up
+  (``--no-cfg5`` skips it).
 
 The CPU baseline is the reference's CPU path restated in ``oracle/`` (float32,
 ``torch.set_num_threads(os.cpu_count())``) timed on a bounded sample of the same
@@ -101,13 +110,27 @@ def time_launches(fn, n_iter, stream):
     return e0.elapsed_time(e1) * 1e3 / n_iter  # us
 
 
-# HBM traffic of one tmix_decode launch at the leg's shape, from rocprofv3 --pmc runs of
-# `bench.py --workload tmix` (profiles/tmix_decode_rollout_shape_pmc.md): FETCH_SIZE and
-# WRITE_SIZE means in KiB per dispatch, each scaled by the same counter's reading for a
-# plain copy of known size in the same run (FETCH reads 0.5x, WRITE 1.0x of the true bytes)
-TMIX_PMC_FETCH_KIB, TMIX_PMC_WRITE_KIB = 70238.7, 132118.2
-PMC_FETCH_SCALE, PMC_WRITE_SCALE = 131072.0 / 65547.6, 131072.0 / 131072.0
-TMIX_TRAFFIC_BYTES = (TMIX_PMC_FETCH_KIB * PMC_FETCH_SCALE + TMIX_PMC_WRITE_KIB * PMC_WRITE_SCALE) * 1024
+def pmc_traffic(path=os.path.join(ROOT, "profiles", "tmix_decode_cfg4_shape_pmc.md")):
+    """HBM bytes per tmix_decode launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE and WRITE_SIZE in KiB per dispatch, each scaled by the same
+    counter's reading for a plain copy of known size in the same run), or None."""
+    import re
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    rows = {}
+    for line in text.splitlines():
+        m = re.match(r"\|\s*(.+?)\s*\|\s*([0-9.]+)\s*\|\s*([0-9.]+)\s*\|\s*$", line)
+        if m:
+            rows[m.group(1)] = (float(m.group(2)), float(m.group(3)))
+    copy = next((v for k, v in rows.items() if k.startswith("plain copy")), None)
+    kern = next((v for k, v in rows.items() if "tmix_decode_kernel" in k), None)
+    m = re.search(r"plain copy of ([0-9,]+) B", text)
+    if copy is None or kern is None or m is None:
+        return None
+    true_kib = int(m.group(1).replace(",", "")) / 1024.0
+    return (kern[0] * true_kib / copy[0] + kern[1] * true_kib / copy[1]) * 1024
 
 
 def copy_reference(dev, n_bytes=256 * 32 * 64 * 64 * 4, reps=8):
@@ -150,6 +173,57 @@ def tmix_decode_leg(dev, iters=480, S=256, H=32, L=24):
     return {"kernel": "tmix_decode_kernel<bf16> (fused WKV decode time-mix)", "slots": S, "H": H, "pools": L,
             "us_per_launch": us, "bytes_per_launch": units * TMIX_BYTES_PER_UNIT, "GBs": gbs,
             "frac": gbs / PEAK_HBM_GBS, "launches": iters}
+
+
+def gemm_decode_leg(model, dev, M=256, reps=10):
+    """The decode step's projections on the packed-weight grouped GEMM, exactly
+    as forward_pooled issues them (r/k/v + LoRA downs, LoRA ups, output
+    projection partials, FFN key with relu^2, FFN value partials), at M rows,
+    over all layers in turn (each layer's weights are cold when reached).
+    Algorithmic bytes = the packed weights' N x K x 2 per layer (activations are
+    small and L2-resident); HIP events on the launch stream."""
+    from rwkvtune_amd import _lib
+    from rwkvtune_amd.model import RWKV7Model
+    packs = model.packs()
+    C = model.config.n_embd
+    dt = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(9)
+    mixes = torch.randn((7, M, C), generator=g, device=dev).to(dt)
+    rkv = torch.empty((3, M, C), dtype=dt, device=dev)
+    o = torch.randn((M, C), generator=g, device=dev).to(dt)
+    xk = torch.randn((M, C), generator=g, device=dev).to(dt)
+    st = torch.cuda.current_stream(dev)
+    stream = _lib.stream_of(o)
+    bufs = {}
+
+    def layer(l):
+        pk = packs[l]
+        gp = pk.gp
+        nl, D = pk.lora_down.shape[0], pk.lora_down.shape[2]
+        if (nl, D) not in bufs:
+            bufs[(nl, D)] = (torch.zeros((nl, M, D), dtype=dt, device=dev), torch.empty((nl, M, C), dtype=dt, device=dev))
+        h, up = bufs[(nl, D)]
+        xr, xkk, xv, xw, xa, xg, _ = mixes.unbind(0)
+        dn = [("w1", 0, 2), ("a1", 1, 0), ("g1", 2, 3)] + ([] if l == 0 else [("v1", 3, 0)])
+        src = {"w1": xw, "a1": xa, "g1": xg, "v1": xv}
+        probs = [(xr, gp["r"], rkv[0], 0), (xkk, gp["k"], rkv[1], 0), (xv, gp["v"], rkv[2], 0)]
+        probs += [(src[n], gp[n], h[i, :, :gp[n].N], e) for n, i, e in dn]
+        RWKV7Model._gemm_group(M, probs, stream)
+        ups = [("w2", 0), ("a2", 1), ("g2", 2)] + ([] if l == 0 else [("v2", 3)])
+        RWKV7Model._gemm_group(M, [(h[i, :, :gp[n].K], gp[n], up[i], 0) for n, i in ups], stream)
+        RWKV7Model._gemm_partials(M, o, gp["o"], stream)
+        hk = bufs.setdefault("hk", torch.empty((M, gp["fk"].N), dtype=dt, device=dev))
+        RWKV7Model._gemm_group(M, [(xk, gp["fk"], hk, 1)], stream)
+        RWKV7Model._gemm_partials(M, hk, gp["fv"], stream)
+
+    L = len(packs)
+    for l in range(L):
+        layer(l)
+    us = time_launches(lambda i: layer(i % L), reps * L, st)
+    wbytes = sum(sum(w.N * w.K * 2 for w in pk.gp.values()) for pk in packs) / L
+    gbs = wbytes / (us * 1e-6) / 1e9
+    return {"kernel": "gemm_decode_kernel (5 grouped launches per layer)", "M": M, "us_per_layer": us,
+            "weight_bytes_per_layer": wbytes, "GBs": gbs, "frac": gbs / PEAK_HBM_GBS}
 
 
 def wkv_decode_leg(dev, iters=800, pools_n=8):
@@ -285,6 +359,28 @@ def rollout(steps, warmup, dev):
             f"(prefill {st['prefill_s']:.3f}s, decode {st['decode_s']:.3f}s, {st['decode_steps']} steps)")
     return model, prompts, caps, {"tokens": total_gen, "seconds": total_s, "value": total_gen / total_s,
                                   "ms_per_step": total_s / steps * 1e3, "runs": stats}
+
+
+def rollout_roofline(model, ro, n_paths):
+    """Algorithmic HBM bytes of the rollout's decode steps over their measured
+    time: every step reads each decode weight once (the packed projections and
+    the LM head), and every live row reads and writes its recurrent state (WKV
+    state 2 x L x H x 64 x 64 x 4 B, x_prev rows 4 x L x C x 4 B).  Live rows
+    summed over the steps = tokens made by decode steps = generated tokens minus
+    the first token of each path (drawn from the prefill logits)."""
+    cfg = model.config
+    packs = model.packs()
+    w_step = sum(sum(w.N * w.K * 2 for w in pk.gp.values()) for pk in packs)
+    w_step += cfg.vocab_size * cfg.n_embd * 2
+    row = 2 * cfg.n_layer * cfg.n_head * 64 * 64 * 4 + 4 * cfg.n_layer * cfg.n_embd * 4
+    run = ro["runs"][-1]
+    steps, dec_s = run["decode_steps"], run["decode_s"]
+    live_rows = run["generated_tokens"] - n_paths
+    total = steps * w_step + live_rows * row
+    gbs = total / dec_s / 1e9
+    return {"bound": "hbm", "achieved": gbs, "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": gbs / PEAK_HBM_GBS,
+            "ms_per_step": dec_s / steps * 1e3, "weight_bytes_per_step": w_step, "state_bytes_per_live_row": row,
+            "decode_steps": steps, "live_rows": live_rows, "bytes": total}
 
 
 def rollout_cfg5(steps, warmup, dev):
@@ -507,6 +603,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="rollout", choices=["rollout", "cfg5", "decode", "prefill", "tmix", "logprob", "train"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cfg5", action="store_true", help="skip the 7.2B rollout leg of the default workload")
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {a.gpus}): this build measures one GPU's "
@@ -533,11 +630,27 @@ def main():
         pf = prefill_leg(dev)
         log(f"[bench] wkv7 chunked prefill cfg3: {pf['us_per_launch']:.0f} us, {pf['mfma_bf16_TFLOPs']:.0f} "
             f"bf16 MFMA TFLOP/s, {pf['speedup_vs_token_serial']:.2f}x token-serial")
+        gm = gemm_decode_leg(model, dev)
+        log(f"[bench] decode GEMM (M=256): {gm['us_per_layer']:.1f} us/layer, {gm['GBs']:.0f} GB/s of weights")
+        rr = rollout_roofline(model, ro, n_paths=len(caps))
+        log(f"[bench] rollout decode step: {rr['ms_per_step']:.3f} ms, {rr['achieved']:.0f} GB/s algorithmic")
         cpu = None
         if not a.no_cpu_baseline:
             log("[bench] cpu baseline (restated reference rollout, bounded sample) ...")
             cpu = cpu_baseline_rollout(model, prompts)
             log(f"[bench] cpu: {cpu['sample']}")
+        c5 = None
+        if not a.no_cfg5:
+            del model
+            torch.cuda.empty_cache()
+            r5 = rollout_cfg5(1, 1, dev)
+            run5 = r5["runs"][-1]
+            c5 = {"tokens_per_s": r5["value"], "generated_tokens": r5["tokens"], "prompt_tokens": r5["prompt_tokens"],
+                  "decode_steps": run5["decode_steps"], "prefill_s": run5["prefill_s"], "decode_s": run5["decode_s"],
+                  "workload": "RWKV7-7.2B (L=32, C=4096, H=64) bf16, 128 prompts x 2048 tokens, chunk 256, "
+                              "temp 1.0, top_p 0.95, max 1024 new, geometric(600) stops, 128 slots; 1 timed rollout "
+                              "after 1 warm-up"}
+            log(f"[bench] cfg5: {r5['value']:.0f} tokens/s")
         out = {
             "metric": METRIC, "value": ro["value"], "unit": "tokens/s", "n_gpus": 1, "steps": steps,
             "warmup": warmup, "ms_per_step": ro["ms_per_step"], "higher_is_better": True, "scaling": "weak",
@@ -550,8 +663,11 @@ def main():
                        "decode_steps": ro["runs"][-1]["decode_steps"],
                        "prefill_s": ro["runs"][-1]["prefill_s"], "decode_s": ro["runs"][-1]["decode_s"]},
             "roofline": {"bound": "hbm", "achieved": tm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": tm["frac"], "traffic": TMIX_TRAFFIC_BYTES, "kernel": tm["kernel"],
+                         "frac": tm["frac"], "traffic": pmc_traffic(), "kernel": tm["kernel"],
                          "us_per_launch": tm["us_per_launch"], "algorithmic_bytes": tm["bytes_per_launch"]},
+            "roofline_rollout": rr,
+            "gemm_decode": {k: gm[k] for k in ("M", "us_per_layer", "weight_bytes_per_layer", "GBs", "frac")},
+            "cfg5_rollout": c5,
             "wkv7_decode_cfg2": {"GBs": wk["GBs"], "frac": wk["frac"], "us_per_step": wk["us_per_step"]},
             "wkv7_prefill_cfg3": {k: pf[k] for k in ("us_per_launch", "tokens_per_s", "mfma_bf16_TFLOPs",
                                                      "mfma_frac", "GBs", "hbm_frac", "speedup_vs_token_serial")},
@@ -638,7 +754,7 @@ def main():
             "config": {"workload": "fused decode time-mix (tmix_decode_kernel) at the cfg4 decode shape: 256 rows, "
                                    "H=32, 24 rotating layer pools", "copy_reference_bytes": ref},
             "roofline": {"bound": "hbm", "achieved": tm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": tm["frac"], "traffic": TMIX_TRAFFIC_BYTES, "kernel": tm["kernel"],
+                         "frac": tm["frac"], "traffic": pmc_traffic(), "kernel": tm["kernel"],
                          "us_per_launch": tm["us_per_launch"], "algorithmic_bytes": tm["bytes_per_launch"]},
             "cpu_baseline": None,
         }

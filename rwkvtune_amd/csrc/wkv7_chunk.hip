@@ -490,14 +490,17 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
     const int lane = tid & 63;
     const int wave = tid >> 6;
 
-    // Ragged batches run longest sequence first: block group r takes the r-th
-    // longest sequence (ties by index, so every sequence is taken once), and the
-    // longest chains of chunks start earliest instead of stretching the launch's
-    // tail.  The lengths are ranked from LDS (the X buffer, unused until phase C).
+    // Ragged batches of up to 256 sequences run longest sequence first: block
+    // group r takes the r-th longest sequence (ties by index, so every sequence
+    // is taken once), and the longest chains of chunks start earliest instead of
+    // stretching the launch's tail.  The lengths are ranked from LDS (the X
+    // buffer, unused until phase C): one length per thread against all nseq, so
+    // at most 256 LDS reads per thread.  Larger batches keep their order (the
+    // ranking would cost more than the tail it shortens).
     int s = unit / H;
     if (cu_seqlens != nullptr) {
         const int nseq = (int)(gridDim.x / (unsigned)H);
-        if (nseq <= NH * TP) {
+        if (nseq <= 256) {
             int* lens = reinterpret_cast<int*>(&sm.X[0][0]);
             for (int c = tid; c < nseq; c += 256) lens[c] = cu_seqlens[c + 1] - cu_seqlens[c];
             __syncthreads();

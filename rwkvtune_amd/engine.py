@@ -19,8 +19,10 @@ Used by the drop-in front ends (``GRPOBatchGenerator``, ``SchedulerCore``,
    length) and admits waiting ones into the freed slots by copying their
    prompt's state from the store (fork-on-admit: G generations of one prompt
    share one prefill).  The step is captured once in a HIP graph and replayed;
-   the host only polls the finished-sequence counter every few steps through an
-   asynchronous copy, so steps run back to back.
+   the host polls the finished-sequence counter every ``poll_every`` (2) steps
+   through an asynchronous copy and reads the copy made one period earlier, so
+   steps run back to back (2-4 steps stay queued) and at most 2 periods of
+   all-idle steps follow the last finished sequence.
 4. **Collect**: one copy of the token table back to the host.
 
 Every sequence's tokens depend only on its prompt state and its own
@@ -61,7 +63,7 @@ class RolloutEngine:
     """Slot-pool rollout on one GPU for a ``RWKV7Model``."""
 
     def __init__(self, model: RWKV7Model, n_slots: int, *, eos_token_id: Optional[int] = None,
-                 max_valid_id: Optional[int] = None, use_graph: bool = True, poll_every: int = 8):
+                 max_valid_id: Optional[int] = None, use_graph: bool = True, poll_every: int = 2):
         if n_slots < 1 or n_slots > 1024:
             raise ValueError("n_slots must be in [1, 1024]")
         self.model = model

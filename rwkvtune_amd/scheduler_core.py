@@ -6,22 +6,30 @@ max_batch_size, max_batch_tokens, prefill_chunk_size, state_cache)`` with
 step_sync / run_to_completion_sync / step_async`` (``:111-782``) and
 ``create_scheduler_core`` (``:789-815``).
 
-Semantics kept: every sequence is prefilled in chunks of ``prefill_chunk_size``
-tokens under a ``max_batch_tokens`` budget per forward, its first token comes
-from the prefill logits and every token uses ``TokenSampler.sample`` rules with
-the sequence's own temperature / top_p / top_k / logit_bias; a sequence finishes
-on ``eos_token_id`` or after ``max_new_tokens`` tokens (the first token included,
-``:90-108``), freeing its slot for the next waiting sequence; at most
-``max_batch_size`` sequences decode together.
+One ``step_sync`` is one step of the reference's loop (``:250-299, 445-600,
+606-664``):
 
-Execution differs: the waiting sequences of a call run as one device-resident
-rollout (``rwkvtune_amd.engine``), so the per-step token lists that
-``step_sync`` / ``run_to_completion_sync`` hand out are recorded on the GPU and
-returned after it finishes rather than with a host round trip per step and per
-sequence.  Sequences added while results are being handed out run in the next
-call.  Identical prompts are prefilled once.  Stop strings, JSON-schema
-enforcers and the prefix state cache are not supported (``stop`` is accepted and
-ignored, ``enforcer`` / ``state_cache`` raise).
+1. admit waiting sequences into free slots (status PREFILLING) and zero those
+   slots' state;
+2. decode one token for every running sequence - one pooled single-token forward
+   over their slots (rows addressed through the slot table, no gather / scatter
+   of states) and one device sampler launch with each sequence's own
+   temperature / top_p / top_k / logit_bias (``TokenSampler.sample`` rules);
+3. prefill the next chunk (at most ``prefill_chunk_size`` tokens) of prefilling
+   sequences under the ``max_batch_tokens`` budget, all chunks in one ragged
+   forward (no grouping by length); a sequence whose prompt is complete draws its
+   first token from the prefill logits and runs from the next step on;
+4. a sequence finishes on ``eos_token_id`` or after ``max_new_tokens`` tokens
+   (the first included, ``:90-108``) and frees its slot for the next admission.
+
+The step returns its new ``(seq_id, token_id)`` pairs; sequences added between
+steps are admitted as slots free up.  The slot pool (``max_batch_size`` slots,
+float32 state) is allocated once, so memory does not grow with the queue.  The
+step's one host synchronisation is the copy of the sampled ids.  Random draws
+are keyed by (sequence, position), so a sequence's tokens do not depend on what
+else is batched with it.  Stop strings, JSON-schema enforcers and the prefix
+state cache are not supported (``stop`` is accepted and ignored, ``enforcer`` /
+``state_cache`` raise).
 """
 
 from __future__ import annotations
@@ -33,10 +41,9 @@ from typing import Any, Dict, Iterator, List, Optional, Tuple, Union
 
 import torch
 
-from ._common import dedupe, max_valid_token_id
-from .engine import RolloutEngine
-from .model import as_hip_model
-from .sampler import RULE_SINGLE, TokenSampler
+from ._common import max_valid_token_id
+from .model import StatePool, as_hip_model
+from .sampler import RULE_SINGLE, SamplerBuffers, TokenSampler, sample_rows
 
 
 class SeqStatus(Enum):
@@ -86,6 +93,8 @@ class SchedulerCore:
                  prefill_chunk_size: int = 512, state_cache=None):
         if state_cache is not None:
             raise NotImplementedError("the prefix state cache is not part of rwkvtune_amd")
+        if max_batch_size < 1 or max_batch_size > 1024:
+            raise ValueError("max_batch_size must be in [1, 1024]")
         self.model = model
         self._hip = as_hip_model(model)
         self.tokenizer = tokenizer
@@ -103,19 +112,22 @@ class SchedulerCore:
         mv = max_valid_token_id(tokenizer)
         if mv is not None:
             TokenSampler._max_valid_token_id = mv
-        self._engine: Optional[RolloutEngine] = None
-        self._calls = 0
+        # the slot pool: fixed size, whatever the queue length
+        self.state_pool = StatePool(self._hip.config, max_batch_size, self.device)
+        self._seed = TokenSampler._seed * 7919 + TokenSampler._next_key()
+        self._keys = 0
+        self._step_counter = 0
         self.reset()
 
     # -- queues ----------------------------------------------------------------
 
     def reset(self) -> None:
+        """Clear the queues and free every slot (the state pool is kept)."""
         self.waiting_queue: collections.deque = collections.deque()
         self.prefilling_seqs: List[SequenceState] = []
         self.running_seqs: List[SequenceState] = []
         self.slots: List[Optional[SequenceState]] = [None] * self.max_batch_size
         self.free_slots = collections.deque(range(self.max_batch_size))
-        self._pending_steps: collections.deque = collections.deque()
 
     def add_sequences(self, sequences: List[SequenceState]) -> None:
         for s in sequences:
@@ -124,85 +136,155 @@ class SchedulerCore:
     def add_sequence(self, seq: SequenceState) -> None:
         if seq.enforcer is not None:
             raise NotImplementedError("JSON-schema enforcers are not supported")
+        if len(seq.prompt_tokens) == 0:
+            raise ValueError(f"sequence {seq.seq_id} has an empty prompt")
+        seq._rng_key = self._keys  # random stream of this sequence
+        self._keys += 1
         self.waiting_queue.append(seq)
 
     def has_pending_work(self) -> bool:
-        return bool(self.waiting_queue or self.running_seqs or self._pending_steps)
+        return bool(self.waiting_queue or self.prefilling_seqs or self.running_seqs)
 
     def get_stats(self) -> Dict[str, int]:
         return {"waiting": len(self.waiting_queue), "prefilling": len(self.prefilling_seqs),
                 "running": len(self.running_seqs), "free_slots": len(self.free_slots)}
 
+    # -- scheduling (scheduler_core.py:250-299) ---------------------------------
+
+    def _schedule(self):
+        admitted = []
+        while self.waiting_queue and self.free_slots:
+            seq = self.waiting_queue.popleft()
+            slot = self.free_slots.popleft()
+            seq.slot_id = slot
+            seq.status = SeqStatus.PREFILLING
+            self.slots[slot] = seq
+            self.prefilling_seqs.append(seq)
+            admitted.append(slot)
+        if admitted:
+            self.state_pool.zero_(torch.tensor(admitted, dtype=torch.long, device=self.device))
+        decode_batch = list(self.running_seqs)[:self.max_batch_size]
+        prefill_batch = []
+        budget = self.max_batch_tokens
+        for seq in list(self.prefilling_seqs):
+            if budget <= 0:
+                break
+            n = min(len(seq.prompt_tokens) - seq.prefill_offset, self.prefill_chunk_size, budget)
+            if n > 0:
+                prefill_batch.append((seq, seq.prompt_tokens[seq.prefill_offset:seq.prefill_offset + n]))
+                budget -= n
+        return decode_batch, prefill_batch
+
+    def _finish_sequence(self, seq: SequenceState) -> None:
+        seq.status = SeqStatus.FINISHED
+        if seq in self.running_seqs:
+            self.running_seqs.remove(seq)
+        if seq in self.prefilling_seqs:
+            self.prefilling_seqs.remove(seq)
+        self.slots[seq.slot_id] = None
+        self.free_slots.append(seq.slot_id)
+
     # -- execution --------------------------------------------------------------
 
-    def _run_waiting(self) -> None:
-        """Roll out every waiting sequence on the device and queue the per-step
-        token lists they produced."""
-        seqs = list(self.waiting_queue)
-        self.waiting_queue.clear()
-        if not seqs:
-            return
-        # one device rollout per distinct (eos, logit_bias): both are per-run settings
-        groups = collections.OrderedDict()
-        for s in seqs:
-            if len(s.prompt_tokens) == 0:
-                raise ValueError(f"sequence {s.seq_id} has an empty prompt")
-            key = (s.eos_token_id, tuple(sorted((int(k), float(v)) for k, v in (s.logit_bias or {}).items())))
-            groups.setdefault(key, []).append(s)
-        per_step = collections.defaultdict(list)
-        slots = max(1, min(self.max_batch_size, 1024))
-        for (eos, bias), group in groups.items():
-            eng = RolloutEngine(self._hip, min(slots, len(group)), eos_token_id=eos,
-                                max_valid_id=TokenSampler._max_valid_token_id)
-            uniq, index = dedupe([s.prompt_tokens for s in group])
-            for s in group:
-                s.status = SeqStatus.RUNNING
-            self.running_seqs.extend(group)
-            res = eng.run(uniq, index, [s.max_new_tokens for s in group],
-                          logit_bias=dict(bias) if bias else None, first_rule=RULE_SINGLE,
-                          decode_rule=RULE_SINGLE, first_can_finish=True, chunk_size=self.prefill_chunk_size,
-                          max_batch_tokens=self.max_batch_tokens,
-                          per_seq_sampling=([s.temperature for s in group], [s.top_p for s in group],
-                                            [s.top_k for s in group]),
-                          seed=TokenSampler._seed * 7919 + self._calls)
-            self._calls += 1
-            for s, toks, lps, steps in zip(group, res.tokens, res.logps, res.steps):
-                for t, lp, st in zip(toks, lps, steps):
-                    per_step[st].append((s, t, lp))
-        for st in sorted(per_step):
-            self._pending_steps.append(per_step[st])
+    def _i32(self, x):
+        return torch.tensor(x, dtype=torch.int32).to(self.device, non_blocking=True)
+
+    def _sample(self, logits: torch.Tensor, seqs: List[SequenceState]) -> List[Tuple[int, float]]:
+        """One token per row with each sequence's own sampling settings
+        (``TokenSampler.sample`` rules, ``scheduler_core.py:470-476, 563-569``)."""
+        n = len(seqs)
+        dev = self.device
+        buf = SamplerBuffers(n, dev)
+        buf.temperature.copy_(torch.tensor([float(s.temperature) for s in seqs], dtype=torch.float32))
+        buf.top_p.copy_(torch.tensor([float(s.top_p) for s in seqs], dtype=torch.float32))
+        buf.top_k.copy_(torch.tensor([int(s.top_k) for s in seqs], dtype=torch.int32))
+        buf.rng_key.copy_(torch.tensor([s._rng_key for s in seqs], dtype=torch.int64))
+        buf.rng_ctr.copy_(torch.tensor([len(s.generated_tokens) for s in seqs], dtype=torch.int32))
+        if any(s.logit_bias for s in seqs):
+            off, ids, vals = [0], [], []
+            for s in seqs:
+                for k, v in (s.logit_bias or {}).items():
+                    ids.append(int(k))
+                    vals.append(float(v))
+                off.append(len(ids))
+            buf.bias_off = self._i32(off)
+            buf.bias_ids = self._i32(ids)
+            buf.bias_val = torch.tensor(vals, dtype=torch.float32).to(dev)
+        tok = torch.empty(n, dtype=torch.int64, device=dev)
+        lp = torch.empty(n, dtype=torch.float32, device=dev)
+        sample_rows(logits, buf, rule=RULE_SINGLE, max_valid_id=TokenSampler._max_valid_token_id,
+                    seed=self._seed, out_tok=tok, out_logp=lp)
+        return list(zip(tok.tolist(), lp.tolist()))
+
+    def _append(self, seq: SequenceState, tok: int, lp: float, out: list) -> None:
+        seq.last_token_id = tok
+        seq.generated_tokens.append(tok)
+        seq.generated_logps.append(lp)
+        out.append((seq.seq_id, tok))
+        if seq.is_finished:
+            self._finish_sequence(seq)
+
+    def _execute_decode(self, batch: List[SequenceState]) -> List[Tuple[Union[int, str], int]]:
+        if not batch:
+            return []
+        R = len(batch)
+        tokens = torch.tensor([s.last_token_id for s in batch], dtype=torch.int64).to(self.device)
+        rows = torch.arange(R, dtype=torch.int32, device=self.device)
+        logits = self._hip.forward_pooled(tokens, self._i32([s.slot_id for s in batch]), rows, self.state_pool,
+                                          decode=True)
+        out = []
+        for seq, (t, lp) in zip(batch, self._sample(logits, batch)):
+            self._append(seq, t, lp, out)
+        return out
+
+    def _execute_prefill(self, batch) -> List[Tuple[Union[int, str], int]]:
+        if not batch:
+            return []
+        toks, row_slot, row_last, cu, seq_slot, last_rows, done = [], [], [], [0], [], [], []
+        for seq, chunk in batch:
+            base = cu[-1]
+            n = len(chunk)
+            toks.extend(chunk)
+            row_slot.extend([seq.slot_id] * n)
+            row_last.extend([base + n - 1] + [-1] * (n - 1))
+            cu.append(base + n)
+            seq_slot.append(seq.slot_id)
+            if seq.prefill_offset + n >= len(seq.prompt_tokens):
+                last_rows.append(base + n - 1)
+                done.append(seq)
+        tokens = torch.tensor(toks, dtype=torch.int64).to(self.device)
+        logits = self._hip.forward_pooled(tokens, self._i32(row_slot), self._i32(row_last), self.state_pool,
+                                          decode=False, cu_seqlens=self._i32(cu), seq_slot=self._i32(seq_slot),
+                                          logit_rows=self._i32(last_rows), n_logit_rows=len(last_rows))
+        for seq, chunk in batch:
+            seq.prefill_offset += len(chunk)
+        out = []
+        if done:
+            picks = self._sample(logits, done)
+            for seq, (t, lp) in zip(done, picks):
+                seq.status = SeqStatus.RUNNING
+                self.prefilling_seqs.remove(seq)
+                self.running_seqs.append(seq)
+                self._append(seq, t, lp, out)
+        return out
 
     def step_sync(self) -> List[Tuple[Union[int, str], int]]:
-        """New tokens of the next step: ``[(seq_id, token_id), ...]``."""
+        """One scheduling step: admit, decode the running sequences, prefill the
+        next chunks; returns the step's new ``(seq_id, token_id)`` pairs."""
         with torch.no_grad():
-            if not self._pending_steps and self.waiting_queue:
-                self._run_waiting()
-            if not self._pending_steps:
+            decode_batch, prefill_batch = self._schedule()
+            if not decode_batch and not prefill_batch:
                 return []
-            out = []
-            for s, t, lp in self._pending_steps.popleft():
-                s.last_token_id = t
-                s.generated_tokens.append(t)
-                s.generated_logps.append(lp)
-                s.prefill_offset = len(s.prompt_tokens)
-                out.append((s.seq_id, t))
-                if s.is_finished:
-                    s.status = SeqStatus.FINISHED
-                    if s in self.running_seqs:
-                        self.running_seqs.remove(s)
-            return out
+            new_tokens = self._execute_decode(decode_batch)
+            new_tokens.extend(self._execute_prefill(prefill_batch))
+            self._step_counter += 1
+            return new_tokens
 
     def run_to_completion_sync(self) -> Iterator[List[Tuple[Union[int, str], int]]]:
         while self.has_pending_work():
             new = self.step_sync()
             if new:
                 yield new
-            elif not self._pending_steps and not self.waiting_queue:
-                # nothing left to hand out: sequences still marked running ended
-                # without a terminating token (cannot happen with a finite cap)
-                for s in list(self.running_seqs):
-                    s.status = SeqStatus.FINISHED
-                self.running_seqs.clear()
 
     async def step_async(self):
         return self.step_sync()
