@@ -334,11 +334,17 @@ int rwkv7_repetition_penalty(int64_t M, int64_t V, float *logits, int64_t ld, fl
  *                         (int32 / float32 / int32: token, its sampling
  *                         log-probability, the decode step that made it)
  *   slot_seq[S] int32     sequence in the slot, -1 = free
- *   row_slot[S] int32     slot index or -1: the row_slot of the model kernels
- *   tok_in[S] int64       next input token of the slot
- *   counters[4] int32     next waiting sequence, finished sequences, decode
- *                         steps committed, admissions of the current step
+ *   row_slot[S] int32     slot of row r or -1: the row_slot of the model kernels
+ *   tok_in[S] int64       next input token of row r
+ *   slot_row[S] int32     (optional, compaction) row of slot s, -1 = free
+ *   counters[5] int32     next waiting sequence, finished sequences, decode
+ *                         steps committed, admissions of the current step, live
+ *                         rows (with compaction)
  *   admit_slot / admit_src [S] int32: this step's admissions (slot <- store entry)
+ * Rows are what a decode step computes; slots hold the state.  Without
+ * compaction row r is slot r.  With it, the live slots take rows 0 .. live-1 in
+ * slot order and rows past them are -1, so a step may run only a leading bucket
+ * of rows that covers the live ones.
  * ------------------------------------------------------------------------ */
 
 /* Record each sequence's first token (sampled from its prompt's last logits):
@@ -350,23 +356,29 @@ int rwkv7_rollout_first(int64_t n, int64_t maxlen, const int64_t *tok, const flo
                         int32_t *out_tok, float *out_logp, int32_t *out_step, int64_t eos,
                         int first_can_finish, int32_t *counters, void *stream);
 
-/* One block: with have_sample, append tok[s] / logp[s] to the sequence in slot
- * s, finish it on EOS or its cap; then every free slot takes the next waiting,
- * unfinished sequence (index order) and lists the state copy it needs.  S <= 1024. */
+/* One block: with have_sample, append tok[r] / logp[r] of the row r the slot
+ * ran in to the sequence in slot s, finish it on EOS or its cap; then every free
+ * slot takes the next waiting, unfinished sequence (index order) and lists the
+ * state copy it needs; finally the row table is rebuilt (compacted when slot_row
+ * is non-NULL; slot_row must then start as all -1 with every slot free).
+ * S <= 1024. */
 int rwkv7_rollout_commit(int64_t S, int64_t n, int64_t maxlen, int have_sample, const int64_t *tok,
-                         const float *logp, int32_t *slot_seq, int32_t *row_slot, int64_t *tok_in,
+                         const float *logp, int32_t *slot_seq, int32_t *row_slot, int32_t *slot_row,
+                         int64_t *tok_in,
                          const int32_t *seq_prompt, const int32_t *seq_max_new, int32_t *seq_ngen,
                          uint8_t *seq_done, int32_t *out_tok, float *out_logp, int32_t *out_step,
                          int64_t eos, int32_t *counters, int32_t *admit_slot, int32_t *admit_src,
                          void *stream);
 
-/* Per-slot sampler inputs of the step: active[s], rng_key[s] = sequence,
- * rng_ctr[s] = its position; optionally (hist_start non-NULL) the two history
- * segments of the repetition penalty (prompt ids in a packed prompt array at
- * prompt_start[p] / prompt_len[p]; generated ids in out_tok), and optionally
- * (seq_temp non-NULL) per-sequence temperature / top_p / top_k copied to the
- * slot's row. */
-int rwkv7_rollout_prepare(int64_t S, int64_t maxlen, const int32_t *slot_seq, const int32_t *seq_ngen,
+/* Per-row sampler inputs of the step for rows 0 .. S-1 (row r holds slot
+ * row_slot[r]; row_slot NULL: row r is slot r): active[r], rng_key[r] =
+ * seq_key[q] of the row's sequence q (seq_key NULL: q), rng_ctr[r] = its
+ * position; optionally (hist_start non-NULL) the two history segments of the
+ * repetition penalty (prompt ids in a packed prompt array at prompt_start[p] /
+ * prompt_len[p]; generated ids in out_tok), and optionally (seq_temp non-NULL)
+ * per-sequence temperature / top_p / top_k copied to the row. */
+int rwkv7_rollout_prepare(int64_t S, int64_t maxlen, const int32_t *row_slot, const int32_t *slot_seq,
+                          const int64_t *seq_key, const int32_t *seq_ngen,
                           const int32_t *seq_prompt, const int64_t *prompt_start,
                           const int32_t *prompt_len, uint8_t *active, int64_t *rng_key,
                           int32_t *rng_ctr, int64_t *hist_start, int32_t *hist_len,

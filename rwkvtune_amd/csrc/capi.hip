@@ -105,7 +105,7 @@ bool misaligned(int dtype, const void* state, const void* r, const void* w, cons
 
 }  // namespace
 
-extern "C" int rwkv7_abi_version(void) { return 1; }
+extern "C" int rwkv7_abi_version(void) { return 2; }
 
 extern "C" const char* rwkv7_last_error(void) { return g_err; }
 
@@ -427,11 +427,13 @@ hipError_t launch_rollout_first(int n, int maxlen, const int64_t* tok, const flo
                                 int32_t* out_step, int64_t eos, int first_can_finish, int32_t* counters,
                                 hipStream_t st);
 hipError_t launch_rollout_commit(int S, int n, int maxlen, int have_sample, const int64_t* tok, const float* logp,
-                                 int32_t* slot_seq, int32_t* row_slot, int64_t* tok_in, const int32_t* seq_prompt,
+                                 int32_t* slot_seq, int32_t* row_slot, int32_t* slot_row, int64_t* tok_in,
+                                 const int32_t* seq_prompt,
                                  const int32_t* seq_max_new, int32_t* seq_ngen, uint8_t* seq_done,
                                  int32_t* out_tok, float* out_logp, int32_t* out_step, int64_t eos,
                                  int32_t* counters, int32_t* admit_slot, int32_t* admit_src, hipStream_t st);
-hipError_t launch_rollout_prepare(int S, int maxlen, const int32_t* slot_seq, const int32_t* seq_ngen,
+hipError_t launch_rollout_prepare(int S, int maxlen, const int32_t* row_slot, const int32_t* slot_seq,
+                                  const int64_t* seq_key, const int32_t* seq_ngen,
                                   const int32_t* seq_prompt, const int64_t* prompt_start,
                                   const int32_t* prompt_len, uint8_t* active, int64_t* rng_key,
                                   int32_t* rng_ctr, int64_t* hist_start, int32_t* hist_len,
@@ -458,7 +460,8 @@ extern "C" int rwkv7_rollout_first(int64_t n, int64_t maxlen, const int64_t* tok
 }
 
 extern "C" int rwkv7_rollout_commit(int64_t S, int64_t n, int64_t maxlen, int have_sample, const int64_t* tok,
-                                    const float* logp, int32_t* slot_seq, int32_t* row_slot, int64_t* tok_in,
+                                    const float* logp, int32_t* slot_seq, int32_t* row_slot, int32_t* slot_row,
+                                    int64_t* tok_in,
                                     const int32_t* seq_prompt, const int32_t* seq_max_new, int32_t* seq_ngen,
                                     uint8_t* seq_done, int32_t* out_tok, float* out_logp, int32_t* out_step,
                                     int64_t eos, int32_t* counters, int32_t* admit_slot, int32_t* admit_src,
@@ -470,13 +473,14 @@ extern "C" int rwkv7_rollout_commit(int64_t S, int64_t n, int64_t maxlen, int ha
         !out_logp || !counters || !admit_slot || !admit_src)
         return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_commit: null pointer");
     return launch_status(launch_rollout_commit((int)S, (int)n, (int)maxlen, have_sample, tok, logp, slot_seq, row_slot,
-                                               tok_in, seq_prompt, seq_max_new, seq_ngen, seq_done, out_tok,
+                                               slot_row, tok_in, seq_prompt, seq_max_new, seq_ngen, seq_done, out_tok,
                                                out_logp, out_step, eos, counters, admit_slot, admit_src,
                                                (hipStream_t)stream),
                          "rollout_commit_kernel");
 }
 
-extern "C" int rwkv7_rollout_prepare(int64_t S, int64_t maxlen, const int32_t* slot_seq, const int32_t* seq_ngen,
+extern "C" int rwkv7_rollout_prepare(int64_t S, int64_t maxlen, const int32_t* row_slot, const int32_t* slot_seq,
+                                     const int64_t* seq_key, const int32_t* seq_ngen,
                                      const int32_t* seq_prompt, const int64_t* prompt_start,
                                      const int32_t* prompt_len, uint8_t* active, int64_t* rng_key,
                                      int32_t* rng_ctr, int64_t* hist_start, int32_t* hist_len,
@@ -491,7 +495,8 @@ extern "C" int rwkv7_rollout_prepare(int64_t S, int64_t maxlen, const int32_t* s
         return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_prepare: history outputs need the prompt table");
     if (seq_temp && (!seq_top_p || !seq_top_k || !temp || !top_p || !top_k))
         return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_prepare: per-sequence parameters come as a set");
-    return launch_status(launch_rollout_prepare((int)S, (int)maxlen, slot_seq, seq_ngen, seq_prompt, prompt_start,
+    return launch_status(launch_rollout_prepare((int)S, (int)maxlen, row_slot, slot_seq, seq_key, seq_ngen, seq_prompt,
+                                                prompt_start,
                                                 prompt_len, active, rng_key, rng_ctr, hist_start, hist_len,
                                                 hist2_start, hist2_len, seq_temp, seq_top_p, seq_top_k, temp,
                                                 top_p, top_k, (hipStream_t)stream),

@@ -11,20 +11,27 @@
 //   sequence table  seq_prompt[n] (index of the prefilled prompt state),
 //                   seq_max_new[n], seq_ngen[n], seq_done[n],
 //                   out_tok / out_logp / out_step [n, maxlen]
-//   slot table      slot_seq[S] (-1 = free), row_slot[S] (slot or -1, what the
-//                   model kernels read), tok_in[S] (next input token)
+//   slot table      slot_seq[S] (-1 = free)
+//   row table       row_slot[S] (slot of row r, or -1: what the model kernels
+//                   read), tok_in[S] (next input token of row r), and with
+//                   compaction slot_row[S] (row of slot s, -1 = free)
 //   counters        [0] next waiting sequence, [1] finished sequences,
-//                   [2] decode steps committed, [3] admissions of this step
+//                   [2] decode steps committed, [3] admissions of this step,
+//                   [4] live rows (with compaction)
 //   admit list      admit_slot[S], admit_src[S] for the state copy
+//
+// Compaction: the live slots occupy rows 0 .. live-1 (in slot order), so a step
+// can run only its first rows (a multiple of a row bucket >= live) and skip the
+// dead tail.  Without it (slot_row == NULL) row r is slot r.
 //
 // Admission takes waiting sequences in index order (sequences finished at their
 // first token are skipped); a sequence's tokens depend only on its own state and
-// its (sequence, position) random stream, never on which slot it runs in.
+// its (sequence, position) random stream, never on which slot or row it runs in.
 #include "common.hpp"
 
 namespace {
 
-enum { C_NEXT = 0, C_DONE = 1, C_STEP = 2, C_NADMIT = 3 };
+enum { C_NEXT = 0, C_DONE = 1, C_STEP = 2, C_NADMIT = 3, C_LIVE = 4 };
 
 // First generated token of every sequence (sampled from its prompt's logits).
 __global__ void rollout_first_kernel(int n, int maxlen, const int64_t* __restrict__ tok,
@@ -47,28 +54,34 @@ __global__ void rollout_first_kernel(int n, int maxlen, const int64_t* __restric
 }
 
 // One block of >= S threads.  Commits the step's sampled tokens (have_sample),
-// retires finished sequences and admits waiting ones into free slots.
+// retires finished sequences and admits waiting ones into free slots; then
+// (slot_row non-null) ranks the live slots into rows 0 .. live-1.
 __global__ __launch_bounds__(1024) void rollout_commit_kernel(
     int S, int n, int maxlen, int have_sample, const int64_t* __restrict__ tok,
     const float* __restrict__ logp, int32_t* __restrict__ slot_seq, int32_t* __restrict__ row_slot,
-    int64_t* __restrict__ tok_in, const int32_t* __restrict__ seq_prompt,
+    int32_t* __restrict__ slot_row, int64_t* __restrict__ tok_in, const int32_t* __restrict__ seq_prompt,
     const int32_t* __restrict__ seq_max_new, int32_t* __restrict__ seq_ngen, uint8_t* __restrict__ seq_done,
     int32_t* __restrict__ out_tok, float* __restrict__ out_logp, int32_t* __restrict__ out_step, int64_t eos,
     int32_t* __restrict__ counters, int32_t* __restrict__ admit_slot, int32_t* __restrict__ admit_src)
 {
+    __shared__ int wave_live[16];
     const int s = threadIdx.x;
+    const bool compact = slot_row != nullptr;
     if (s == 0) atomicExch(&counters[C_NADMIT], 0);
     __syncthreads();
     const int step = counters[C_STEP];
+    int64_t next_tok = 0;  // the slot's next input token
     if (s < S) {
         const int q = slot_seq[s];
+        const int row = compact ? slot_row[s] : s;  // the row this slot ran in
         bool admit = q < 0;
-        if (q >= 0 && have_sample) {
-            const int64_t t = tok[s];
+        if (q >= 0) next_tok = (row >= 0) ? tok_in[row] : 0;
+        if (q >= 0 && have_sample && row >= 0) {
+            const int64_t t = tok[row];
             const int pos = seq_ngen[q];
             if (pos < maxlen) {
                 out_tok[(size_t)q * maxlen + pos] = (int32_t)t;
-                out_logp[(size_t)q * maxlen + pos] = logp[s];
+                out_logp[(size_t)q * maxlen + pos] = logp[row];
                 if (out_step != nullptr) out_step[(size_t)q * maxlen + pos] = step + 1;
             }
             seq_ngen[q] = pos + 1;
@@ -78,7 +91,7 @@ __global__ __launch_bounds__(1024) void rollout_commit_kernel(
                 atomicAdd(&counters[C_DONE], 1);
                 admit = true;
             } else {
-                tok_in[s] = t;
+                next_tok = t;
             }
         }
         if (admit) {
@@ -89,27 +102,68 @@ __global__ __launch_bounds__(1024) void rollout_commit_kernel(
             }
             if (q2 >= n) {
                 slot_seq[s] = -1;
-                row_slot[s] = -1;
-                tok_in[s] = 0;
+                next_tok = 0;
             } else {
                 slot_seq[s] = q2;
-                row_slot[s] = s;
                 const int last = seq_ngen[q2] - 1;
-                tok_in[s] = out_tok[(size_t)q2 * maxlen + (last < 0 ? 0 : last)];
+                next_tok = out_tok[(size_t)q2 * maxlen + (last < 0 ? 0 : last)];
                 const int i = atomicAdd(&counters[C_NADMIT], 1);
                 admit_slot[i] = s;
                 admit_src[i] = seq_prompt[q2];
             }
         }
     }
+    // every thread has read its row's tok_in before any row is rewritten
+    __syncthreads();
+    if (!compact) {
+        if (s < S) {
+            const bool live = slot_seq[s] >= 0;
+            row_slot[s] = live ? s : -1;
+            tok_in[s] = live ? next_tok : 0;
+        }
+    } else {
+        // rank of each live slot among the live slots: ballot within the wave,
+        // wave totals through LDS
+        const bool live = s < S && slot_seq[s] >= 0;
+        const unsigned long long bal = __ballot(live);
+        const int lane = s & 63, w = s >> 6;
+        const int in_wave = __popcll(bal & ((1ull << lane) - 1ull));
+        if (lane == 0) wave_live[w] = __popcll(bal);
+        __syncthreads();
+        int before = 0, total = 0;
+        const int nw = (int)((blockDim.x + 63) >> 6);
+        for (int i = 0; i < nw; ++i) {
+            const int c = wave_live[i];
+            before += i < w ? c : 0;
+            total += c;
+        }
+        if (s < S) {
+            if (live) {
+                const int r = before + in_wave;
+                row_slot[r] = s;
+                slot_row[s] = r;
+                tok_in[r] = next_tok;
+            } else {
+                slot_row[s] = -1;
+            }
+            if (s >= total) {  // rows past the live ones
+                row_slot[s] = -1;
+                tok_in[s] = 0;
+            }
+        }
+        if (s == 0) counters[C_LIVE] = total;
+    }
     __syncthreads();
     if (s == 0 && have_sample) counters[C_STEP] = step + 1;
 }
 
-// Per-slot inputs of the sampler and the repetition penalty for this step.
+// Per-row inputs of the sampler and the repetition penalty for this step: row r
+// holds slot row_slot[r] (row_slot NULL: row r is slot r).  Its random stream is
+// keyed by seq_key[q] (NULL: the sequence index q) and the sequence's position.
 // seq_temp / seq_top_p / seq_top_k (nullable together): per-sequence sampling
-// parameters copied to the slot's row.
-__global__ void rollout_prepare_kernel(int S, int maxlen, const int32_t* __restrict__ slot_seq,
+// parameters copied to the row.
+__global__ void rollout_prepare_kernel(int S, int maxlen, const int32_t* __restrict__ row_slot,
+                                       const int32_t* __restrict__ slot_seq, const int64_t* __restrict__ seq_key,
                                        const int32_t* __restrict__ seq_ngen,
                                        const int32_t* __restrict__ seq_prompt,
                                        const int64_t* __restrict__ prompt_start,
@@ -121,24 +175,25 @@ __global__ void rollout_prepare_kernel(int S, int maxlen, const int32_t* __restr
                                        const int32_t* __restrict__ seq_top_k, float* __restrict__ temp,
                                        float* __restrict__ top_p, int32_t* __restrict__ top_k)
 {
-    const int s = blockIdx.x * blockDim.x + threadIdx.x;
-    if (s >= S) return;
-    const int q = slot_seq[s];
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= S) return;
+    const int s = row_slot != nullptr ? row_slot[r] : r;
+    const int q = (s >= 0 && s < S) ? slot_seq[s] : -1;
     const bool on = q >= 0;
-    active[s] = on ? 1 : 0;
-    rng_key[s] = on ? q : 0;
-    rng_ctr[s] = on ? seq_ngen[q] : 0;
+    active[r] = on ? 1 : 0;
+    rng_key[r] = on ? (seq_key != nullptr ? seq_key[q] : (int64_t)q) : 0;
+    rng_ctr[r] = on ? seq_ngen[q] : 0;
     if (seq_temp != nullptr && on) {
-        temp[s] = seq_temp[q];
-        top_p[s] = seq_top_p[q];
-        top_k[s] = seq_top_k[q];
+        temp[r] = seq_temp[q];
+        top_p[r] = seq_top_p[q];
+        top_k[r] = seq_top_k[q];
     }
     if (hist_start != nullptr) {
         const int p = on ? seq_prompt[q] : 0;
-        hist_start[s] = on ? prompt_start[p] : 0;
-        hist_len[s] = on ? prompt_len[p] : 0;
-        hist2_start[s] = on ? (int64_t)q * maxlen : 0;
-        hist2_len[s] = on ? seq_ngen[q] : 0;
+        hist_start[r] = on ? prompt_start[p] : 0;
+        hist_len[r] = on ? prompt_len[p] : 0;
+        hist2_start[r] = on ? (int64_t)q * maxlen : 0;
+        hist2_len[r] = on ? seq_ngen[q] : 0;
     }
 }
 
@@ -189,19 +244,21 @@ hipError_t launch_rollout_first(int n, int maxlen, const int64_t* tok, const flo
 }
 
 hipError_t launch_rollout_commit(int S, int n, int maxlen, int have_sample, const int64_t* tok, const float* logp,
-                                 int32_t* slot_seq, int32_t* row_slot, int64_t* tok_in, const int32_t* seq_prompt,
+                                 int32_t* slot_seq, int32_t* row_slot, int32_t* slot_row, int64_t* tok_in,
+                                 const int32_t* seq_prompt,
                                  const int32_t* seq_max_new, int32_t* seq_ngen, uint8_t* seq_done,
                                  int32_t* out_tok, float* out_logp, int32_t* out_step, int64_t eos,
                                  int32_t* counters, int32_t* admit_slot, int32_t* admit_src, hipStream_t st)
 {
     const int threads = ((S + 63) / 64) * 64;
     hipLaunchKernelGGL(rollout_commit_kernel, dim3(1), dim3(threads), 0, st, S, n, maxlen, have_sample, tok, logp,
-                       slot_seq, row_slot, tok_in, seq_prompt, seq_max_new, seq_ngen, seq_done, out_tok,
+                       slot_seq, row_slot, slot_row, tok_in, seq_prompt, seq_max_new, seq_ngen, seq_done, out_tok,
                        out_logp, out_step, eos, counters, admit_slot, admit_src);
     return hipGetLastError();
 }
 
-hipError_t launch_rollout_prepare(int S, int maxlen, const int32_t* slot_seq, const int32_t* seq_ngen,
+hipError_t launch_rollout_prepare(int S, int maxlen, const int32_t* row_slot, const int32_t* slot_seq,
+                                  const int64_t* seq_key, const int32_t* seq_ngen,
                                   const int32_t* seq_prompt, const int64_t* prompt_start,
                                   const int32_t* prompt_len, uint8_t* active, int64_t* rng_key,
                                   int32_t* rng_ctr, int64_t* hist_start, int32_t* hist_len,
@@ -209,8 +266,8 @@ hipError_t launch_rollout_prepare(int S, int maxlen, const int32_t* slot_seq, co
                                   const float* seq_top_p, const int32_t* seq_top_k, float* temp, float* top_p,
                                   int32_t* top_k, hipStream_t st)
 {
-    hipLaunchKernelGGL(rollout_prepare_kernel, dim3((S + 255) / 256), dim3(256), 0, st, S, maxlen, slot_seq,
-                       seq_ngen, seq_prompt, prompt_start, prompt_len, active, rng_key, rng_ctr, hist_start,
+    hipLaunchKernelGGL(rollout_prepare_kernel, dim3((S + 255) / 256), dim3(256), 0, st, S, maxlen, row_slot,
+                       slot_seq, seq_key, seq_ngen, seq_prompt, prompt_start, prompt_len, active, rng_key, rng_ctr, hist_start,
                        hist_len, hist2_start, hist2_len, seq_temp, seq_top_p, seq_top_k, temp, top_p, top_k);
     return hipGetLastError();
 }

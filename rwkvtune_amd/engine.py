@@ -14,15 +14,21 @@ Used by the drop-in front ends (``GRPOBatchGenerator``, ``SchedulerCore``,
 2. **First token** of every sequence from its prompt's logits, all sequences in
    one sampler launch (``grpo_batch_generator.py:262-310``).
 3. **Decode**: ``n_slots`` slots hold live sequences.  A step is the model's
-   fused single-token forward over every slot, the sampler, and the commit
+   fused single-token forward over the live rows, the sampler, and the commit
    kernel that appends tokens, retires finished sequences (EOS or per-sequence
-   length) and admits waiting ones into the freed slots by copying their
-   prompt's state from the store (fork-on-admit: G generations of one prompt
-   share one prefill).  The step is captured once in a HIP graph and replayed;
-   the host polls the finished-sequence counter every ``poll_every`` (2) steps
-   through an asynchronous copy and reads the copy made one period earlier, so
-   steps run back to back (2-4 steps stay queued) and at most 2 periods of
-   all-idle steps follow the last finished sequence.
+   length), admits waiting ones into the freed slots by copying their prompt's
+   state from the store (fork-on-admit: G generations of one prompt share one
+   prefill) and packs the live slots into the leading rows.  A step runs the
+   smallest row bucket (32, 64, 128, 192, 256, ...) that covers the live rows,
+   so the projections, row kernels and head shrink as the rollout drains; the
+   host bounds the live rows by the sequences not yet known to be finished.
+   Each bucket's step is captured once in a HIP graph and replayed; the graphs
+   and every buffer they reference live in a decode context that is reused by
+   later runs of the same configuration.  The host polls the
+   finished-sequence counter every ``poll_every`` (2) steps through an
+   asynchronous copy and reads the copy made one period earlier, so steps run
+   back to back (2-4 steps stay queued) and at most 2 periods of all-idle
+   steps follow the last finished sequence.
 4. **Collect**: one copy of the token table back to the host.
 
 Every sequence's tokens depend only on its prompt state and its own
@@ -42,7 +48,21 @@ from . import _lib
 from .model import RWKV7Model, StatePool
 from .sampler import RULE_BATCH, RULE_SINGLE, SamplerBuffers, repetition_penalty_, sample_rows
 
-C_NEXT, C_DONE, C_STEP, C_NADMIT = 0, 1, 2, 3
+C_NEXT, C_DONE, C_STEP, C_NADMIT, C_LIVE = 0, 1, 2, 3, 4
+
+ROW_BUCKETS = (32, 64, 128, 192, 256, 384, 512, 768, 1024)
+
+
+def row_buckets(S: int):
+    """Row counts a decode step may run with ``S`` slots: the buckets below S, and S."""
+    return sorted({b for b in ROW_BUCKETS if b < S} | {S})
+
+
+def seq_keys(seed: int, n: int) -> torch.Tensor:
+    """Per-sequence random-stream keys of a run (int64): distinct per (seed, sequence)."""
+    base = (int(seed) * 0x9E3779B97F4A7C15) & 0x3FFFFFFFFFFFFFFF
+    q = torch.arange(n, dtype=torch.int64)
+    return (q * 0x2545F4914F6CDD1D + base) & 0x3FFFFFFFFFFFFFFF
 
 
 @dataclass
@@ -78,12 +98,16 @@ class RolloutEngine:
     # -- prefill ---------------------------------------------------------------
 
     def prefill_store(self, prompts: Sequence[Sequence[int]], chunk_size: int, max_batch_tokens: int,
-                      max_seqs_per_forward: int = 0):
-        """Prefill ``prompts`` into a new store; returns (store, last-token logits [U, V] float32)."""
+                      max_seqs_per_forward: int = 0, store: Optional[StatePool] = None):
+        """Prefill ``prompts`` into ``store`` (zeroed first; a new one when None);
+        returns (store, last-token logits [U, V] float32)."""
         m = self.model
         dev = self.dev
         U = len(prompts)
-        store = StatePool(m.config, U, dev)
+        if store is None:
+            store = StatePool(m.config, U, dev)
+        else:
+            store.zero_()
         V = m.config.vocab_size
         last_logits = torch.empty((U, V), dtype=torch.float32, device=dev)
         lens = [len(p) for p in prompts]
@@ -138,6 +162,17 @@ class RolloutEngine:
 
     # -- full rollout ------------------------------------------------------------
 
+    def _context(self, key, n, maxlen, U, bias):
+        """The decode context of this configuration: reused (with its captured
+        graphs) when the key matches the previous run's, else built anew."""
+        ctx = getattr(self, "_ctx", None)
+        if ctx is not None and ctx.key == key and key is not None:
+            return ctx
+        self._ctx = None
+        ctx = _DecodeCtx(key, self.model, self.n_slots, n, maxlen, U, bias, self.dev)
+        self._ctx = ctx
+        return ctx
+
     @torch.no_grad()
     def run(self, prompts: Sequence[Sequence[int]], seq_prompt: Sequence[int], max_new_tokens,
             *, temperature: float = 1.0, top_p: float = 1.0, top_k: int = 0, logit_bias: Optional[dict] = None,
@@ -150,7 +185,6 @@ class RolloutEngine:
         ``(temperature[n], top_p[n], top_k[n])`` overriding the scalars per sequence."""
         m = self.model
         dev = self.dev
-        V = m.config.vocab_size
         n = len(seq_prompt)
         S = self.n_slots
         if isinstance(max_new_tokens, int):
@@ -165,124 +199,116 @@ class RolloutEngine:
         maxlen = max(max(max_new), 1 if first_can_finish else 2)
         if max_len_cap is not None:
             maxlen = min(maxlen, max_len_cap)
+        U = len(prompts)
+        use_pen = repetition_penalty != 1.0 and repetition_penalty > 0
+        bias = tuple(sorted((int(k), float(v)) for k, v in (logit_bias or {}).items()))
+        # what the captured step graphs bake in; runs with the repetition penalty
+        # (prompt-sized tables) or per-sequence sampling are not cached
+        m.packs()
+        ws = RWKV7Model.gemm_workspace(dev)
+        key = None if (use_pen or per_seq_sampling is not None) else (
+            S, n, maxlen, U, self.eos, decode_rule, self.max_valid_id, bias, m._packs_gen, ws.ws.data_ptr())
         timings = {}
         torch.cuda.synchronize(dev)
         t0 = time.perf_counter()
+        ctx = self._context(key, n, maxlen, U, bias)
 
-        # 1. prefill distinct prompts
-        store, last_logits = self.prefill_store(prompts, chunk_size, max_batch_tokens, max_seqs_per_forward)
+        # 1. prefill distinct prompts into the context's store
+        _, last_logits = self.prefill_store(prompts, chunk_size, max_batch_tokens, max_seqs_per_forward,
+                                            store=ctx.store)
         torch.cuda.synchronize(dev)
         t1 = time.perf_counter()
         timings["prefill_s"] = t1 - t0
 
-        # sequence table
-        sp = _i32(seq_prompt, dev)
-        seq_max_new = _i32(max_new, dev)
-        seq_ngen = torch.zeros(n, dtype=torch.int32, device=dev)
-        seq_done = torch.zeros(n, dtype=torch.uint8, device=dev)
-        out_tok = torch.zeros((n, maxlen), dtype=torch.int32, device=dev)
-        out_lp = torch.zeros((n, maxlen), dtype=torch.float32, device=dev)
-        out_step = torch.zeros((n, maxlen), dtype=torch.int32, device=dev)
-        counters = torch.zeros(4, dtype=torch.int32, device=dev)
-        # prompt table for the repetition penalty
+        # sequence table of this run
+        ctx.reset(seq_prompt, max_new, seq_keys(seed, n), temperature, top_p, top_k)
         plen = [len(p) for p in prompts]
-        pstart = [0]
-        for L in plen[:-1]:
-            pstart.append(pstart[-1] + L)
-        use_pen = repetition_penalty != 1.0 and repetition_penalty > 0
         if use_pen:
+            pstart = [0]
+            for L in plen[:-1]:
+                pstart.append(pstart[-1] + L)
             flat = torch.tensor([t for p in prompts for t in p], dtype=torch.int32).to(dev)
             p_start = torch.tensor(pstart, dtype=torch.int64).to(dev)
             p_len = _i32(plen, dev)
-
-        # 2. first token of every sequence
-        P = _lib.ptr
-        cur = lambda: _lib.stream_of(counters)  # the stream current at call time (graph capture changes it)
-        fbuf = SamplerBuffers(n, dev)
-        fbuf.set_uniform(temperature, top_p, top_k)
+            h_start = torch.zeros(S, dtype=torch.int64, device=dev)
+            h_len = torch.zeros(S, dtype=torch.int32, device=dev)
+            h2_start = torch.zeros(S, dtype=torch.int64, device=dev)
+            h2_len = torch.zeros(S, dtype=torch.int32, device=dev)
         if per_seq_sampling is not None:
             s_temp = torch.tensor(per_seq_sampling[0], dtype=torch.float32).to(dev)
             s_topp = torch.tensor(per_seq_sampling[1], dtype=torch.float32).to(dev)
             s_topk = torch.tensor(per_seq_sampling[2], dtype=torch.int32).to(dev)
+        else:
+            s_temp = s_topp = s_topk = None
+
+        # 2. first token of every sequence
+        P = _lib.ptr
+        c = ctx
+        cur = lambda: _lib.stream_of(c.counters)  # the stream current at call time (graph capture changes it)
+        fbuf = SamplerBuffers(n, dev)
+        fbuf.set_uniform(temperature, top_p, top_k)
+        if per_seq_sampling is not None:
             fbuf.temperature.copy_(s_temp)
             fbuf.top_p.copy_(s_topp)
             fbuf.top_k.copy_(s_topk)
-        else:
-            s_temp = s_topp = s_topk = None
         fbuf.set_bias(logit_bias, n)
-        fbuf.rng_key.copy_(torch.arange(n, dtype=torch.int64, device=dev))
+        fbuf.rng_key.copy_(c.seq_key)
         fbuf.rng_ctr.zero_()
         f_tok = torch.empty(n, dtype=torch.int64, device=dev)
         f_lp = torch.empty(n, dtype=torch.float32, device=dev)
         CH = 1024
         for a in range(0, n, CH):
             b = min(n, a + CH)
-            lg = last_logits.index_select(0, sp[a:b].long())
+            lg = last_logits.index_select(0, c.sp[a:b].long())
             if use_pen:
-                idx = sp[a:b].long()
+                idx = c.sp[a:b].long()
                 repetition_penalty_(lg, repetition_penalty, flat, p_start[idx], p_len[idx])
             sub = SamplerBuffers.__new__(SamplerBuffers)
             sub.temperature, sub.top_p, sub.top_k = fbuf.temperature[a:b], fbuf.top_p[a:b], fbuf.top_k[a:b]
             sub.rng_key, sub.rng_ctr = fbuf.rng_key[a:b], fbuf.rng_ctr[a:b]
             sub.bias_off = fbuf.bias_off[: b - a + 1] if fbuf.bias_off is not None else None
             sub.bias_ids, sub.bias_val = fbuf.bias_ids, fbuf.bias_val
-            sample_rows(lg, sub, rule=first_rule, max_valid_id=self.max_valid_id, seed=seed,
+            sample_rows(lg, sub, rule=first_rule, max_valid_id=self.max_valid_id, seed=0,
                         out_tok=f_tok[a:b], out_logp=f_lp[a:b])
-        _lib.call("rwkv7_rollout_first", n, maxlen, P(f_tok), P(f_lp), P(seq_max_new), P(seq_ngen), P(seq_done),
-                  P(out_tok), P(out_lp), P(out_step), self.eos, int(first_can_finish), P(counters), cur())
+        _lib.call("rwkv7_rollout_first", n, maxlen, P(f_tok), P(f_lp), P(c.seq_max_new), P(c.seq_ngen),
+                  P(c.seq_done), P(c.out_tok), P(c.out_lp), P(c.out_step), self.eos, int(first_can_finish),
+                  P(c.counters), cur())
         del last_logits
 
         # 3. decode
-        if self.pool is None or self.pool.n_slots != S:
-            self.pool = StatePool(m.config, S, dev)
-        pool = self.pool
-        slot_seq = torch.full((S,), -1, dtype=torch.int32, device=dev)
-        row_slot = torch.full((S,), -1, dtype=torch.int32, device=dev)
-        row_last = torch.arange(S, dtype=torch.int32, device=dev)
-        tok_in = torch.zeros(S, dtype=torch.int64, device=dev)
-        admit_slot = torch.zeros(S, dtype=torch.int32, device=dev)
-        admit_src = torch.zeros(S, dtype=torch.int32, device=dev)
-        s_tok = torch.zeros(S, dtype=torch.int64, device=dev)
-        s_lp = torch.zeros(S, dtype=torch.float32, device=dev)
-        buf = SamplerBuffers(S, dev)
-        buf.set_uniform(temperature, top_p, top_k)
-        buf.set_bias(logit_bias, S)
-        active = torch.zeros(S, dtype=torch.uint8, device=dev)
-        if use_pen:
-            h_start = torch.zeros(S, dtype=torch.int64, device=dev)
-            h_len = torch.zeros(S, dtype=torch.int32, device=dev)
-            h2_start = torch.zeros(S, dtype=torch.int64, device=dev)
-            h2_len = torch.zeros(S, dtype=torch.int32, device=dev)
         cfg = m.config
         kv_elems = cfg.n_head * 64 * 64
-        U = store.n_slots
+        pool = c.pool
 
         def commit(have_sample):
             st = cur()
-            _lib.call("rwkv7_rollout_commit", S, n, maxlen, int(have_sample), P(s_tok), P(s_lp), P(slot_seq),
-                      P(row_slot), P(tok_in), P(sp), P(seq_max_new), P(seq_ngen), P(seq_done), P(out_tok),
-                      P(out_lp), P(out_step), self.eos, P(counters), P(admit_slot), P(admit_src), st)
-            _lib.call("rwkv7_admit_copy", P(counters), P(admit_slot), P(admit_src), cfg.n_layer, S, U, kv_elems,
-                      cfg.n_embd, P(store.kv), P(store.att_x), P(store.ffn_x), P(pool.kv), P(pool.att_x),
-                      P(pool.ffn_x), st)
+            _lib.call("rwkv7_rollout_commit", S, n, maxlen, int(have_sample), P(c.s_tok), P(c.s_lp),
+                      P(c.slot_seq), P(c.row_slot), P(c.slot_row), P(c.tok_in), P(c.sp), P(c.seq_max_new),
+                      P(c.seq_ngen), P(c.seq_done), P(c.out_tok), P(c.out_lp), P(c.out_step), self.eos,
+                      P(c.counters), P(c.admit_slot), P(c.admit_src), st)
+            _lib.call("rwkv7_admit_copy", P(c.counters), P(c.admit_slot), P(c.admit_src), cfg.n_layer, S, U,
+                      kv_elems, cfg.n_embd, P(c.store.kv), P(c.store.att_x), P(c.store.ffn_x), P(pool.kv),
+                      P(pool.att_x), P(pool.ffn_x), st)
 
-        def step():
-            logits = m.forward_pooled(tok_in, row_slot, row_last, pool, decode=True)
+        def step(Mb):
+            logits = m.forward_pooled(c.tok_in[:Mb], c.row_slot[:Mb], c.row_last[:Mb], pool, decode=True)
             st = cur()
+            buf = c.buf
             if use_pen:
-                _lib.call("rwkv7_rollout_prepare", S, maxlen, P(slot_seq), P(seq_ngen), P(sp), P(p_start),
-                          P(p_len), P(active), P(buf.rng_key), P(buf.rng_ctr), P(h_start), P(h_len),
-                          P(h2_start), P(h2_len), P(s_temp), P(s_topp), P(s_topk), P(buf.temperature),
-                          P(buf.top_p), P(buf.top_k), st)
+                _lib.call("rwkv7_rollout_prepare", S, maxlen, P(c.row_slot), P(c.slot_seq), P(c.seq_key),
+                          P(c.seq_ngen), P(c.sp), P(p_start), P(p_len), P(c.active), P(buf.rng_key),
+                          P(buf.rng_ctr), P(h_start), P(h_len), P(h2_start), P(h2_len), P(s_temp), P(s_topp),
+                          P(s_topk), P(buf.temperature), P(buf.top_p), P(buf.top_k), st)
                 logits = logits.float()
-                repetition_penalty_(logits, repetition_penalty, flat, h_start, h_len, out_tok.view(-1),
-                                    h2_start, h2_len, active)
+                repetition_penalty_(logits, repetition_penalty, flat, h_start, h_len, c.out_tok.view(-1),
+                                    h2_start, h2_len, c.active)
             else:
-                _lib.call("rwkv7_rollout_prepare", S, maxlen, P(slot_seq), P(seq_ngen), None, None, None,
-                          P(active), P(buf.rng_key), P(buf.rng_ctr), None, None, None, None, P(s_temp),
-                          P(s_topp), P(s_topk), P(buf.temperature), P(buf.top_p), P(buf.top_k), st)
-            sample_rows(logits, buf, rule=decode_rule, max_valid_id=self.max_valid_id, seed=seed,
-                        out_tok=s_tok, out_logp=s_lp, active=active)
+                _lib.call("rwkv7_rollout_prepare", S, maxlen, P(c.row_slot), P(c.slot_seq), P(c.seq_key),
+                          P(c.seq_ngen), None, None, None, P(c.active), P(buf.rng_key), P(buf.rng_ctr), None, None,
+                          None, None, P(s_temp), P(s_topp), P(s_topk), P(buf.temperature), P(buf.top_p),
+                          P(buf.top_k), st)
+            sample_rows(logits, buf, rule=decode_rule, max_valid_id=self.max_valid_id, seed=0,
+                        out_tok=c.s_tok, out_logp=c.s_lp, active=c.active)
             commit(True)
 
         commit(False)  # initial admission
@@ -290,46 +316,58 @@ class RolloutEngine:
         t2 = time.perf_counter()
         timings["first_token_s"] = t2 - t1
 
+        buckets = row_buckets(S)
         h_done = torch.zeros(2, dtype=torch.int32).pin_memory()
         cap = n * maxlen + 16
         n_steps = 0
-        graph = None
         pending_evt = None
         done = False
+        finished = 0  # sequences known to be finished (from the last completed poll)
         while not done and n_steps < cap:
             for _ in range(self.poll_every):
-                if graph is None and self.use_graph and n_steps >= 1:
-                    graph = torch.cuda.CUDAGraph()
-                    with torch.cuda.graph(graph):
-                        step()
-                if graph is not None:
-                    graph.replay()
+                if ws.ws.data_ptr() != c.ws_ptr:
+                    # the split-K workspace was reallocated: the captured graphs hold the old one
+                    c.graphs.clear()
+                    c.ws_ptr = ws.ws.data_ptr()
+                # rows needed: the live rows are at most the sequences not known to be finished
+                bound = min(S, n - finished)
+                Mb = next(b for b in buckets if b >= bound)
+                g = c.graphs.get(Mb)
+                if g is None and self.use_graph and Mb in c.warm:
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g, pool=c.graph_pool):
+                        step(Mb)
+                    c.graphs[Mb] = g
+                if g is not None:
+                    g.replay()
                 else:
-                    step()
+                    step(Mb)  # the first step of a bucket runs eagerly (lazy allocations happen outside capture)
+                    c.warm.add(Mb)
                 n_steps += 1
             # read the counters copied one polling period ago (already complete
             # unless the GPU is behind), then queue a fresh copy
             if pending_evt is not None:
                 pending_evt.synchronize()
-                if int(h_done[0]) >= n:
+                finished = int(h_done[0])
+                if finished >= n:
                     done = True
-            h_done[0:2].copy_(counters[1:3], non_blocking=True)
+            h_done[0:2].copy_(c.counters[1:3], non_blocking=True)
             pending_evt = torch.cuda.Event()
             pending_evt.record()
         torch.cuda.synchronize(dev)
         if int(h_done[0]) < n:
-            h = counters.cpu()
+            h = c.counters.cpu()
             if int(h[C_DONE]) < n:
                 raise RuntimeError(f"rollout did not finish: {int(h[C_DONE])}/{n} sequences after {n_steps} steps")
         t3 = time.perf_counter()
         timings["decode_s"] = t3 - t2
 
         # 4. collect
-        ng = seq_ngen.cpu().tolist()
-        ot = out_tok.cpu()
-        ol = out_lp.cpu()
-        os_ = out_step.cpu()
-        n_dec = int(counters[C_STEP].item())
+        ng = c.seq_ngen.cpu().tolist()
+        ot = c.out_tok.cpu()
+        ol = c.out_lp.cpu()
+        os_ = c.out_step.cpu()
+        n_dec = int(c.counters[C_STEP].item())
         toks = [ot[q, :ng[q]].tolist() for q in range(n)]
         lps = [ol[q, :ng[q]].tolist() for q in range(n)]
         stp = [os_[q, :ng[q]].tolist() for q in range(n)]
@@ -337,4 +375,57 @@ class RolloutEngine:
         timings["collect_s"] = t4 - t3
         timings["total_s"] = t4 - t0
         timings["decode_steps_issued"] = n_steps
+        if key is None:
+            self._ctx = None  # uncached: drop its buffers and graphs
         return RolloutResult(toks, lps, stp, n_dec, timings, prompt_tokens=sum(plen))
+
+
+class _DecodeCtx:
+    """Every buffer a decode step reads or writes, for one configuration (slots,
+    sequences, token columns, prompts, logit bias): the prompt store, the slot
+    pool, the sequence / slot / row tables, the sampler's per-row inputs and the
+    captured step graph of each row bucket.  Kept by the engine so that later
+    runs of the same configuration replay the same graphs."""
+
+    def __init__(self, key, model, S, n, maxlen, U, bias, dev):
+        self.key = key
+        cfg = model.config
+        self.store = StatePool(cfg, U, dev)
+        self.pool = StatePool(cfg, S, dev)
+        self.sp = torch.zeros(n, dtype=torch.int32, device=dev)
+        self.seq_max_new = torch.zeros(n, dtype=torch.int32, device=dev)
+        self.seq_key = torch.zeros(n, dtype=torch.int64, device=dev)
+        self.seq_ngen = torch.zeros(n, dtype=torch.int32, device=dev)
+        self.seq_done = torch.zeros(n, dtype=torch.uint8, device=dev)
+        self.out_tok = torch.zeros((n, maxlen), dtype=torch.int32, device=dev)
+        self.out_lp = torch.zeros((n, maxlen), dtype=torch.float32, device=dev)
+        self.out_step = torch.zeros((n, maxlen), dtype=torch.int32, device=dev)
+        self.counters = torch.zeros(8, dtype=torch.int32, device=dev)
+        self.slot_seq = torch.full((S,), -1, dtype=torch.int32, device=dev)
+        self.row_slot = torch.full((S,), -1, dtype=torch.int32, device=dev)
+        self.slot_row = torch.full((S,), -1, dtype=torch.int32, device=dev)
+        self.row_last = torch.arange(S, dtype=torch.int32, device=dev)
+        self.tok_in = torch.zeros(S, dtype=torch.int64, device=dev)
+        self.admit_slot = torch.zeros(S, dtype=torch.int32, device=dev)
+        self.admit_src = torch.zeros(S, dtype=torch.int32, device=dev)
+        self.s_tok = torch.zeros(S, dtype=torch.int64, device=dev)
+        self.s_lp = torch.zeros(S, dtype=torch.float32, device=dev)
+        self.active = torch.zeros(S, dtype=torch.uint8, device=dev)
+        self.buf = SamplerBuffers(S, dev)
+        self.buf.set_bias(dict(bias) if bias else None, S)
+        self.graphs: Dict[int, torch.cuda.CUDAGraph] = {}
+        self.warm = set()
+        self.graph_pool = torch.cuda.graph_pool_handle()
+        self.ws_ptr = RWKV7Model.gemm_workspace(dev).ws.data_ptr()
+
+    def reset(self, seq_prompt, max_new, keys, temperature, top_p, top_k):
+        self.sp.copy_(torch.as_tensor(seq_prompt, dtype=torch.int32))
+        self.seq_max_new.copy_(torch.as_tensor(max_new, dtype=torch.int32))
+        self.seq_key.copy_(keys)
+        for t in (self.seq_ngen, self.seq_done, self.out_tok, self.out_lp, self.out_step, self.counters,
+                  self.tok_in, self.s_tok, self.s_lp, self.active):
+            t.zero_()
+        for t in (self.slot_seq, self.row_slot, self.slot_row):
+            t.fill_(-1)
+        # (the slot pool needs no clearing: admission copies a slot's whole state)
+        self.buf.set_uniform(temperature, top_p, top_k)

@@ -397,6 +397,7 @@ class RWKV7Model(nn.Module):
         self._packs = None
         self._packs_key = None
         self._packs_struct = None
+        self._packs_gen = 0  # bumped whenever the packs are rebuilt (new buffers)
         # decode rows of a bf16 model run their projections on the library's
         # grouped MFMA GEMM over packed weights: r, k, v and the LoRA downs (tanh /
         # sigmoid fused) in one launch, the LoRA ups in one, the FFN key (relu^2
@@ -481,6 +482,7 @@ class RWKV7Model(nn.Module):
                 self._ln_out = (self.ln_out.weight.detach().float().contiguous(),
                                 self.ln_out.bias.detach().float().contiguous())
                 self._packs_struct = self._struct_key()
+                self._packs_gen += 1
         self._packs_key = key
         return self._packs
 
@@ -510,6 +512,14 @@ class RWKV7Model(nn.Module):
                 self.ws = torch.empty(max(floats, 2 * self.ws.numel()), dtype=torch.float32, device=self.ws.device)
 
     _gemm_ws = {}
+
+    @staticmethod
+    def gemm_workspace(dev) -> "RWKV7Model.GemmWorkspace":
+        """The device's shared split-K workspace (created on first use)."""
+        ws = RWKV7Model._gemm_ws.get(dev)
+        if ws is None:
+            ws = RWKV7Model._gemm_ws[dev] = RWKV7Model.GemmWorkspace(dev)
+        return ws
 
     @staticmethod
     def _gemm_group(M: int, probs, stream):

@@ -40,7 +40,7 @@ def test_header_matches_exports(lib):
 
 
 def test_abi_version(lib):
-    assert lib.rwkv7_abi_version() == 1
+    assert lib.rwkv7_abi_version() == 2
 
 
 def _null6():

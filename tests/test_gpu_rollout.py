@@ -238,3 +238,38 @@ def test_scheduler_sampled_streams_independent_of_slots(tiny):
         runs.append([s.generated_tokens for s in seqs])
     assert runs[0] == runs[1]
     assert all(len(t) == 8 for t in runs[0])
+
+
+def test_row_buckets_greedy_parity_and_graph_reuse(tiny):
+    """96 slots run rows in buckets of 32 / 64 / 96 as the rollout drains (live
+    slots packed into the leading rows): 150 greedy paths with caps 1..24 equal
+    the reference loop.  A second engine run of the same configuration replays
+    the first run's captured graphs: a sampled run with a new seed equals the
+    same seed's run on a fresh engine, and repeating a seed repeats the tokens."""
+    print("[case] row buckets: parity across buckets, graph reuse", flush=True)
+    m, sd = tiny
+    ps = prompts(50, 50, 2, 12)
+    g = torch.Generator().manual_seed(51)
+    caps = torch.randint(1, 25, (150,), generator=g).tolist()
+    gen = GRPOBatchGenerator(m, TinyTok(), chunk_size=16, max_decode_batch_size=96, verbose=False)
+    out = gen.generate(ps, 24, num_generations=3, temperature=0.0, top_p=1.0, max_new_tokens_per_seq=caps)
+    ref, _ = orl.grpo_rollout(sd, ps, 24, 3, max_valid_id=V - 4, caps=caps)
+    ids, masks = out["completion_ids"].cpu(), out["masks"].cpu()
+    for q, r in enumerate(ref):
+        assert ids[q, :int(masks[q].sum())].tolist() == r, q
+    eng = gen._engines[96]
+    assert set(eng._ctx.graphs) == {32, 64, 96}, sorted(eng._ctx.graphs)
+
+    def sampled(generator, seed):
+        o = generator.generate(ps, 24, num_generations=3, temperature=1.0, top_p=0.9, max_new_tokens_per_seq=caps,
+                               seed=seed)
+        i, mk = o["completion_ids"].cpu(), o["masks"].cpu()
+        return [i[q, :int(mk[q].sum())].tolist() for q in range(i.shape[0])]
+
+    graphs_before = dict(eng._ctx.graphs)
+    a = sampled(gen, 5)
+    assert eng._ctx.graphs == graphs_before   # the same graph objects were replayed
+    b = sampled(gen, 6)
+    fresh = GRPOBatchGenerator(m, TinyTok(), chunk_size=16, max_decode_batch_size=96, verbose=False)
+    assert sampled(fresh, 6) == b
+    assert sampled(gen, 5) == a and a != b
