@@ -258,7 +258,7 @@ def test_row_buckets_greedy_parity_and_graph_reuse(tiny):
     for q, r in enumerate(ref):
         assert ids[q, :int(masks[q].sum())].tolist() == r, q
     eng = gen._engines[96]
-    assert set(eng._ctx.graphs) == {32, 64, 96}, sorted(eng._ctx.graphs)
+    assert set(eng._ctx.graphs) >= {32, 64, 96}, sorted(eng._ctx.graphs)
 
     def sampled(generator, seed):
         o = generator.generate(ps, 24, num_generations=3, temperature=1.0, top_p=0.9, max_new_tokens_per_seq=caps,
