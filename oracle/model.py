@@ -10,7 +10,12 @@ Follows ``rwkvtune/models/rwkv7/model.py``:
   model            :468-497  (embedding, blocks, ln_out, head over every position)
 The WKV recurrence is ``oracle.wkv7``: ``wkv7_cpu`` (the reference CPU operator,
 ``wkv_cpu.py:9-76``) when ``dtype`` is float32, ``wkv7_rowwise`` otherwise
-(float64 is the high-precision oracle).  Parameters come as a plain
+(float64 is the high-precision oracle).  ``dtype=torch.bfloat16`` restates the
+reference's bf16 GPU path: every eager op runs on bf16 tensors and rounds its
+result to bf16 (the residual stream included, ``model.py:190-278, 310-343,
+382-418``), and the WKV op gets bf16 operands - the raw decay ``w`` too - keeps
+its state in float32 and returns bf16 ``y`` (``model.py:233-250``,
+``wkv7s.cu:22-53``).  Parameters come as a plain
 ``{name: tensor}`` state dict with the reference's names; all math runs in
 ``dtype`` on the CPU (the reference runs float32 on CPU, ``pipeline.py:166-175``).
 
@@ -27,7 +32,12 @@ key update k (1 + (a - 1) k_a) = 3/4 k; the bonus |x|^2 x; the token-shift
 direction (mix 1 reads the previous token); relu(x)^2 of the channel mix at
 six points and its shift.  Swapping the decay sign, the value-residual
 direction, b = kk for kk * a, relu for relu^2, the shift direction, the bonus
-axis or the gate's sigmoid placement each fails at least one of these.
+axis or the gate's sigmoid placement each fails at least one of these.  The
+bf16 statement is pinned by hand-rounded values on the transparent layer: the
+decay operand at w0 = 0 is bf16(-bf16(ln 2) - 0.5) = -1.1875 (not -1.1931), and
+a = sigmoid(1) reaches the delta rule as 0.73046875 (not 0.7310586); on a random
+model it stays within bf16 rounding of the float64 statement but not closer
+than the rounding allows, and its WKV state is float32.
 """
 
 from __future__ import annotations
@@ -96,6 +106,11 @@ def time_mix(sd, i, cfg, x, v_first, x_prev, att_kv, dtype):
     w = -F.softplus(-(sd[p + "w0"].reshape(C) + w_lin)) - 0.5
     if dtype == torch.float32:
         y, S = wkv7_cpu(r, w, k, v, -kk, kk * a, N, att_kv)
+    elif dtype == torch.bfloat16:
+        # the reference's GPU op: bf16 operands, float32 state, bf16 y
+        ops = [t.to(torch.bfloat16) for t in (r, w, k, v, -kk, kk * a)]
+        y, S = wkv7_rowwise(*ops, N, att_kv.to(torch.float32), dtype=torch.float32)
+        y = y.to(torch.bfloat16)
     else:
         y, S = wkv7_rowwise(r, w, k, v, -kk, kk * a, N, att_kv, dtype=dtype)
     y = F.group_norm(y.reshape(B * T, C).to(dtype), H, sd[p + "ln_x.weight"], sd[p + "ln_x.bias"],
@@ -103,7 +118,7 @@ def time_mix(sd, i, cfg, x, v_first, x_prev, att_kv, dtype):
     bonus = (r.view(B, T, H, N) * k.view(B, T, H, N) * sd[p + "r_k"].reshape(H, N)).sum(-1, keepdim=True)
     y = y + (bonus * v.view(B, T, H, N)).view(B, T, C)
     y = (y * g) @ sd[p + "output.weight"].T
-    return y, v_first, x[:, -1], S.to(dtype)
+    return y, v_first, x[:, -1], (S if dtype == torch.bfloat16 else S.to(dtype))
 
 
 def channel_mix(sd, i, x, x_prev):
@@ -136,8 +151,9 @@ def forward_with_state(sd, idx, states=None, dtype=torch.float64, skip_ln0=False
         if i == 0 and not skip_ln0:
             x = _ln(x, sd, "blocks.0.ln0")
         h = _ln(x, sd, f"blocks.{i}.ln1")
+        kv_dt = torch.float32 if dtype == torch.bfloat16 else dtype
         att, v_first, ax, kv = time_mix(sd, i, cfg, h, v_first, st["att_x_prev"].to(dtype),
-                                        st["att_kv"].to(dtype), dtype)
+                                        st["att_kv"].to(kv_dt), dtype)
         x = x + att
         h2 = _ln(x, sd, f"blocks.{i}.ln2")
         ffn, fx = channel_mix(sd, i, h2, st["ffn_x_prev"].to(dtype))

@@ -4,9 +4,13 @@ GEMMs) against the float64 CPU oracle (oracle/model.py).
 Tolerances:
   float32 model: logits and every state tensor within 1e-4 relative (norm over the
       whole tensor); the GEMMs accumulate in float32 in a different order.
-  bfloat16 model: activations are rounded to bf16 at every GEMM boundary (as in
-      the reference's bf16 path), so logits within 3e-2 relative and the WKV state
-      within 3e-2 relative of the float64 oracle run on the same bf16 weights.
+  bfloat16 model: activations are rounded to bf16 at every GEMM boundary, so logits
+      within 3e-2 relative and the WKV state within 3e-2 relative of the float64
+      oracle run on the same bf16 weights.  The reference's bf16 path rounds more
+      often (every eager op, and the WKV operands); the oracle's bf16 statement
+      follows those rounding points: the bf16 model must be no further from float64
+      than that path is (measured: 0.52-0.57x), and within 1.5x of that path's own
+      error from it (measured: 1.14-1.17x).
 """
 
 import pytest
@@ -182,3 +186,61 @@ def test_activation_kernel(gpu_device, dtype):
             d = (view.float() - exp.float()).abs()
             ulp = torch.finfo(dtype).eps * exp.float().abs().clamp_min(torch.finfo(dtype).tiny)
             assert bool((d <= 2 * ulp + 1e-7).all()), (kind, float(d.max()))
+
+
+BF16_SHAPES = {
+    "tiny": lambda: RWKV7Config(n_layer=3, n_embd=256, vocab_size=V, dim_att_lora=32, dim_gate_lora=64,
+                                dim_mv_lora=32),
+    "1.5b-width": lambda: config_from_preset("rwkv7-1.5b", n_layer=2, vocab_size=V),
+}
+
+
+@pytest.mark.parametrize("grouped", [False, True])
+@pytest.mark.parametrize("shape", sorted(BF16_SHAPES))
+def test_bf16_error_within_reference_bf16_path(gpu_device, shape, grouped):
+    """The reference's bf16 path (model.py:190-278, 310-343, 382-418 on bf16
+    tensors; wkv7s.cu with bf16 operands and a float32 state) is restated by the
+    oracle's bf16 statement.  The bf16 model rounds less often (element-wise work
+    and the WKV operands stay float32 inside the fused kernels), so for the
+    logits and every state tensor, after a 12-token prefill and after each of
+    three decode steps:
+      rel(ours, fp64) <= rel(ref_bf16, fp64) + 1e-4
+      rel(ours, ref_bf16) <= 1.5 rel(ref_bf16, fp64) + 1e-4
+    i.e. the HIP path is no further from exact arithmetic than the reference's
+    own bf16 path and lies within that path's rounding scale of it."""
+    print(f"[case] bf16 vs the reference bf16 path: {shape}, grouped decode GEMM {grouped}", flush=True)
+    m = build_model(BF16_SHAPES[shape](), dtype=torch.bfloat16, device="cuda", seed=41)
+    sd16 = om.cast_state_dict(m.state_dict(), torch.bfloat16)
+    sd64 = om.cast_state_dict(sd16, torch.float64)
+    g = torch.Generator().manual_seed(42)
+    worst = [0.0, 0.0]
+
+    def check(tag, ours, r16, r64):
+        e_o, e_r, e_or = rel(ours, r64), rel(r16, r64), rel(ours, r16)
+        worst[0] = max(worst[0], e_o / e_r)
+        worst[1] = max(worst[1], e_or / e_r)
+        assert e_o <= e_r + 1e-4, f"{tag}: ours {e_o:.3e} vs reference bf16 path {e_r:.3e}"
+        assert e_or <= 1.5 * e_r + 1e-4, f"{tag}: ours to reference bf16 path {e_or:.3e} (its error {e_r:.3e})"
+
+    def check_all(tag, out, ref16, ref64):
+        check(tag + " logits", out[0], ref16[0], ref64[0])
+        for l, (a, b, c) in enumerate(zip(out[1], ref16[1], ref64[1])):
+            for k in ("att_x_prev", "att_kv", "ffn_x_prev"):
+                check(f"{tag} layer {l} {k}", a[k], b[k], c[k])
+
+    idx = torch.randint(0, V, (3, 12), generator=g)
+    out = m.forward_with_state(idx.to(gpu_device))
+    ref16 = om.forward_with_state(sd16, idx, dtype=torch.bfloat16)
+    ref64 = om.forward_with_state(sd64, idx)
+    check_all("prefill", out, ref16, ref64)
+    m.use_grouped_gemm = grouped
+    try:
+        for step in range(3):
+            tok = torch.randint(0, V, (3, 1), generator=g)
+            out = m.forward_with_state(tok.to(gpu_device), out[1])
+            ref16 = om.forward_with_state(sd16, tok, ref16[1], dtype=torch.bfloat16)
+            ref64 = om.forward_with_state(sd64, tok, ref64[1])
+            check_all(f"decode {step}", out, ref16, ref64)
+    finally:
+        m.use_grouped_gemm = False
+    print(f"  worst ratio to the reference bf16 error: from fp64 {worst[0]:.2f}, from it {worst[1]:.2f}", flush=True)

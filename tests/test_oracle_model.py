@@ -343,3 +343,87 @@ def test_channel_mix_relu_squared_and_shift():
     out, _ = om.channel_mix(sd, 0, seq, pts.view(1, C))
     assert torch.allclose(out[0, 0], want, rtol=0, atol=1e-14)
     assert torch.allclose(out[0, 1], torch.clamp(other, min=0) ** 2, rtol=1e-14, atol=1e-14)
+
+
+# ---------------------------------------------------------------------------
+# bf16 statement (the reference's bf16 GPU path): hand-rounded values on the
+# transparent layer show which operands are rounded to bf16 before the WKV op.
+# ---------------------------------------------------------------------------
+
+def _run_time_mix_bf16(sd, i, x, S0=None):
+    sd16 = om.cast_state_dict(sd, torch.bfloat16)
+    cfg = om.config_of(sd16)
+    B, T, C = x.shape
+    kv = torch.zeros(B, cfg.n_head, N, N, dtype=torch.float32) if S0 is None else S0.float()
+    return om.time_mix(sd16, i, cfg, x.to(torch.bfloat16), None, torch.zeros(B, C, dtype=torch.bfloat16), kv,
+                       torch.bfloat16)
+
+
+def test_bf16_decay_operand_is_rounded():
+    """The reference computes w = -softplus(-(w0 + w_lora)) - 0.5 on bf16 tensors
+    (model.py:227) and hands the rounded w to the WKV op (wkv7s.cu:27 applies
+    exp(-exp(w)) in float).  At w0 = 0: softplus(0) = ln 2 = 0.693147 rounds to
+    177/256 = 0.69140625; minus 0.5 gives 1.19140625 = 1.0011000|1b, a tie that
+    rounds to even: w = -1.1875 and d = exp(-exp(-1.1875)) = 0.7371361..., not
+    the unrounded 0.7384031.  At w0 = +30, w = -0.5 exactly; at -30, w = -30.5.
+    Inputs in {+-1, +-2} keep every other product exact, so the float32 state is
+    S = x1 x1^T diag(d) + x2 x2^T to float32 rounding."""
+    sd = tiny_sd(31, L=1)
+    C = 256
+    H = C // N
+    p = _transparent(sd, 0, C)
+    pattern = torch.tensor([30.0, 0.0, -30.0], dtype=torch.float64)
+    sd[p + "w0"] = pattern.repeat(C // 3 + 1)[:C].reshape(sd[p + "w0"].shape)
+    d_of = {30.0: math.exp(-math.exp(-0.5)), 0.0: math.exp(-math.exp(-1.1875)), -30.0: 1.0}
+    assert abs(d_of[0.0] - 0.7371361) < 1e-7
+    d = torch.tensor([d_of[float(w)] for w in sd[p + "w0"].reshape(C)], dtype=torch.float64)
+    g = torch.Generator().manual_seed(32)
+    x = torch.tensor([-2.0, -1.0, 1.0, 2.0], dtype=torch.float64)[torch.randint(0, 4, (1, 2, C), generator=g)]
+    y, _, _, S = _run_time_mix_bf16(sd, 0, x)
+    assert y.dtype == torch.bfloat16 and S.dtype == torch.float32
+    x1, x2, dh = x[0, 0].view(H, N), x[0, 1].view(H, N), d.view(H, N)
+    expect = x1[:, :, None] * (x1 * dh)[:, None, :] + x2[:, :, None] * x2[:, None, :]
+    assert torch.allclose(S[0].double(), expect, rtol=2e-7, atol=2e-7)
+
+
+def test_bf16_delta_rule_gets_rounded_a():
+    """a = sigmoid(a0 + a_lora) is a bf16 tensor in the reference (model.py:221),
+    so b = kk * a reaches the WKV op rounded: at a0 = 1, sigmoid(1) = 0.7310586
+    rounds to 187/256 = 0.73046875.  As in the float64 delta-rule test (kk = e_0,
+    v = 0, decay 1, S0 = I) one step gives S1[0, 0] = 1 - a = 0.26953125
+    exactly, where the unrounded a would give 0.2689414."""
+    sd = tiny_sd(33, L=1)
+    C = 256
+    H = C // N
+    p = _transparent(sd, 0, C)
+    sd[p + "value.weight"] = torch.zeros(C, C, dtype=torch.float64)
+    sd[p + "k_k"] = torch.ones_like(sd[p + "k_k"])
+    sd[p + "a0"] = torch.ones_like(sd[p + "a0"])
+    x = torch.zeros(1, 1, C, dtype=torch.float64)
+    x[0, 0, ::N] = 3.0
+    S0 = torch.eye(N, dtype=torch.float64).expand(1, H, N, N).clone()
+    _, _, _, S = _run_time_mix_bf16(sd, 0, x, S0=S0)
+    expect = S0.clone()
+    expect[0, :, 0, 0] = 0.26953125
+    assert torch.equal(S.double(), expect)
+
+
+def test_bf16_statement_within_rounding_of_fp64():
+    """On a random two-layer model the bf16 statement's logits and states stay
+    within bf16 rounding of the float64 statement on the same (bf16) weights,
+    and differ from it by more than float32 arithmetic would: each eager op is
+    rounded.  The WKV state it returns is float32 and the logits bf16."""
+    sd16 = tiny_sd(34, L=2, dtype=torch.bfloat16)
+    sd64 = om.cast_state_dict(sd16, torch.float64)
+    idx = torch.randint(0, 300, (2, 9), generator=torch.Generator().manual_seed(35))
+    l16, s16 = om.forward_with_state(sd16, idx, dtype=torch.bfloat16)
+    l64, s64 = om.forward_with_state(sd64, idx, dtype=torch.float64)
+    assert l16.dtype == torch.bfloat16 and s16[0]["att_kv"].dtype == torch.float32
+
+    def rel(a, b):
+        return float((a.double() - b).norm() / b.norm())
+
+    assert 1e-4 < rel(l16, l64) < 2e-2
+    for l in range(2):
+        for k in ("att_x_prev", "att_kv", "ffn_x_prev"):
+            assert rel(s16[l][k], s64[l][k]) < 2e-2, (l, k)
