@@ -238,8 +238,10 @@ int rwkv7_gemm_decode(int64_t M, int count, const void *const *A, const void *co
  * split-K partials go to the library's static scratch, a fixed array of
  * RWKV7_GEMM_SCRATCH_FLOATS floats (8 MiB) that every GPU the library runs on
  * holds until the process ends.  Problem sets needing more (see
- * rwkv7_gemm_decode_workspace; every 1.5B / 7.2B decode projection set needs at
- * most 1.6M floats) return RWKV7_ERR_INVALID.  The scratch needs no clearing
+ * rwkv7_gemm_decode_workspace) return RWKV7_ERR_INVALID; with the library's
+ * split plan none does: K is split only at M <= 64 rows, to about 256 blocks of
+ * at most 64 x 64 outputs, so a set needs at most 510 * 64 * 64 = 2,088,960
+ * floats.  The check stays for plans that may split more.  The scratch needs no clearing
  * (every range writes all its partials before they are read).  All calls on one
  * GPU share its scratch, so calls that overlap on one GPU (concurrent streams,
  * threads) race; calls in one stream's order do not.  The first call on a device
@@ -258,7 +260,8 @@ int rwkv7_gemm_decode_noalloc(int64_t M, int count, const void *const *A, const 
  * of the plan's P = rwkv7_gemm_decode_partial_count(M, N, K) K ranges are left in
  * `workspace` as float32 planes [P][M][N] (16-byte aligned, P * M * N floats),
  * and *parts (host) receives P (also when P = 1).  Their in-order sum rounded to
- * bf16 equals rwkv7_gemm_decode's C; rwkv7_shift_mix / rwkv7_final_norm take the
+ * bf16 is the product (rwkv7_gemm_decode may split K differently, so its C can
+ * differ in the last bit); rwkv7_shift_mix / rwkv7_final_norm take the
  * planes directly (add_parts = P, add_part_stride = M * N), which saves the
  * reduction launch.  For the FFN value projection (model.py:338) ahead of the
  * next layer's residual add.  partial_count returns -1 on invalid sizes.

@@ -21,7 +21,7 @@
 //     ~5 TB/s for long contiguous runs (measured on MI355X);
 //   * a block of 4 or 8 waves computes a BM x BN tile (a template: waves in a
 //     WM x WN grid, each MS x NS tiles of v_mfma_f32_32x32x16_bf16; BN a
-//     multiple of 64).  A CU moves roughly 30-40 GB/s of vector loads whether
+//     multiple of 32); the tile and the K split are chosen by row count.  A CU moves roughly 30-40 GB/s of vector loads whether
 //     they hit L2 or not (measured), so at M = 256 the activation re-reads,
 //     not the weights, dominate a small tile; large tiles cut them, and split
 //     K restores the block count;
@@ -483,22 +483,52 @@ hipError_t launch_tile(int M, int count, const void* const* A, const void* const
     return hipGetLastError();
 }
 
-// The library's tile: 64 x 64, 8 waves (two K groups), 4 stages.  Sweeps over
-// 64..256 x 64..256 tiles, 4, 8 or 16 waves, 2..8 stages and 1..8 K splits at
-// the 1.5B decode shapes (M = 32..256) put it first or within a few percent of
-// the best everywhere: a CU's load path, not the tile, bounds these launches.
-// Launches aim at 384 blocks (1.5 per CU) by splitting K into ranges of at
-// least 512.
-using TileDecode = Tile<2, 2, 1, 1, 4, 2>;
-// At most 32 rows (the ragged tail of a rollout) every block only streams
-// weights, and a 32 x 32 tile (4 K groups) gives twice the column tiles and
-// half the dead activation rows: ~7% faster there (measured).
+// Tiles and K splits by row count, chosen by a sweep of tiles (32 x 32 to
+// 256 x 32, 64 x 64, 128 x 64; 4 to 16 waves) and block targets (1 to 512)
+// over the five launches of a 1.5B decode layer at M = 32 .. 256, cold weights
+// (MI355X):
+//   * up to 32 rows a 32 x 32 tile (4 K groups): every block only streams
+//     weights, and the narrow tile gives twice the column tiles and half the dead
+//     activation rows; up to 128 rows 64 x 64 (8 waves, two K groups); above,
+//     128 x 64 (8 waves, one K group), which halves the activation re-reads of a
+//     column tile and is 10-25% faster there (87.7 -> 73 us per layer at M = 256);
+//   * results the kernel writes itself (epilogue applied) split K only at
+//     M <= 64, to about 256 blocks: above that the reduction launch costs more
+//     than the split gains;
+//   * partial planes (summed by the next row kernel, no reduction launch)
+//     split to about 512 blocks up to 128 rows and 256 above.
 using TileNarrow = Tile<1, 1, 1, 1, 4, 4>;
-constexpr int kTarget = 384, kMinK = 512;
+using TileDecode = Tile<2, 2, 1, 1, 4, 2>;
+using TileWide = Tile<4, 2, 1, 1, 4, 1>;
+constexpr int kMinK = 512;
 
-Plan plan_for(int M, int count, const int* N, const int* K) {
-    if (M <= 32) return make_plan(TileNarrow::BM, TileNarrow::BN, M, count, N, K, kTarget, kMinK, 0);
-    return make_plan(TileDecode::BM, TileDecode::BN, M, count, N, K, kTarget, kMinK, 0);
+enum TileKind { kNarrow, kDecode, kWide };
+
+TileKind tile_for(int M) { return M <= 32 ? kNarrow : (M <= 128 ? kDecode : kWide); }
+
+int target_for(int M, bool partial) {
+    if (partial) return M <= 128 ? 512 : 256;
+    return M <= 64 ? 256 : 1;
+}
+
+Plan plan_for(int M, int count, const int* N, const int* K, bool partial) {
+    const int target = target_for(M, partial);
+    switch (tile_for(M)) {
+        case kNarrow: return make_plan(TileNarrow::BM, TileNarrow::BN, M, count, N, K, target, kMinK, 0);
+        case kDecode: return make_plan(TileDecode::BM, TileDecode::BN, M, count, N, K, target, kMinK, 0);
+        default: return make_plan(TileWide::BM, TileWide::BN, M, count, N, K, target, kMinK, 0);
+    }
+}
+
+hipError_t launch_for(int M, int count, const void* const* A, const void* const* B, void* const* C,
+                      const int64_t* lda, const int64_t* ldc, const int* N, const int* K, const int* epi, float* ws,
+                      hipStream_t st, int partial) {
+    const Plan pl = plan_for(M, count, N, K, partial != 0);
+    switch (tile_for(M)) {
+        case kNarrow: return launch_tile<TileNarrow>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl, partial);
+        case kDecode: return launch_tile<TileDecode>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl, partial);
+        default: return launch_tile<TileWide>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl, partial);
+    }
 }
 
 }  // namespace
@@ -506,7 +536,7 @@ Plan plan_for(int M, int count, const int* N, const int* K) {
 int gemm_decode_max_problems() { return kMaxProblems; }
 
 int64_t gemm_decode_workspace(int M, int count, const int* N, const int* K) {
-    return plan_for(M, count, N, K).ws_floats;
+    return plan_for(M, count, N, K, false).ws_floats;
 }
 
 // problems: count entries of {A, packed B, C, lda, ldc, N, K, epi}
@@ -514,26 +544,22 @@ hipError_t launch_gemm_decode(int M, int count, const void* const* A, const void
                               const int64_t* lda, const int64_t* ldc, const int* N, const int* K,
                               const int* epi, float* ws, hipStream_t st)
 {
-    const Plan pl = plan_for(M, count, N, K);
-    if (M <= 32) return launch_tile<TileNarrow>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl);
-    return launch_tile<TileDecode>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl);
+    return launch_for(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, 0);
 }
 
 // One problem, its K-range partial products left as float32 [splits][M][N] rows
 // at the start of ws (no epilogue, no reduction pass; one range when the plan
-// does not split).  Their in-order sum rounded to bf16 is what
-// launch_gemm_decode writes with epi 0.
-int gemm_decode_partial_splits(int M, int N, int K) { return plan_for(M, 1, &N, &K).splits[0]; }
+// does not split).  Their in-order sum rounded to bf16 is the product with
+// epi 0 (launch_gemm_decode may split it differently).
+int gemm_decode_partial_splits(int M, int N, int K) { return plan_for(M, 1, &N, &K, true).splits[0]; }
 
 hipError_t launch_gemm_decode_partials(int M, const void* A, const void* B, int64_t lda, int N, int K, float* ws,
                                        hipStream_t st)
 {
-    const Plan pl = plan_for(M, 1, &N, &K);
     void* C = nullptr;
     const int64_t ldc = N;
     const int epi = 0;
-    if (M <= 32) return launch_tile<TileNarrow>(M, 1, &A, &B, &C, &lda, &ldc, &N, &K, &epi, ws, st, pl, 1);
-    return launch_tile<TileDecode>(M, 1, &A, &B, &C, &lda, &ldc, &N, &K, &epi, ws, st, pl, 1);
+    return launch_for(M, 1, &A, &B, &C, &lda, &ldc, &N, &K, &epi, ws, st, 1);
 }
 
 int64_t gemm_packed_elems(int N, int K) { return (int64_t)((N + 63) / 64) * 64 * ((K + BK - 1) / BK) * BK; }

@@ -109,6 +109,29 @@ def test_gemm_host_side_errors(lib):
     assert lib.rwkv7_gemm_decode_workspace(256, 1, one(2048), one(60)) == -1
 
 
+def test_gemm_scratch_bound(lib):
+    """rwkv7_gemm_decode_noalloc keeps split-K partials in a static scratch of
+    RWKV7_GEMM_SCRATCH_FLOATS floats.  The split plan (a host computation) splits
+    K only at M <= 64 rows, to about 256 blocks of at most 64 x 64 outputs, so no
+    problem set needs more than 510 * 64 * 64 floats: swept here over every
+    column count of one to eight problems on a 32-column grid, row counts 1 .. 64
+    and deep K, and no plan above 64 rows splits at all."""
+    scratch = 1 << 21   # RWKV7_GEMM_SCRATCH_FLOATS in include/rwkv7_hip.h
+    bound = 510 * 64 * 64
+    assert bound <= scratch
+    worst = 0
+    arr = lambda xs: (ctypes.c_int * len(xs))(*xs)
+    for M in list(range(1, 65)) + [65, 96, 128, 200, 256, 1024]:
+        for n in range(32, 16416, 32):
+            for count in (1, 3, 8):
+                need = lib.rwkv7_gemm_decode_workspace(M, count, arr([n] * count), arr([16384] * count))
+                assert need >= 0
+                worst = max(worst, need)
+                if M > 64:
+                    assert need == 0, (M, n, count)
+    assert 0 < worst <= bound
+
+
 def test_partials_host_side_errors(lib):
     P = ctypes.c_void_p
     fake = P(16)

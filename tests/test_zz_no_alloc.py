@@ -1,8 +1,8 @@
 """``rwkv7_gemm_decode_noalloc`` (split-K partials in the library's static
 scratch, no allocation) against ``rwkv7_gemm_decode`` (caller workspace), both
 called through the C ABI: bit-identical outputs on two calls in a row, the
-second with a smaller problem set; a problem set needing more scratch than
-RWKV7_GEMM_SCRATCH_FLOATS is rejected with a clear error and writes nothing.
+second with a smaller problem set.  (That no valid problem set needs more
+scratch than RWKV7_GEMM_SCRATCH_FLOATS is checked on the CPU, test_capi.py.)
 """
 
 import ctypes
@@ -57,11 +57,11 @@ def _no_alloc(M, probs, st):
 
 def test_noalloc_equals_workspace_entry_point(gpu_device):
     dev = gpu_device
-    # call 1: the 1.5B decode step's FFN value (2048 x 8192, split K) at 256
-    # rows with a sigmoid LoRA down (256 x 2048); call 2: a smaller set (64 rows,
-    # a 7.2B-like output projection, split, and a tanh LoRA down)
-    calls = [(256, [(2048, 8192, 0), (256, 2048, 3)], 11),
-             (64, [(4096, 4096, 0), (128, 4096, 2)], 12)]
+    # call 1: the 1.5B decode step's FFN value (2048 x 8192, split K 8 ways) at
+    # 64 rows with a sigmoid LoRA down (256 x 2048, 4 ways); call 2: a smaller set
+    # (32 rows, a 7.2B-like output projection and a tanh LoRA down, 2 ways each)
+    calls = [(64, [(2048, 8192, 0), (256, 2048, 3)], 11),
+             (32, [(4096, 4096, 0), (128, 4096, 2)], 12)]
     for i, (M, shapes, seed) in enumerate(calls):
         print(f"[case] no-alloc call {i + 1}: M={M}, shapes {shapes}", flush=True)
         ref = _problems(dev, M, shapes, seed)
@@ -74,31 +74,3 @@ def test_noalloc_equals_workspace_entry_point(gpu_device):
         for (_, _, c_ref, _), (_, _, c_got, _), shp in zip(ref, got, shapes):
             assert torch.equal(c_ref, c_got), f"call {i + 1}, shape {shp}"
             assert bool(torch.isfinite(c_got.float()).all())
-
-
-def test_noalloc_rejects_oversized_problem_sets(gpu_device):
-    """Find a problem set whose split-K plan needs more floats than the scratch
-    holds (the plan is a host computation), then check the entry point refuses
-    it with its message and leaves C untouched."""
-    print("[case] no-alloc oversize rejection", flush=True)
-    lib = _lib.load()
-    found = None
-    for M in range(512, 1025, 64):
-        for n_cols in (2048, 3072, 4096, 6144):
-            N = (ctypes.c_int * 1)(n_cols)
-            K = (ctypes.c_int * 1)(16384)
-            need = lib.rwkv7_gemm_decode_workspace(M, 1, N, K)
-            if need > SCRATCH_FLOATS:
-                found = (M, n_cols, need)
-                break
-        if found:
-            break
-    assert found is not None, "no oversized plan in the searched range"
-    M, n_cols, need = found
-    dev = gpu_device
-    probs = _problems(dev, M, [(n_cols, 16384, 0)], 13)
-    before = probs[0][2].clone()
-    with pytest.raises(ValueError, match="static scratch"):
-        _no_alloc(M, probs, _lib.stream_of(probs[0][0]))
-    torch.cuda.synchronize()
-    assert torch.equal(probs[0][2], before)
