@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of rwkvtune's batched-generation hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|cfg5|decode|prefill|tmix|logprob|train]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|cfg5|decode|prefill|tmix|gemm|logprob|train]
 
 Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a message.
 
@@ -601,7 +601,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
-    ap.add_argument("--workload", default="rollout", choices=["rollout", "cfg5", "decode", "prefill", "tmix", "logprob", "train"])
+    ap.add_argument("--workload", default="rollout",
+                    choices=["rollout", "cfg5", "decode", "prefill", "tmix", "gemm", "logprob", "train"])
+    ap.add_argument("--rows", type=int, default=256, help="rows of the gemm workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cfg5", action="store_true", help="skip the 7.2B rollout leg of the default workload")
     a = ap.parse_args()
@@ -739,6 +741,25 @@ def main():
             "roofline": {"bound": "hbm", "achieved": tr["bwd_GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
                          "frac": tr["bwd_GBs"] / PEAK_HBM_GBS, "traffic": None, "kernel": tr["kernels"]},
             "cpu_baseline": cpu,
+        }
+    elif a.workload == "gemm":
+        # the decode step's projections alone (for kernel-trace / PMC runs) at --rows
+        # rows over the 1.5B model's 24 layers, then a plain copy of known size
+        from rwkvtune_amd.model import build_model, config_from_preset
+        reps = 10 if a.steps is None else a.steps
+        model = build_model(config_from_preset("rwkv7-1.5b"), dtype=torch.bfloat16, device=dev, seed=1234)
+        gm = gemm_decode_leg(model, dev, M=a.rows, reps=reps)
+        ref = copy_reference(dev)
+        out = {
+            "metric": METRIC, "value": gm["GBs"], "unit": "GB/s of packed weights", "n_gpus": 1, "steps": reps,
+            "warmup": 1, "ms_per_step": gm["us_per_layer"] * 24 / 1e3, "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "bf16 in, fp32 accumulate", "data": "synthetic",
+            "config": {"workload": f"decode projections of RWKV7-1.5B (5 grouped GEMM launches per layer, 24 "
+                                   f"layers in turn) at M={a.rows} rows", "copy_reference_bytes": ref},
+            "roofline": {"bound": "hbm", "achieved": gm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gm["frac"], "traffic": None, "kernel": gm["kernel"],
+                         "us_per_layer": gm["us_per_layer"], "algorithmic_bytes": gm["weight_bytes_per_layer"]},
+            "cpu_baseline": None,
         }
     elif a.workload == "tmix":
         # the roofline kernel alone (for kernel-trace / PMC runs), then a plain copy of
