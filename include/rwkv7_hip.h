@@ -185,7 +185,8 @@ int rwkv7_activation(int dtype, int kind, int64_t n, void *x, void *stream);
  * (w_lora = tanh(xw@w1)@w2, a_lora = (xa@a1)@a2, v_lora = (xv@v1)@v2), write the
  * six WKV operands wkv_ops = {r, w_raw, k', v', -kk, kk*a} ([M, C] each, in the
  * I/O dtype: the reference hands its WKV kernel tensors of the model dtype) and,
- * on layer 0, v_first = v (float32 [M, C]; read on later layers).
+ * on layer 0, v_first = v (float32 [M, C]; read on later layers).  wkv_ops[0]
+ * may be NULL: r is then not copied and the caller hands r itself to the WKV op.
  * Replaces model.py:215-227 and the operand construction of model.py:233-247.
  */
 int rwkv7_tmix_prep(int dtype, int64_t M, int64_t H, int layer0, const void *r, const void *k,

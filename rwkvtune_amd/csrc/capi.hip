@@ -303,7 +303,7 @@ extern "C" int rwkv7_tmix_prep(int dtype, int64_t M, int64_t H, int layer0, cons
     if (!params || !wkv_ops || !params_ok(params) || !r || !k || !v || !w_lora || !a_lora || !v_first)
         return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_prep: null pointer");
     if (!layer0 && (!v_lora || !params[2])) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_prep: layer > 0 needs v_lora and v0");
-    for (int i = 0; i < 6; ++i)
+    for (int i = 1; i < 6; ++i)  // wkv_ops[0] (the copy of r) may be null
         if (!wkv_ops[i]) return fail(RWKV7_ERR_INVALID, "rwkv7_tmix_prep: null output");
     hipError_t e;
     RWKV7_DISPATCH(dtype, (launch_tmix_prep<IO>((int)M, (int)H, layer0, r, k, v, w_lora, a_lora, v_lora,

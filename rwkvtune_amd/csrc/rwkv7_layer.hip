@@ -465,12 +465,110 @@ __global__ __launch_bounds__(kThreads) void tmix_prep_kernel(
     const int ch = h * RWKV7_HEAD + j;
     const size_t off = (size_t)m * C + ch;
     const PrepOut o = tmix_prep_elem(layer0, off, ch, r, k, v, wl, al, vl, vfirst, P);
-    r_op[off] = r[off];
+    if (r_op != nullptr) r_op[off] = r[off];
     w_op[off] = tr::from_f32(o.w_raw);
     k_op[off] = tr::from_f32(o.k);
     v_op[off] = tr::from_f32(o.v);
     a_op[off] = tr::from_f32(o.a_op);
     b_op[off] = tr::from_f32(o.b_op);
+}
+
+// Sum over the 16 lanes of a DPP row, returned in every lane of the row.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_xor1(v);
+    v += dpp_xor2(v);
+    v += dpp_xor7(v);
+    v += dpp_xor15(v);
+    return v;
+}
+
+__device__ __forceinline__ f32x4 ld4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+
+// Prefill prep, four channels per thread with 8-byte (16-bit I/O) or 16-byte
+// (float32) accesses: 16 threads (one DPP row) per head, so the kk norm is a
+// row sum.  The same math as tmix_prep_elem.  n4 = M * C / 4 threads, a
+// multiple of 16; every lane stays active for the row sums.  r_op may be null
+// (r is then not copied).
+template <typename IO>
+__global__ __launch_bounds__(kThreads) void tmix_prep4_kernel(
+    int64_t n4, int C, int layer0, const IO* __restrict__ r, const IO* __restrict__ k,
+    const IO* __restrict__ v, const IO* __restrict__ wl, const IO* __restrict__ al,
+    const IO* __restrict__ vl, float* __restrict__ vfirst, TmixParams P,
+    IO* __restrict__ r_op, IO* __restrict__ w_op, IO* __restrict__ k_op,
+    IO* __restrict__ v_op, IO* __restrict__ a_op, IO* __restrict__ b_op)
+{
+    const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const bool live = q < n4;
+    const int64_t off = (live ? q : 0) * 4;
+    const int ch = (int)(off % C);
+    const f32x4 kj = vec4io<IO>::load(k + off);
+    f32x4 vj = vec4io<IO>::load(v + off);
+    const f32x4 wlj = vec4io<IO>::load(wl + off), alj = vec4io<IO>::load(al + off);
+    const f32x4 w0 = ld4f(P.w0 + ch), a0 = ld4f(P.a0 + ch), kk_w = ld4f(P.k_k + ch), ka = ld4f(P.k_a + ch);
+    f32x4 vf, vlj, v0;
+    if (!layer0) {
+        vf = ld4f(vfirst + off);
+        vlj = vec4io<IO>::load(vl + off);
+        v0 = ld4f(P.v0 + ch);
+    }
+    f32x4 w_raw, aj, kkr;
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        w_raw[e] = -softplusf_(-(w0[e] + wlj[e])) - 0.5f;          // model.py:227
+        if (!layer0) vj[e] = vj[e] + (vf[e] - vj[e]) * sigmoidf_(v0[e] + vlj[e]);  // model.py:215-218
+        aj[e] = sigmoidf_(a0[e] + alj[e]);                           // model.py:220
+        kkr[e] = kj[e] * kk_w[e];                                    // model.py:223
+        ss += kkr[e] * kkr[e];
+    }
+    const float inv = 1.0f / fmaxf(sqrtf(row16_sum(ss)), 1e-12f);  // F.normalize, eps 1e-12
+    if (!live) return;
+    f32x4 kn, na, nb;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const float kk = kkr[e] * inv;
+        kn[e] = kj[e] * (1.0f + (aj[e] - 1.0f) * ka[e]);             // model.py:225
+        na[e] = -kk;                                                 // model.py:246
+        nb[e] = kk * aj[e];
+    }
+    if (layer0) *reinterpret_cast<f32x4*>(vfirst + off) = vj;
+    if (r_op != nullptr) vec4io<IO>::store(r_op + off, vec4io<IO>::load(r + off));
+    vec4io<IO>::store(w_op + off, w_raw);
+    vec4io<IO>::store(k_op + off, kn);
+    vec4io<IO>::store(v_op + off, vj);
+    vec4io<IO>::store(a_op + off, na);
+    vec4io<IO>::store(b_op + off, nb);
+}
+
+// Prefill post, four channels per thread (16 per head): GroupNorm over the
+// head, the bonus, the gate; the same math as tmix_post_kernel.
+template <typename IO>
+__global__ __launch_bounds__(kThreads) void tmix_post4_kernel(
+    int64_t n4, int C, const IO* __restrict__ y, const IO* __restrict__ r_op,
+    const IO* __restrict__ k_op, const IO* __restrict__ v_op, const IO* __restrict__ g,
+    TmixParams P, IO* __restrict__ out)
+{
+    const int64_t q = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    const bool live = q < n4;
+    const int64_t off = (live ? q : 0) * 4;
+    const int ch = (int)(off % C);
+    const f32x4 yj = vec4io<IO>::load(y + off), rj = vec4io<IO>::load(r_op + off);
+    const f32x4 kj = vec4io<IO>::load(k_op + off), vj = vec4io<IO>::load(v_op + off);
+    const f32x4 gj = vec4io<IO>::load(g + off);
+    const f32x4 lw = ld4f(P.lnx_w + ch), lb = ld4f(P.lnx_b + ch), rk = ld4f(P.r_k + ch);
+    const float mean = row16_sum(yj[0] + yj[1] + yj[2] + yj[3]) * (1.0f / 64.0f);
+    const f32x4 d = yj - mean;
+    const float var = row16_sum(d[0] * d[0] + d[1] * d[1] + d[2] * d[2] + d[3] * d[3]) * (1.0f / 64.0f);
+    float bp = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bp += rj[e] * kj[e] * rk[e];
+    const float bonus = row16_sum(bp);
+    if (!live) return;
+    const float is = 1.0f / sqrtf(var + 64e-5f);
+    f32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = ((d[e] * is) * lw[e] + lb[e] + bonus * vj[e]) * gj[e];
+    vec4io<IO>::store(out + off, o);
 }
 
 // Prefill: out = (GroupNorm_H(y) + (sum_j r_j k_j r_k_j) v) * g   (model.py:258-269)
@@ -677,10 +775,25 @@ static TmixParams make_params(const float* const* p) {
 }
 
 template <typename IO>
+bool aligned4(const void* p) { return (((uintptr_t)p) % (4 * sizeof(IO))) == 0; }
+
+template <typename IO>
 hipError_t launch_tmix_prep(int M, int H, int layer0, const void* r, const void* k, const void* v,
                             const void* wl, const void* al, const void* vl, float* vfirst,
                             const float* const* params, void* const* ops, hipStream_t st)
 {
+    bool vec = aligned4<IO>(r) && aligned4<IO>(k) && aligned4<IO>(v) && aligned4<IO>(wl) && aligned4<IO>(al) &&
+               (layer0 || aligned4<IO>(vl)) && aligned4<float>(vfirst);
+    for (int i = 0; i < 6; ++i) vec = vec && aligned4<IO>(ops[i]);
+    for (int i = 0; i < 6; ++i) vec = vec && (params[i] == nullptr || aligned4<float>(params[i]));
+    if (vec) {
+        const int64_t n4 = (int64_t)M * H * (RWKV7_HEAD / 4);
+        hipLaunchKernelGGL(tmix_prep4_kernel<IO>, dim3((unsigned)((n4 + kThreads - 1) / kThreads)), dim3(kThreads),
+                           0, st, n4, H * RWKV7_HEAD, layer0, (const IO*)r, (const IO*)k, (const IO*)v,
+                           (const IO*)wl, (const IO*)al, (const IO*)vl, vfirst, make_params(params), (IO*)ops[0],
+                           (IO*)ops[1], (IO*)ops[2], (IO*)ops[3], (IO*)ops[4], (IO*)ops[5]);
+        return hipGetLastError();
+    }
     dim3 grid(M, (H + kWaves - 1) / kWaves);
     hipLaunchKernelGGL(tmix_prep_kernel<IO>, grid, dim3(kThreads), 0, st, M, H, layer0,
                        (const IO*)r, (const IO*)k, (const IO*)v, (const IO*)wl, (const IO*)al,
@@ -694,6 +807,16 @@ hipError_t launch_tmix_post(int M, int H, const void* y, const void* r_op, const
                             const void* v_op, const void* g, const float* const* params, void* out,
                             hipStream_t st)
 {
+    const bool vec = aligned4<IO>(y) && aligned4<IO>(r_op) && aligned4<IO>(k_op) && aligned4<IO>(v_op) &&
+                     aligned4<IO>(g) && aligned4<IO>(out) && aligned4<float>(params[5]) &&
+                     aligned4<float>(params[6]) && aligned4<float>(params[7]);
+    if (vec) {
+        const int64_t n4 = (int64_t)M * H * (RWKV7_HEAD / 4);
+        hipLaunchKernelGGL(tmix_post4_kernel<IO>, dim3((unsigned)((n4 + kThreads - 1) / kThreads)), dim3(kThreads),
+                           0, st, n4, H * RWKV7_HEAD, (const IO*)y, (const IO*)r_op, (const IO*)k_op,
+                           (const IO*)v_op, (const IO*)g, make_params(params), (IO*)out);
+        return hipGetLastError();
+    }
     dim3 grid(M, (H + kWaves - 1) / kWaves);
     hipLaunchKernelGGL(tmix_post_kernel<IO>, grid, dim3(kThreads), 0, st, M, H, (const IO*)y, (const IO*)r_op,
                        (const IO*)k_op, (const IO*)v_op, (const IO*)g, make_params(params), (IO*)out);

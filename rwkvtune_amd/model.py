@@ -609,8 +609,9 @@ class RWKV7Model(nn.Module):
             # prefill WKV operands and output in the model dtype, as the reference
             # passes them to its WKV kernel (model.py:233-250); bf16 / fp16 models
             # then take the 16-bit chunked matrix-core kernel
-            ops = torch.empty((6, M, C), dtype=dt, device=dev)
-            ops_ptrs = (ctypes.c_void_p * 6)(*[ops[i].data_ptr() for i in range(6)])
+            # w, k', v', -kk, kk*a; r goes to the WKV op as the projection wrote it
+            ops = torch.empty((5, M, C), dtype=dt, device=dev)
+            ops_ptrs = (ctypes.c_void_p * 6)(None, *[ops[i].data_ptr() for i in range(5)])
             y = torch.empty((M, C), dtype=dt, device=dev)
         ffn_out = None
         ffn_parts, ffn_stride = 0, 0  # > 0: ffn_out holds the FFN value's float32 partial planes
@@ -675,8 +676,8 @@ class RWKV7Model(nn.Module):
             else:
                 _lib.call("rwkv7_tmix_prep", code, M, H, int(l == 0), P(r), P(k), P(v), P(wl), P(al),
                           P(vl), P(v_first), pk.tparams, ops_ptrs, st)
-                wkv_ops.wkv7_prefill(kv, seq_slot, cu_seqlens, *ops.unbind(0), y=y)
-                _lib.call("rwkv7_tmix_post", code, M, H, P(y), P(ops[0]), P(ops[2]), P(ops[3]), P(g),
+                wkv_ops.wkv7_prefill(kv, seq_slot, cu_seqlens, r, *ops.unbind(0), y=y)
+                _lib.call("rwkv7_tmix_post", code, M, H, P(y), P(r), P(ops[1]), P(ops[2]), P(g),
                           pk.tparams, P(o), st)
             if grouped and self.use_grouped_output:
                 # the output projection's K-range partials, summed by the next shift_mix
