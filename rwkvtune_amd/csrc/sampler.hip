@@ -181,6 +181,28 @@ __device__ T block_incl_scan(T v, T* wsum) {
     return v + off;
 }
 
+// Inclusive prefix sum over the block in thread order, and the exclusive one
+// bit-identical to the previous thread's inclusive sum (lane 0 takes the wave
+// offset, which is the previous wave's last inclusive sum by commutativity), so
+// the intervals [excl, incl) of consecutive threads tile [0, total) with no gap
+// or overlap in float arithmetic.  `wsum` holds one entry per wave.
+__device__ float block_scan_tiled(float v, float* wsum, float& excl) {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const float n = __shfl_up(v, o, 64);
+        if (lane >= o) v += n;
+    }
+    const float prev = __shfl_up(v, 1, 64);
+    __syncthreads();  // wsum of a previous scan has been read
+    if (lane == 63) wsum[w] = v;
+    __syncthreads();
+    float off = 0.f;
+    for (int i = 0; i < w; ++i) off += wsum[i];
+    excl = lane == 0 ? off : prev + off;
+    return v + off;
+}
+
 // argmax with the lowest index on ties: pack (key, ~index) into 64 bits
 __device__ unsigned long long block_max_u64(unsigned long long v, unsigned long long* red) {
 #pragma unroll
@@ -374,7 +396,11 @@ __global__ __launch_bounds__(kT) void sample_kernel(
 #pragma unroll
     for (int j = 0; j < kVPT; ++j) tm += key[j] >= lo ? __uint_as_float(key[j]) : 0.f;
     if (tid == 0) pick = -1;
-    const float acc = block_incl_scan(tm, fsum);  // [before, acc) of consecutive threads tile [0, total)
+    float before;
+    // [before, acc) of consecutive threads tile [0, total) exactly, so exactly one
+    // thread with kept mass owns the target (a rounded acc - tm could leave a gap
+    // that no thread owns, and the draw unwritten)
+    const float acc = block_scan_tiled(tm, fsum, before);
     // every wave reads fsum[0 .. w-1] at the end of the scan: wait for all of
     // them before fsum[0] is reused for the total
     __syncthreads();
@@ -382,7 +408,6 @@ __global__ __launch_bounds__(kT) void sample_kernel(
     __syncthreads();
     const float total = fsum[0];
     const float target = u * total;
-    const float before = acc - tm;
     if (tm > 0.f && target >= before && (target < acc || acc >= total)) {
         // fully unrolled (no early exit) so key[] stays in registers
         float c = before;
@@ -400,6 +425,20 @@ __global__ __launch_bounds__(kT) void sample_kernel(
         atomicMax(&pick, chosen);
     }
     __syncthreads();
+    if (pick < 0) {
+        // not reached when the intervals tile (the total is finite and > 0 here);
+        // kept as a deterministic guard: the lowest kept id
+        if (tid == 0) pick_bin = 0x7fffffff;
+        __syncthreads();
+        int first = 0x7fffffff;
+#pragma unroll
+        for (int j = 0; j < kVPT; ++j)
+            if (key[j] >= lo) first = min(first, elem_of(j, tid));
+        if (first != 0x7fffffff) atomicMin(&pick_bin, first);
+        __syncthreads();
+        if (tid == 0 && pick_bin != 0x7fffffff) pick = pick_bin;
+        __syncthreads();
+    }
     const int tok = pick;
     if (tok >= 0 && tid == owner_of(tok)) {
         uint32_t kq = 0;
