@@ -30,25 +30,31 @@ train              WKV7 training operator (forward with 16-token checkpoints + b
     backward kernel per second against 8 TB/s.
 decode             isolated WKV7 decode kernel at B=256 slots, H=32 (cfg2); a step is
     one launch; value = algorithmic GB/s.
-tmix               the fused decode time-mix kernel alone at the rollout shape (the
-    roofline kernel of the default line), plus a plain copy of known size; for
-    kernel-trace and PMC runs.
+tmix               the fused decode time-mix kernel alone at the rollout shape, plus a
+    plain copy of known size; for kernel-trace and PMC runs.
+gemm               the decode projections alone (the roofline kernel of the default
+    line) at --rows rows over the 1.5B model's 24 layers, plus a plain copy of
+    known size; for kernel-trace and PMC runs.
 prefill            chunked WKV7 prefill of cfg3 (64 ragged prompts ~U(64, 2048), H=32)
     in one launch; value = prompt tokens/s; roofline = bf16 MFMA rate executed
     (three part products per contraction) against the 2.5 PFLOP/s dense peak.
 
 The default line also carries:
-* ``roofline`` - the fused single-token time-mix (``tmix_decode_kernel``: WKV step +
-  decay/LoRA element-wise + GroupNorm / bonus / gate) at the rollout's shape (256
-  slots, H=32), timed with HIP events on its launch stream, rotating over 24 layer
-  pools (3.2 GB) so no state is served from the 256 MB last-level cache; its
-  ``traffic`` is derived from the committed PMC summary
+* ``roofline`` - the rollout's dominant kernel, the decode GEMM
+  (``gemm_decode_kernel``, about half of the decode kernel time): the five grouped
+  packed-weight launches of a layer at 256 rows over all 24 layers in turn (each
+  layer's weights cold when reached), timed with HIP events on their launch stream;
+  algorithmic bytes = the packed weights (activations are small and L2-resident);
+  ``traffic`` = HBM bytes per launch from the committed PMC summary
+  ``profiles/gemm_decode_m256_pmc.md``;
+* ``roofline_tmix`` - the fused single-token time-mix (``tmix_decode_kernel``: WKV
+  step + decay/LoRA element-wise + GroupNorm / bonus / gate, the second largest) at
+  the rollout's shape (256 slots, H=32), rotating over 24 layer pools (3.2 GB) so no
+  state is served from the 256 MB last-level cache; ``traffic`` from
   ``profiles/tmix_decode_cfg4_shape_pmc.md``;
 * ``roofline_rollout`` - the whole rollout decode step: algorithmic bytes (every
   decode weight once per step + each live row's state read and written) over the
   measured decode time;
-* ``gemm_decode`` - the decode projections (five grouped packed-weight GEMM launches
-  per layer) at 256 rows over all 24 layers in turn: weight bytes / time;
 * ``wkv7_decode_cfg2`` / ``wkv7_prefill_cfg3`` - the stand-alone WKV kernels;
 * ``cfg5_rollout`` - one timed 7.2B rollout (the ``cfg5`` workload) after one warm-up
   (``--no-cfg5`` skips it).
@@ -131,6 +137,22 @@ def pmc_traffic(path=os.path.join(ROOT, "profiles", "tmix_decode_cfg4_shape_pmc.
         return None
     true_kib = int(m.group(1).replace(",", "")) / 1024.0
     return (kern[0] * true_kib / copy[0] + kern[1] * true_kib / copy[1]) * 1024
+
+
+def gemm_pmc_traffic(path=os.path.join(ROOT, "profiles", "gemm_decode_m256_pmc.md")):
+    """HBM bytes per decode-GEMM launch at 256 rows from the committed rocprofv3
+    --pmc summary: its line 'Per layer (five launches): fabric reads R MB, writes
+    W MB' (FETCH_SIZE and WRITE_SIZE, each scaled by the counter's reading for a
+    plain copy of known size), divided by the five launches; or None."""
+    import re
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    m = re.search(r"Per layer \(five launches\): fabric reads ([0-9.]+) MB, writes ([0-9.]+) MB", text)
+    if m is None:
+        return None
+    return (float(m.group(1)) + float(m.group(2))) * 1e6 / 5
 
 
 def copy_reference(dev, n_bytes=256 * 32 * 64 * 64 * 4, reps=8):
@@ -664,11 +686,14 @@ def main():
                        "generated_tokens": ro["tokens"] // steps, "prompt_tokens": sum(len(p) for p in prompts),
                        "decode_steps": ro["runs"][-1]["decode_steps"],
                        "prefill_s": ro["runs"][-1]["prefill_s"], "decode_s": ro["runs"][-1]["decode_s"]},
-            "roofline": {"bound": "hbm", "achieved": tm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": tm["frac"], "traffic": pmc_traffic(), "kernel": tm["kernel"],
-                         "us_per_launch": tm["us_per_launch"], "algorithmic_bytes": tm["bytes_per_launch"]},
+            "roofline": {"bound": "hbm", "achieved": gm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": gm["frac"], "traffic": gemm_pmc_traffic(), "kernel": gm["kernel"],
+                         "M": gm["M"], "us_per_launch": gm["us_per_layer"] / 5,
+                         "algorithmic_bytes": gm["weight_bytes_per_layer"] / 5},
+            "roofline_tmix": {"bound": "hbm", "achieved": tm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                              "frac": tm["frac"], "traffic": pmc_traffic(), "kernel": tm["kernel"],
+                              "us_per_launch": tm["us_per_launch"], "algorithmic_bytes": tm["bytes_per_launch"]},
             "roofline_rollout": rr,
-            "gemm_decode": {k: gm[k] for k in ("M", "us_per_layer", "weight_bytes_per_layer", "GBs", "frac")},
             "cfg5_rollout": c5,
             "wkv7_decode_cfg2": {"GBs": wk["GBs"], "frac": wk["frac"], "us_per_step": wk["us_per_step"]},
             "wkv7_prefill_cfg3": {k: pf[k] for k in ("us_per_launch", "tokens_per_s", "mfma_bf16_TFLOPs",
@@ -757,8 +782,9 @@ def main():
             "config": {"workload": f"decode projections of RWKV7-1.5B (5 grouped GEMM launches per layer, 24 "
                                    f"layers in turn) at M={a.rows} rows", "copy_reference_bytes": ref},
             "roofline": {"bound": "hbm", "achieved": gm["GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": gm["frac"], "traffic": None, "kernel": gm["kernel"],
-                         "us_per_layer": gm["us_per_layer"], "algorithmic_bytes": gm["weight_bytes_per_layer"]},
+                         "frac": gm["frac"], "traffic": gemm_pmc_traffic() if a.rows == 256 else None,
+                         "kernel": gm["kernel"], "M": a.rows, "us_per_launch": gm["us_per_layer"] / 5,
+                         "algorithmic_bytes": gm["weight_bytes_per_layer"] / 5},
             "cpu_baseline": None,
         }
     elif a.workload == "tmix":
