@@ -334,12 +334,17 @@ __global__ __launch_bounds__(256) void wkv7_chunk_kernel(
 // recurrence and the state ~5e-6 relative, well inside the bf16 / fp16 output
 // rounding; the float32 kernel above keeps the three-part split instead.
 //
-// One 256-thread block per (sequence, head), one block per CU (~144 KB of LDS).
+// One 256-thread block per (sequence, head), two blocks per CU for bf16 inputs
+// (~78 KB of LDS each; the float32 state in registers, one 32 x 32 tile per wave).
+// The state update is taken as S' = (S + SA b^ + V^T k^) diag(D_L), which equals
+// the form with bbar and kbar above and lets the transposed planes of k^ and b^
+// reuse the hi/lo words already split for their token-major planes.
 // Per chunk: phase A turns the prefetched inputs into the scaled operand planes
 // (log-decay prefix in registers, one barrier); phase B gives each wave one
-// state product (X^T or Y^T of a value tile) and one intra-chunk matrix; phase C
-// adds V^T A_ak to X; the right-looking triangular solve (quad broadcasts) runs
-// with each wave's state-tile MFMAs interleaved; phase D finishes Y and S.
+// state product (X or Y of a value tile) and one intra-chunk matrix; phase C
+// adds V^T A_ak to X (waves 0/1) and V^T B_rk to Y (waves 2/3); the
+// right-looking triangular solve (quad broadcasts) runs with each wave's
+// state-tile MFMAs interleaved; phase D finishes Y and S.
 //
 // 32x32x16 operand layout: lane l supplies row (l % 32) of A (and of B^T) at
 // k = 8*(l/32) .. +7; accumulator q of lane l is C[8*(q/4) + 4*(l/32) + q%4][l%32].
@@ -352,20 +357,51 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 constexpr int KP = 72;  // bf16 row stride of planes whose K is 64 (144 B)
 constexpr int TQ = 40;  // bf16 row stride of planes whose K is 32 (80 B)
 
+// LDS of the 16-bit kernel, under 80 KB for bf16 inputs so that two blocks share
+// a CU (each SIMD then runs two waves, which hide each other's VALU and LDS
+// latencies and barrier waits).  The float32 state lives in the waves' registers
+// (one 32 x 32 tile per wave); the operand planes of phase A and the products of
+// phase B share one region (the planes are dead once phase B has read them); the
+// planes of S and SA are unpadded with XOR-swizzled 16-byte groups.
+template <bool V_LO>
 struct __attribute__((aligned(16))) ChunkLds2 {
-    uint16_t Rt[2][L][KP], At[2][L][KP], Kh[2][L][KP], Bh[2][L][KP];  // rows t, K = key j
-    uint16_t Sp[2][NH][KP];                                           // rows i, K = j
-    uint16_t VT[2][NH][TQ], BbT[2][NH][TQ], KbT[2][NH][TQ];           // rows i (VT) / j, K = t
-    uint16_t AakT[2][L][TQ], BrbT[2][L][TQ], BrkT[2][L][TQ];          // rows t, K = s
-    uint16_t SA[2][NH][TQ];                                           // rows i, K = t
-    float Sf[NH][SP];   // float32 state [i][j]
-    float X[NH][TP];    // S a~^T + V^T A_ak  [i][t]
-    float AT[L][TP];    // A_ab transposed: [t][s], zero for s >= t
+    union {
+        struct {  // phase A -> B
+            uint16_t Rt[2][L][KP], At[2][L][KP], Kh[2][L][KP], Bh[2][L][KP];  // rows t, K = key j
+        } pa;
+        struct {  // phase B -> D
+            float AT[L][TP];                                          // A_ab^T [t][s], 0 for s >= t
+            uint16_t AakT[2][L][TQ], BrbT[2][L][TQ], BrkT[2][L][TQ];  // rows t, K = s
+            float XT[L][NH];                                          // S a~^T + V^T A_ak, [t][i] (xtswz)
+            uint16_t SA[2][NH][L];                                    // rows i, K = t (saswz)
+        } pb;
+        float Sf[NH][SP];   // float32 state [i][j] while a chunk runs token-serially
+        int lens[256];      // sequence lengths while ranking them
+    } u;
+    uint16_t VT[V_LO ? 2 : 1][NH][TQ], BhT[2][NH][TQ], KhT[2][NH][TQ];  // rows i (VT) / j, K = t (tswz)
+    uint16_t Sp[2][NH][NH];   // state hi / lo planes, rows i, K = j (spswz)
     float tot[4][NH];   // per wave: log2-decay sums over its 8 tokens  [w][j]
     float DL[NH];       // decay over the whole chunk
     alignas(16) int slow[4];  // per wave: a token of the chunk decays below the floor
     int pick;                 // the block's sequence (ragged batches, longest first)
 };
+
+// Swizzled offsets (elements).  A fragment read covers 32 rows x one 16-byte group
+// and a stored accumulator 32 rows x one group; with these layouts any 16
+// consecutive rows of one group fall on 16 distinct 16-byte bank slots of the
+// 256-byte bank space, as the padded strides did.
+// Sp: 64 bf16 per row (8 groups), group ^= row bits 1-3
+__device__ __forceinline__ int spswz(int row, int col) {
+    return row * NH + ((((col >> 3) ^ (row >> 1)) & 7) << 3) + (col & 7);
+}
+// XT: 64 floats per row, columns XOR 8 * (row % 4): the solve's 4-byte reads
+// (8 consecutive columns for each of 4 consecutive rows per half-wave) reach 32
+// distinct banks (measured conflict-free on gfx950; XOR 16 * (row % 4) is not)
+__device__ __forceinline__ int xtswz(int row, int col) { return row * NH + (col ^ ((row & 3) << 3)); }
+// SA: 32 bf16 per row (4 groups), group ^= row bits 2-3
+__device__ __forceinline__ int saswz(int row, int col) {
+    return row * L + ((((col >> 3) ^ (row >> 2)) & 3) << 3) + (col & 7);
+}
 
 __device__ __forceinline__ void split2(float x0, float x1, uint32_t& hi, uint32_t& lo) {
     const f32x2 v = {x0, x1};
@@ -397,12 +433,28 @@ template <> __device__ __forceinline__ f32x4 unpack4<f16_t>(uint2 u) {
     return o;
 }
 
+// 4 consecutive outputs as one 8-byte word, rounded to nearest-even (the
+// hardware conversions)
+template <typename IO> __device__ __forceinline__ uint2 pack4(float x0, float x1, float x2, float x3);
+template <> __device__ __forceinline__ uint2 pack4<bf16_t>(float x0, float x1, float x2, float x3) {
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    const f32x2 p = {x0, x1}, q = {x2, x3};
+    return make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(p, b2)),
+                      __builtin_bit_cast(uint32_t, __builtin_convertvector(q, b2)));
+}
+template <> __device__ __forceinline__ uint2 pack4<f16_t>(float x0, float x1, float x2, float x3) {
+    typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+    const f32x2 p = {x0, x1}, q = {x2, x3};
+    return make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(p, h2)),
+                      __builtin_bit_cast(uint32_t, __builtin_convertvector(q, h2)));
+}
+
 // 8 bf16 of plane row (row0 + l%32) at k0 + 8*(l/32)
 __device__ __forceinline__ bf16x8_t frag(const uint16_t* plane, int stride, int row0, int k0, int lane) {
     return *reinterpret_cast<const bf16x8_t*>(plane + (row0 + (lane & 31)) * stride + k0 + 8 * (lane >> 5));
 }
 
-// Token-major planes ([row][t] with TQ stride: VT, KbT, BbT) keep their 16-byte
+// Token-major planes ([row][t] with TQ stride: VT, KhT, BhT) keep their 16-byte
 // groups of 8 tokens XOR-swizzled by row bits 4-5.  Phase A's transposing stores
 // (a wave writes 4 consecutive words into each of 16 rows 4 apart) then reach 64
 // distinct banks instead of 16; a fragment read covers 16 consecutive rows with
@@ -430,6 +482,17 @@ __device__ __forceinline__ f32x16 mfma_v(f32x16 acc, bf16x8_t a0, bf16x8_t a1, b
     }
 }
 
+// mfma3 with an A operand that has no lo part when V_HI_ONLY
+template <bool V_HI_ONLY>
+__device__ __forceinline__ f32x16 mfma_av(f32x16 acc, bf16x8_t a0, bf16x8_t a1, bf16x8_t b0, bf16x8_t b1) {
+    if constexpr (V_HI_ONLY) {
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1, acc, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0, acc, 0, 0, 0);
+    } else {
+        return mfma3(acc, a0, a1, b0, b1);
+    }
+}
+
 // Store accumulator C (= M^T of the stored matrix M) as hi/lo planes of M:
 // lane l holds M[l%32][8g + 4*(l/32) + 0..3] in acc[4g .. 4g+3].
 __device__ __forceinline__ void store_planes_T(uint16_t* P, int stride, int plane, int row0, int col0,
@@ -445,7 +508,29 @@ __device__ __forceinline__ void store_planes_T(uint16_t* P, int stride, int plan
     }
 }
 
-constexpr int RT_PLANE = L * KP, S_PLANE = NH * KP, T32_PLANE = L * TQ;
+constexpr int RT_PLANE = L * KP, S_PLANE = NH * NH, T32_PLANE = L * TQ, SA_PLANE = NH * L;
+
+// fragments of the swizzled S and SA planes (row0 + l%32, k0 + 8*(l/32))
+__device__ __forceinline__ bf16x8_t fragSp(const uint16_t* plane, int row0, int k0, int lane) {
+    return *reinterpret_cast<const bf16x8_t*>(plane + spswz(row0 + (lane & 31), k0 + 8 * (lane >> 5)));
+}
+__device__ __forceinline__ bf16x8_t fragSA(const uint16_t* plane, int row0, int k0, int lane) {
+    return *reinterpret_cast<const bf16x8_t*>(plane + saswz(row0 + (lane & 31), k0 + 8 * (lane >> 5)));
+}
+
+// A wave's state tile (rows 32*ir + l%32, columns 32*jt + 8g + 4*(l/32) + 0..3 in
+// acc[4g .. 4g+3]) stored as the hi/lo planes of S
+__device__ __forceinline__ void store_state_planes(uint16_t* Sp, int ir, int jt, const f32x16& acc, int lane) {
+    const int row = 32 * ir + (lane & 31);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        uint2 hi, lo;
+        split4(acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3], hi, lo);
+        const int o = spswz(row, 32 * jt + 8 * g + 4 * (lane >> 5));
+        *reinterpret_cast<uint2*>(Sp + o) = hi;
+        *reinterpret_cast<uint2*>(Sp + S_PLANE + o) = lo;
+    }
+}
 
 // The 16-bit kernel keeps log-decays in base 2, so every exponential is one
 // v_exp_f32 (about 1 ulp for the arguments here, all >= -58).  Their accuracy is
@@ -473,7 +558,7 @@ __device__ __forceinline__ void split1(float x, uint16_t& hi, uint16_t& lo) {
 }
 
 template <typename IO>
-__global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
+__global__ __launch_bounds__(256, (std::is_same<IO, bf16_t>::value ? 2 : 1)) void wkv7_chunk2_kernel(
     int H, int T_uniform, const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_idx, int pool_slots,
     int total_tokens, float* __restrict__ state, const IO* __restrict__ r, const IO* __restrict__ w,
     const IO* __restrict__ k, const IO* __restrict__ v, const IO* __restrict__ a, const IO* __restrict__ b,
@@ -483,7 +568,8 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
     // bf16 inputs are exact as bf16 MFMA operands: V (unscaled) has no lo plane, and
     // the products with V skip their hi.lo term
     constexpr bool kVExact = std::is_same<IO, bf16_t>::value;
-    __shared__ ChunkLds2 sm;
+    constexpr int kVLo = kVExact ? 0 : 1;  // plane of V's lo part (none for bf16)
+    __shared__ ChunkLds2<!kVExact> sm;
     const int unit = blockIdx.x;
     const int h = unit % H;
     const int tid = threadIdx.x;
@@ -493,15 +579,15 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
     // Ragged batches of up to 256 sequences run longest sequence first: block
     // group r takes the r-th longest sequence (ties by index, so every sequence
     // is taken once), and the longest chains of chunks start earliest instead of
-    // stretching the launch's tail.  The lengths are ranked from LDS (the X
-    // buffer, unused until phase C): one length per thread against all nseq, so
-    // at most 256 LDS reads per thread.  Larger batches keep their order (the
-    // ranking would cost more than the tail it shortens).
+    // stretching the launch's tail.  The lengths are ranked from LDS: one length
+    // per thread against all nseq, so at most 256 LDS reads per thread.  Larger
+    // batches keep their order (the ranking would cost more than the tail it
+    // shortens).
     int s = unit / H;
     if (cu_seqlens != nullptr) {
         const int nseq = (int)(gridDim.x / (unsigned)H);
         if (nseq <= 256) {
-            int* lens = reinterpret_cast<int*>(&sm.X[0][0]);
+            int* lens = sm.u.lens;
             for (int c = tid; c < nseq; c += 256) lens[c] = cu_seqlens[c + 1] - cu_seqlens[c];
             __syncthreads();
             for (int c = tid; c < nseq; c += 256) {
@@ -527,35 +613,50 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
     const int C = H * NH;
     float* gS = state + ((size_t)slot * H + h) * (NH * NH);
 
-    // state -> float32 master and hi/lo planes; thread: row i, 16 columns
-    {
-        const int i = tid >> 2, c0 = (tid & 3) * 16;
+    // The float32 state: wave w holds the tile of value rows 32*ir_t .. and keys
+    // 32*jt_t .. (ir_t = w / 2, jt_t = w % 2), lane l row 32*ir_t + l%32 and keys
+    // 32*jt_t + 8g + 4*(l/32) + 0..3 in tile[4g .. 4g+3] (the accumulator layout of
+    // the products that update it); the hi/lo planes in LDS are the MFMA operand.
+    const int ir_t = wave >> 1, jt_t = wave & 1;
+    f32x16 tile;
+    auto tile_io = [&](float* base, int ld, bool store) {
+        const int i = 32 * ir_t + (lane & 31);
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const f32x4 x = *reinterpret_cast<const f32x4*>(gS + i * NH + c0 + 4 * q);
-            *reinterpret_cast<f32x4*>(&sm.Sf[i][c0 + 4 * q]) = x;
-            uint2 hi, lo;
-            split4(x.x, x.y, x.z, x.w, hi, lo);
-            *reinterpret_cast<uint2*>(&sm.Sp[0][i][c0 + 4 * q]) = hi;
-            *reinterpret_cast<uint2*>(&sm.Sp[1][i][c0 + 4 * q]) = lo;
+        for (int g = 0; g < 4; ++g) {
+            f32x4* p = reinterpret_cast<f32x4*>(base + i * ld + 32 * jt_t + 8 * g + 4 * (lane >> 5));
+            if (store) {
+                *p = f32x4{tile[4 * g], tile[4 * g + 1], tile[4 * g + 2], tile[4 * g + 3]};
+            } else {
+                const f32x4 x = *p;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) tile[4 * g + e] = x[e];
+            }
         }
-    }
+    };
+    tile_io(gS, NH, false);
+    store_state_planes(&sm.Sp[0][0][0], ir_t, jt_t, tile, lane);
 
     // phase-A mapping: tokens 2*tp, 2*tp+1 of the chunk, channels 4*c4 .. +3; the 16
     // lanes of a row read one 128-byte token row of the head
     const int tp = tid >> 4, c4 = tid & 15, j0 = 4 * c4;
     uint2 raw[6][2];  // r, w, k, v, a, b of this thread's two tokens (zero past the end)
+    // Buffer loads: one resource per input, based at the chunk's first row of the
+    // head and ending after its last row in the sequence, so each load is one
+    // per-lane offset (the same for all six inputs) and rows past the sequence read
+    // as zero (the hardware range check) without any select.
     auto fetch = [&](int t0c) {
+        const uint32_t bytes = (uint32_t)min(L, te - t0c) * (uint32_t)C * (uint32_t)sizeof(IO);
+        const size_t base = (size_t)t0c * C + h * NH;
+        const IO* src[6] = {r, w, k, v, a, b};
 #pragma unroll
-        for (int e = 0; e < 2; ++e) {
-            const int t = t0c + 2 * tp + e;
-            const bool ok = t < te;
-            const size_t off = (size_t)(ok ? t : tb) * C + h * NH + j0;  // clamped to a valid row
-            const IO* src[6] = {r, w, k, v, a, b};
+        for (int q = 0; q < 6; ++q) {
+            const __amdgpu_buffer_rsrc_t rs =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<IO*>(src[q] + base), 0, (int)bytes, 0x00020000);
 #pragma unroll
-            for (int q = 0; q < 6; ++q) {
-                const uint2 u = *reinterpret_cast<const uint2*>(src[q] + off);
-                raw[q][e] = ok ? u : make_uint2(0u, 0u);
+            for (int e = 0; e < 2; ++e) {
+                const int off = ((2 * tp + e) * C + j0) * (int)sizeof(IO);
+                const auto u = __builtin_amdgcn_raw_buffer_load_b64(rs, off, 0, 0);
+                raw[q][e] = make_uint2((uint32_t)u[0], (uint32_t)u[1]);
             }
         }
     };
@@ -610,7 +711,8 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                 if (tp == 0) *reinterpret_cast<f32x4*>(&sm.DL[j0]) = DLv;
                 const f32x4 ld_before = base + exc;  // log2 D of the token before 2tp
                 const f32x4 ld_first = ld_before + lw[0];
-                f32x4 vv[2], kb[2], bb[2], Dprev;
+                f32x4 vv[2], Dprev;
+                uint2 kw[2][2], bw[2][2];  // hi / lo words of k^ and b^ for the two tokens
 #pragma unroll
                 for (int e = 0; e < 2; ++e) {
                     const int t = 2 * tp + e;
@@ -623,29 +725,31 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                     for (int c = 0; c < 4; ++c) {
                         const float Dt = ex2(ld[c]), iD = ex2(-ld[c]);
                         const float Dtm1 = e == 0 ? ex2(ld_before[c]) : Dprev[c];
-                        const float ratio = DLv[c] * iD;  // D_L / D_t
                         Dprev[c] = Dt;
                         rt[c] = rv[c] * Dt;
                         at[c] = av[c] * Dtm1;
                         kh[c] = kv[c] * iD;
                         bh[c] = bv[c] * iD;
-                        kb[e][c] = kv[c] * ratio;
-                        bb[e][c] = bv[c] * ratio;
                     }
                     uint2 hi, lo;
                     split4(rt.x, rt.y, rt.z, rt.w, hi, lo);
-                    *reinterpret_cast<uint2*>(&sm.Rt[0][t][j0]) = hi;
-                    *reinterpret_cast<uint2*>(&sm.Rt[1][t][j0]) = lo;
+                    *reinterpret_cast<uint2*>(&sm.u.pa.Rt[0][t][j0]) = hi;
+                    *reinterpret_cast<uint2*>(&sm.u.pa.Rt[1][t][j0]) = lo;
                     split4(at.x, at.y, at.z, at.w, hi, lo);
-                    *reinterpret_cast<uint2*>(&sm.At[0][t][j0]) = hi;
-                    *reinterpret_cast<uint2*>(&sm.At[1][t][j0]) = lo;
-                    split4(kh.x, kh.y, kh.z, kh.w, hi, lo);
-                    *reinterpret_cast<uint2*>(&sm.Kh[0][t][j0]) = hi;
-                    *reinterpret_cast<uint2*>(&sm.Kh[1][t][j0]) = lo;
-                    split4(bh.x, bh.y, bh.z, bh.w, hi, lo);
-                    *reinterpret_cast<uint2*>(&sm.Bh[0][t][j0]) = hi;
-                    *reinterpret_cast<uint2*>(&sm.Bh[1][t][j0]) = lo;
+                    *reinterpret_cast<uint2*>(&sm.u.pa.At[0][t][j0]) = hi;
+                    *reinterpret_cast<uint2*>(&sm.u.pa.At[1][t][j0]) = lo;
+                    split4(kh.x, kh.y, kh.z, kh.w, kw[e][0], kw[e][1]);
+                    *reinterpret_cast<uint2*>(&sm.u.pa.Kh[0][t][j0]) = kw[e][0];
+                    *reinterpret_cast<uint2*>(&sm.u.pa.Kh[1][t][j0]) = kw[e][1];
+                    split4(bh.x, bh.y, bh.z, bh.w, bw[e][0], bw[e][1]);
+                    *reinterpret_cast<uint2*>(&sm.u.pa.Bh[0][t][j0]) = bw[e][0];
+                    *reinterpret_cast<uint2*>(&sm.u.pa.Bh[1][t][j0]) = bw[e][1];
                 }
+                // channel c of tokens 2tp, 2tp+1 as one word, from the two tokens' words
+                auto tword = [](const uint2& w0, const uint2& w1, int c) -> uint32_t {
+                    const uint32_t a = c < 2 ? w0.x : w0.y, b = c < 2 ? w1.x : w1.y;
+                    return (c & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+                };
                 // transposed planes: key / value j, tokens 2tp and 2tp+1 in one word
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
@@ -653,36 +757,31 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                     uint32_t hi, lo;
                     if constexpr (kVExact) {
                         // the raw bf16 bits of channel j for tokens 2tp, 2tp+1 (no lo plane)
-                        const uint32_t w0 = c < 2 ? raw[3][0].x : raw[3][0].y;
-                        const uint32_t w1 = c < 2 ? raw[3][1].x : raw[3][1].y;
-                        hi = (c & 1) ? ((w0 >> 16) | (w1 & 0xffff0000u)) : ((w0 & 0xffffu) | (w1 << 16));
-                        *reinterpret_cast<uint32_t*>(&sm.VT[0][0][0] + tswz(j, 2 * tp)) = hi;
+                        *reinterpret_cast<uint32_t*>(&sm.VT[0][0][0] + tswz(j, 2 * tp)) = tword(raw[3][0], raw[3][1], c);
                     } else {
                         split2(vv[0][c], vv[1][c], hi, lo);
                         *reinterpret_cast<uint32_t*>(&sm.VT[0][0][0] + tswz(j, 2 * tp)) = hi;
                         *reinterpret_cast<uint32_t*>(&sm.VT[1][0][0] + tswz(j, 2 * tp)) = lo;
                     }
-                    split2(kb[0][c], kb[1][c], hi, lo);
-                    *reinterpret_cast<uint32_t*>(&sm.KbT[0][0][0] + tswz(j, 2 * tp)) = hi;
-                    *reinterpret_cast<uint32_t*>(&sm.KbT[1][0][0] + tswz(j, 2 * tp)) = lo;
-                    split2(bb[0][c], bb[1][c], hi, lo);
-                    *reinterpret_cast<uint32_t*>(&sm.BbT[0][0][0] + tswz(j, 2 * tp)) = hi;
-                    *reinterpret_cast<uint32_t*>(&sm.BbT[1][0][0] + tswz(j, 2 * tp)) = lo;
+                    *reinterpret_cast<uint32_t*>(&sm.KhT[0][0][0] + tswz(j, 2 * tp)) = tword(kw[0][0], kw[1][0], c);
+                    *reinterpret_cast<uint32_t*>(&sm.KhT[1][0][0] + tswz(j, 2 * tp)) = tword(kw[0][1], kw[1][1], c);
+                    *reinterpret_cast<uint32_t*>(&sm.BhT[0][0][0] + tswz(j, 2 * tp)) = tword(bw[0][0], bw[1][0], c);
+                    *reinterpret_cast<uint32_t*>(&sm.BhT[1][0][0] + tswz(j, 2 * tp)) = tword(bw[0][1], bw[1][1], c);
                 }
             }
         }
-        // the raw registers are free: fetch the next chunk while this one computes
-        if (t0 + L < te) fetch(t0 + L);
         __syncthreads();
 
         if (any_slow) {
-            // ---- exact token-serial update on the float32 master -----------------
+            // ---- exact token-serial update on a float32 copy of the state in LDS ----
+            tile_io(&sm.u.Sf[0][0], SP, true);
+            __syncthreads();
             const int i = tid >> 2, q = tid & 3;
             for (int t = 0; t < n; ++t) {
                 const size_t off = (size_t)(t0 + t) * C + h * NH;
                 float sa = 0.f;
 #pragma unroll
-                for (int c = 0; c < 16; ++c) sa += tr::to_f32(a[off + q * 16 + c]) * sm.Sf[i][q * 16 + c];
+                for (int c = 0; c < 16; ++c) sa += tr::to_f32(a[off + q * 16 + c]) * sm.u.Sf[i][q * 16 + c];
                 sa += __shfl_xor(sa, 1, 64);
                 sa += __shfl_xor(sa, 2, 64);
                 const float vi = tr::to_f32(v[off + i]);
@@ -691,46 +790,42 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                 for (int c = 0; c < 16; ++c) {
                     const int jj = q * 16 + c;
                     const float wd = expf(-expf(tr::to_f32(w[off + jj])));
-                    const float sv = sm.Sf[i][jj] * wd + tr::to_f32(k[off + jj]) * vi + sa * tr::to_f32(b[off + jj]);
-                    sm.Sf[i][jj] = sv;
+                    const float sv = sm.u.Sf[i][jj] * wd + tr::to_f32(k[off + jj]) * vi + sa * tr::to_f32(b[off + jj]);
+                    sm.u.Sf[i][jj] = sv;
                     yi += sv * tr::to_f32(r[off + jj]);
                 }
                 yi += __shfl_xor(yi, 1, 64);
                 yi += __shfl_xor(yi, 2, 64);
                 if (q == 0) y[off + i] = tr::from_f32(yi);
             }
-            // refresh the hi/lo planes of the state (same thread owns the same row)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int jj = q * 16 + 4 * c;
-                const f32x4 x = *reinterpret_cast<const f32x4*>(&sm.Sf[i][jj]);
-                uint2 hi, lo;
-                split4(x.x, x.y, x.z, x.w, hi, lo);
-                *reinterpret_cast<uint2*>(&sm.Sp[0][i][jj]) = hi;
-                *reinterpret_cast<uint2*>(&sm.Sp[1][i][jj]) = lo;
-            }
             __syncthreads();
+            // back to the registers, and the hi/lo planes
+            tile_io(&sm.u.Sf[0][0], SP, false);
+            store_state_planes(&sm.Sp[0][0][0], ir_t, jt_t, tile, lane);
+            if (t0 + L < te) fetch(t0 + L);
+            // the next chunk writes the region that holds Sf after its first barrier
             continue;
         }
 
         // ---- B: two 32x32 tiles per wave, K = 64 over keys, sharing one operand:
-        //   wave 0: X^T (value tile 0) and A_ab,   wave 1: X^T (value tile 1) and A_ak,
-        //   wave 2: Y^T (value tile 0) and B_rb,   wave 3: Y^T (value tile 1) and B_rk,
-        // where X^T[t][i] = a~_t . S_i, Y^T[t][i] = r~_t . S_i, A_ab[s][t] = b^_s . a~_t,
+        //   wave 0: X (value tile 0) and A_ab,   wave 1: X (value tile 1) and A_ak,
+        //   wave 2: Y (value tile 0) and B_rb,   wave 3: Y (value tile 1) and B_rk,
+        // where X[i][t] = S_i . a~_t, Y[i][t] = S_i . r~_t (lane l holds value rows
+        // 32*vt + 8g + 4*(l/32) + 0..3 of token l%32), A_ab[s][t] = b^_s . a~_t,
         // A_ak[s][t] = k^_s . a~_t (s < t), B_rb[s][t] = b^_s . r~_t, B_rk[s][t] = k^_s . r~_t (s <= t)
         const f32x16 zero16 = {0.f};
-        const int vt = wave & 1;                  // value tile of X^T / Y^T
-        f32x16 accXY = zero16;                    // waves 0/1: X^T, waves 2/3: Y^T
+        const int vt = wave & 1;                  // value tile of X / Y
+        f32x16 accXY = zero16;                    // waves 0/1: X, waves 2/3: Y
         {
-            const uint16_t* Q = wave < 2 ? &sm.At[0][0][0] : &sm.Rt[0][0][0];
-            const uint16_t* P = (wave & 1) ? &sm.Kh[0][0][0] : &sm.Bh[0][0][0];
+            const uint16_t* Q = wave < 2 ? &sm.u.pa.At[0][0][0] : &sm.u.pa.Rt[0][0][0];
+            const uint16_t* P = (wave & 1) ? &sm.u.pa.Kh[0][0][0] : &sm.u.pa.Bh[0][0][0];
             f32x16 c1 = zero16;
             for (int k0 = 0; k0 < NH; k0 += 16) {
-                const bf16x8_t s0 = frag(&sm.Sp[0][0][0], KP, 32 * vt, k0, lane);
-                const bf16x8_t s1 = frag(&sm.Sp[1][0][0], KP, 32 * vt, k0, lane);
+                const bf16x8_t s0 = fragSp(&sm.Sp[0][0][0], 32 * vt, k0, lane);
+                const bf16x8_t s1 = fragSp(&sm.Sp[1][0][0], 32 * vt, k0, lane);
                 const bf16x8_t q0 = frag(Q, KP, 0, k0, lane), q1 = frag(Q + RT_PLANE, KP, 0, k0, lane);
                 const bf16x8_t p0 = frag(P, KP, 0, k0, lane), p1 = frag(P + RT_PLANE, KP, 0, k0, lane);
-                accXY = mfma3(accXY, q0, q1, s0, s1);
+                accXY = mfma3(accXY, s0, s1, q0, q1);
                 c1 = mfma3(c1, p0, p1, q0, q1);
             }
             // lane holds [s = 8g + 4(l/32) + e][t = l%32]
@@ -741,31 +836,39 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
                 const bool keep = wave < 2 ? srow < tcol : srow <= tcol;
                 c1[q] = keep ? c1[q] : 0.f;
             }
+            // the products overwrite the planes they were computed from
+            __syncthreads();
             if (wave == 0) {
+                float* AT = &sm.u.pb.AT[0][0];
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
-                    *reinterpret_cast<f32x4*>(&sm.AT[tcol][8 * g + 4 * (lane >> 5)]) =
+                    *reinterpret_cast<f32x4*>(AT + tcol * TP + 8 * g + 4 * (lane >> 5)) =
                         f32x4{c1[4 * g], c1[4 * g + 1], c1[4 * g + 2], c1[4 * g + 3]};
             } else {
-                uint16_t* out = wave == 1 ? &sm.AakT[0][0][0] : wave == 2 ? &sm.BrbT[0][0][0] : &sm.BrkT[0][0][0];
+                uint16_t* out = wave == 1 ? &sm.u.pb.AakT[0][0][0] : wave == 2 ? &sm.u.pb.BrbT[0][0][0]
+                                                                               : &sm.u.pb.BrkT[0][0][0];
                 store_planes_T(out, TQ, T32_PLANE, 0, 0, c1, lane);
             }
         }
         __syncthreads();
 
-        // ---- C: X^T += A_ak^T V (waves 0/1) ---------------------------------------
-        if (wave < 2) {
+        // ---- C: X += V^T A_ak (waves 0/1), stored as X^T; Y += V^T B_rk (waves 2/3) --
+        {
+            const uint16_t* M = wave < 2 ? &sm.u.pb.AakT[0][0][0] : &sm.u.pb.BrkT[0][0][0];
             for (int k0 = 0; k0 < L; k0 += 16) {
-                const bf16x8_t a0 = frag(&sm.AakT[0][0][0], TQ, 0, k0, lane), a1 = frag(&sm.AakT[1][0][0], TQ, 0, k0, lane);
-                const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * wave, k0, lane);
-                const bf16x8_t v1 = kVExact ? v0 : fragT(&sm.VT[1][0][0], 32 * wave, k0, lane);
-                accXY = mfma_v<kVExact>(accXY, a0, a1, v0, v1);
+                const bf16x8_t a0 = frag(M, TQ, 0, k0, lane), a1 = frag(M + T32_PLANE, TQ, 0, k0, lane);
+                const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * vt, k0, lane);
+                const bf16x8_t v1 = kVExact ? v0 : fragT(&sm.VT[kVLo][0][0], 32 * vt, k0, lane);
+                accXY = mfma_av<kVExact>(accXY, v0, v1, a0, a1);
             }
-            // X[i][t]: lane holds i = 32*wave + l%32, t = 8g + 4(l/32) + 0..3
-            const int i = 32 * wave + (lane & 31);
+        }
+        if (wave < 2) {
+            // XT[t][i]: lane holds t = l%32, i = 32*wave + 8g + 4(l/32) + 0..3
+            const int t = lane & 31;
+            float* XT = &sm.u.pb.XT[0][0];
 #pragma unroll
             for (int g = 0; g < 4; ++g)
-                *reinterpret_cast<f32x4*>(&sm.X[i][8 * g + 4 * (lane >> 5)]) =
+                *reinterpret_cast<f32x4*>(XT + xtswz(t, 32 * wave + 8 * g + 4 * (lane >> 5))) =
                     f32x4{accXY[4 * g], accXY[4 * g + 1], accXY[4 * g + 2], accXY[4 * g + 3]};
         }
         __syncthreads();
@@ -777,40 +880,24 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
         // later sums (which start from X); the dependency chain per step is one DPP
         // move and one FMA, the other FMAs fill its gaps.  Operands are read before the chain: the
         // lane's 8 X values up front, the transposed A_ab rows one group of 4 tokens
-        // ahead as 16-byte reads.  Every wave also issues one state tile's start on the
-        // matrix cores (straight-line code in the same block as the solve, so its MFMAs
-        // overlap the chain).
-        // S^T tile (value rows 32*ir.., keys 32*jt..) = (S D_L)^T + kbar^T V; lane holds
-        // S[i = 32*ir + l%32][j = 32*jt + 8g + 4(l/32) + 0..3]; stored to Sf after the solve
-        const int ir_t = wave >> 1, jt_t = wave & 1;
-        f32x16 tile;
-        bf16x8_t tv[2][2], tk[2][2];  // v and kbar fragments of the tile's two k steps (hi, lo)
+        // ahead as 16-byte reads.  Every wave also issues its state tile's k^^T V
+        // products on the matrix cores (straight-line code in the same block as the
+        // solve, so its MFMAs overlap the chain): the tile becomes S + (k^^T V)^T.
+        bf16x8_t tv[2][2], tk[2][2];  // v and k^ fragments of the tile's two k steps (hi, lo)
         {
-            const int ir = ir_t, jt = jt_t;
-            const int i = 32 * ir + (lane & 31);
-            f32x16 acc;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int jo = 32 * jt + 8 * g + 4 * (lane >> 5);
-                const f32x4 sv = *reinterpret_cast<const f32x4*>(&sm.Sf[i][jo]);
-                const f32x4 dv = *reinterpret_cast<const f32x4*>(&sm.DL[jo]);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[4 * g + e] = sv[e] * dv[e];
-            }
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                tv[ks][0] = fragT(&sm.VT[0][0][0], 32 * ir, 16 * ks, lane);
-                tv[ks][1] = kVExact ? tv[ks][0] : fragT(&sm.VT[1][0][0], 32 * ir, 16 * ks, lane);
-                tk[ks][0] = fragT(&sm.KbT[0][0][0], 32 * jt, 16 * ks, lane);
-                tk[ks][1] = fragT(&sm.KbT[1][0][0], 32 * jt, 16 * ks, lane);
+                tv[ks][0] = fragT(&sm.VT[0][0][0], 32 * ir_t, 16 * ks, lane);
+                tv[ks][1] = kVExact ? tv[ks][0] : fragT(&sm.VT[kVLo][0][0], 32 * ir_t, 16 * ks, lane);
+                tk[ks][0] = fragT(&sm.KhT[0][0][0], 32 * jt_t, 16 * ks, lane);
+                tk[ks][1] = fragT(&sm.KhT[1][0][0], 32 * jt_t, 16 * ks, lane);
             }
-            tile = acc;
         }
         // the tile's six MFMAs, one per group of the solve, in mfma3's order per k step
         // (lo.hi, hi.lo, hi.hi); the scheduling barrier keeps each in its group
         auto tile_mfma = [&](int m) {
             const int ks = m / 3, part = m % 3;
-            if (kVExact && part == 1) return;  // hi(kbar) . lo(v) = 0
+            if (kVExact && part == 1) return;  // hi(k^) . lo(v) = 0
             const bf16x8_t a = part == 0 ? tk[ks][1] : tk[ks][0];
             const bf16x8_t b = part == 1 ? tv[ks][1] : tv[ks][0];
             tile = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, tile, 0, 0, 0);
@@ -818,20 +905,22 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
         };
         {
             const int i = tid >> 2, q = tid & 3;
+            const float* XT = &sm.u.pb.XT[0][0];
+            const float* AT = &sm.u.pb.AT[0][0];
             // pq[m]: X[i][4m + q] plus the terms pushed so far; it is SA[i][4m + q] from the
             // step of token 4m + q on (later pushes into it multiply A_ab entries that are 0)
             float pq[8];
 #pragma unroll
-            for (int m = 0; m < 8; ++m) pq[m] = sm.X[i][4 * m + q];
+            for (int m = 0; m < 8; ++m) pq[m] = XT[xtswz(4 * m + q, i)];
             f32x4 av[L / 4], nx[L / 4];  // AT[4m + q][4g .. 4g+3] for m >= g: this group / the next
 #pragma unroll
-            for (int m = 0; m < L / 4; ++m) av[m] = *reinterpret_cast<const f32x4*>(&sm.AT[4 * m + q][0]);
+            for (int m = 0; m < L / 4; ++m) av[m] = *reinterpret_cast<const f32x4*>(AT + (4 * m + q) * TP);
 #pragma unroll
             for (int g = 0; g < L / 4; ++g) {
                 if (g + 1 < L / 4) {
 #pragma unroll
                     for (int m = g + 1; m < L / 4; ++m)
-                        nx[m] = *reinterpret_cast<const f32x4*>(&sm.AT[4 * m + q][4 * (g + 1)]);
+                        nx[m] = *reinterpret_cast<const f32x4*>(AT + (4 * m + q) * TP + 4 * (g + 1));
                 }
                 if (g >= 1 && g <= 6) tile_mfma(g - 1);
 #pragma unroll
@@ -843,86 +932,57 @@ __global__ __launch_bounds__(256) void wkv7_chunk2_kernel(
 #pragma unroll
                 for (int m = g + 1; m < L / 4; ++m) av[m] = nx[m];
             }
+            uint16_t* SA = &sm.u.pb.SA[0][0][0];
 #pragma unroll
-            for (int m = 0; m < 8; ++m) split1(pq[m], sm.SA[0][i][4 * m + q], sm.SA[1][i][4 * m + q]);
-        }
-        {
-            const int i = 32 * ir_t + (lane & 31);
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-                *reinterpret_cast<f32x4*>(&sm.Sf[i][32 * jt_t + 8 * g + 4 * (lane >> 5)]) =
-                    f32x4{tile[4 * g], tile[4 * g + 1], tile[4 * g + 2], tile[4 * g + 3]};
+            for (int m = 0; m < 8; ++m) {
+                const int o = saswz(i, 4 * m + q);
+                split1(pq[m], SA[o], SA[SA_PLANE + o]);
+            }
         }
         __syncthreads();
 
-        // ---- D: S^T += bbar^T SA (waves 0/1, value rows 32*wave..);
-        //         Y^T += B_rb^T SA + B_rk^T V (waves 2/3, value tile wave - 2) -------------
-        if (wave < 2) {
-            const int ir = wave;
-            const int i = 32 * ir + (lane & 31);
-            f32x16 accS0, accS1;  // lane holds S[i][j = 32*jt + 8g + 4(l/32) + 0..3], jt = 0 / 1
+        // ---- D: every wave: its state tile += (b^^T SA)^T, scaled by D_L and stored as the next chunk's
+        //         planes; waves 2/3 also Y += SA B_rb (value tile wave - 2) and store y
+        // the raw registers are free from here to the next phase A: fetch the next chunk
+        if (t0 + L < te) fetch(t0 + L);
+        const uint16_t* SA = &sm.u.pb.SA[0][0][0];
+        for (int k0 = 0; k0 < L; k0 += 16) {
+            const bf16x8_t s0 = fragSA(SA, 32 * ir_t, k0, lane), s1 = fragSA(SA + SA_PLANE, 32 * ir_t, k0, lane);
+            const bf16x8_t b0 = fragT(&sm.BhT[0][0][0], 32 * jt_t, k0, lane);
+            const bf16x8_t b1 = fragT(&sm.BhT[1][0][0], 32 * jt_t, k0, lane);
+            tile = mfma3(tile, b0, b1, s0, s1);
+        }
+        // S' = (S + k^^T V + b^^T SA) diag(D_L)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int jo = 8 * g + 4 * (lane >> 5);
-                const f32x4 s0 = *reinterpret_cast<const f32x4*>(&sm.Sf[i][jo]);
-                const f32x4 s1 = *reinterpret_cast<const f32x4*>(&sm.Sf[i][32 + jo]);
+        for (int g = 0; g < 4; ++g) {
+            const f32x4 dv = *reinterpret_cast<const f32x4*>(&sm.DL[32 * jt_t + 8 * g + 4 * (lane >> 5)]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    accS0[4 * g + e] = s0[e];
-                    accS1[4 * g + e] = s1[e];
-                }
-            }
+            for (int e = 0; e < 4; ++e) tile[4 * g + e] *= dv[e];
+        }
+        store_state_planes(&sm.Sp[0][0][0], ir_t, jt_t, tile, lane);
+        if (wave >= 2) {
             for (int k0 = 0; k0 < L; k0 += 16) {
-                const bf16x8_t s0 = frag(&sm.SA[0][0][0], TQ, 32 * ir, k0, lane);
-                const bf16x8_t s1 = frag(&sm.SA[1][0][0], TQ, 32 * ir, k0, lane);
-                const bf16x8_t b00 = fragT(&sm.BbT[0][0][0], 0, k0, lane), b01 = fragT(&sm.BbT[1][0][0], 0, k0, lane);
-                const bf16x8_t b10 = fragT(&sm.BbT[0][0][0], 32, k0, lane), b11 = fragT(&sm.BbT[1][0][0], 32, k0, lane);
-                accS0 = mfma3(accS0, b00, b01, s0, s1);
-                accS1 = mfma3(accS1, b10, b11, s0, s1);
+                const bf16x8_t p0 = frag(&sm.u.pb.BrbT[0][0][0], TQ, 0, k0, lane);
+                const bf16x8_t p1 = frag(&sm.u.pb.BrbT[1][0][0], TQ, 0, k0, lane);
+                const bf16x8_t s0 = fragSA(SA, 32 * vt, k0, lane), s1 = fragSA(SA + SA_PLANE, 32 * vt, k0, lane);
+                accXY = mfma3(accXY, s0, s1, p0, p1);
             }
+            // y[t0 + l%32][32*vt + 8g + 4(l/32) + 0..3]: one 8-byte store per g
+            const int t = lane & 31;
+            if (t < n) {
+                IO* yr = y + (size_t)(t0 + t) * C + h * NH + 32 * vt + 4 * (lane >> 5);
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int jo = 8 * g + 4 * (lane >> 5);
-                *reinterpret_cast<f32x4*>(&sm.Sf[i][jo]) =
-                    f32x4{accS0[4 * g], accS0[4 * g + 1], accS0[4 * g + 2], accS0[4 * g + 3]};
-                *reinterpret_cast<f32x4*>(&sm.Sf[i][32 + jo]) =
-                    f32x4{accS1[4 * g], accS1[4 * g + 1], accS1[4 * g + 2], accS1[4 * g + 3]};
-            }
-            store_planes_T(&sm.Sp[0][0][0], KP, S_PLANE, 32 * ir, 0, accS0, lane);
-            store_planes_T(&sm.Sp[0][0][0], KP, S_PLANE, 32 * ir, 32, accS1, lane);
-        } else {
-            for (int k0 = 0; k0 < L; k0 += 16) {
-                const bf16x8_t p0 = frag(&sm.BrbT[0][0][0], TQ, 0, k0, lane), p1 = frag(&sm.BrbT[1][0][0], TQ, 0, k0, lane);
-                const bf16x8_t q0 = frag(&sm.BrkT[0][0][0], TQ, 0, k0, lane), q1 = frag(&sm.BrkT[1][0][0], TQ, 0, k0, lane);
-                const bf16x8_t s0 = frag(&sm.SA[0][0][0], TQ, 32 * vt, k0, lane);
-                const bf16x8_t s1 = frag(&sm.SA[1][0][0], TQ, 32 * vt, k0, lane);
-                const bf16x8_t v0 = fragT(&sm.VT[0][0][0], 32 * vt, k0, lane);
-                const bf16x8_t v1 = kVExact ? v0 : fragT(&sm.VT[1][0][0], 32 * vt, k0, lane);
-                accXY = mfma3(accXY, p0, p1, s0, s1);
-                accXY = mfma_v<kVExact>(accXY, q0, q1, v0, v1);
-            }
-            // y[t0 + t][32*vt + l%32], t = 8g + 4(l/32) + e
-            IO* yb = y + (size_t)t0 * C + h * NH + 32 * vt + (lane & 31);
-            if (n == L) {
-#pragma unroll
-                for (int q = 0; q < 16; ++q)
-                    yb[(8 * (q >> 2) + 4 * (lane >> 5) + (q & 3)) * C] = tr::from_f32(accXY[q]);
-            } else {
-#pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const int t = 8 * (q >> 2) + 4 * (lane >> 5) + (q & 3);
-                    if (t < n) yb[t * C] = tr::from_f32(accXY[q]);
-                }
+                for (int g = 0; g < 4; ++g)
+                    *reinterpret_cast<uint2*>(yr + 8 * g) =
+                        pack4<IO>(accXY[4 * g], accXY[4 * g + 1], accXY[4 * g + 2], accXY[4 * g + 3]);
             }
         }
         // No barrier here: the next chunk's first LDS writes (tot, slow) touch nothing
-        // read in phase D, and its barriers precede every other write.
+        // read in phase D, and its barriers precede every other write (the next phase B
+        // reads the state planes written here after two of them).
     }
-    __syncthreads();
-    for (int e = tid; e < NH * NH / 4; e += 256) {
-        const int i = e >> 4, c = (e & 15) * 4;
-        *reinterpret_cast<f32x4*>(gS + i * NH + c) = *reinterpret_cast<const f32x4*>(&sm.Sf[i][c]);
-    }
+    // the final state, straight from the registers
+    tile_io(gS, NH, true);
 }
 
 }  // namespace
