@@ -240,8 +240,8 @@ int rwkv7_gemm_decode(int64_t M, int count, const void *const *A, const void *co
  * RWKV7_GEMM_SCRATCH_FLOATS floats (8 MiB) that every GPU the library runs on
  * holds until the process ends.  Problem sets needing more (see
  * rwkv7_gemm_decode_workspace) return RWKV7_ERR_INVALID; with the library's
- * split plan none does: K is split only at M <= 64 rows, to about 256 blocks of
- * at most 64 x 64 outputs, so a set needs at most 510 * 64 * 64 = 2,088,960
+ * split plan none does: K is split only at M <= 32 rows, to about 256 blocks of
+ * at most 32 x 32 outputs, so a set needs at most 510 * 32 * 32 = 522,240
  * floats.  The check stays for plans that may split more.  The scratch needs no clearing
  * (every range writes all its partials before they are read).  All calls on one
  * GPU share its scratch, so calls that overlap on one GPU (concurrent streams,

@@ -485,16 +485,18 @@ hipError_t launch_tile(int M, int count, const void* const* A, const void* const
 
 // Tiles and K splits by row count, chosen by a sweep of tiles (32 x 32 to
 // 256 x 32, 64 x 64, 128 x 64; 4 to 16 waves) and block targets (1 to 512)
-// over the five launches of a 1.5B decode layer at M = 32 .. 256, cold weights
-// (MI355X):
+// over the five launches of a 1.5B and a 7.2B decode layer at M = 32 .. 256,
+// cold weights (MI355X; the plans compared in one process, interleaved):
 //   * up to 32 rows a 32 x 32 tile (4 K groups): every block only streams
 //     weights, and the narrow tile gives twice the column tiles and half the dead
-//     activation rows; up to 128 rows 64 x 64 (8 waves, two K groups); above,
-//     128 x 64 (8 waves, one K group), which halves the activation re-reads of a
-//     column tile and is 10-25% faster there (87.7 -> 73 us per layer at M = 256);
-//   * results the kernel writes itself (epilogue applied) split K only at
-//     M <= 64, to about 256 blocks: above that the reduction launch costs more
-//     than the split gains;
+//     activation rows; up to 64 rows 64 x 64 (8 waves, two K groups); above,
+//     128 x 64 (8 waves, one K group), which reads each weight tile once up to
+//     128 rows and halves the activation re-reads of a column tile: 10% faster
+//     than 64 x 64 for a 7.2B layer at 80-128 rows (144 -> 128 us at 80), the same
+//     for 1.5B, and 10-25% faster above 128 rows;
+//   * results the kernel writes itself (epilogue applied) split K only up to 32
+//     rows, to about 256 blocks: above that the reduction launch costs more than
+//     the split gains (1.5B layer at 40-64 rows: 86 -> 74-81 us without it);
 //   * partial planes (summed by the next row kernel, no reduction launch)
 //     split to about 512 blocks up to 128 rows and 256 above.
 using TileNarrow = Tile<1, 1, 1, 1, 4, 4>;
@@ -504,11 +506,11 @@ constexpr int kMinK = 512;
 
 enum TileKind { kNarrow, kDecode, kWide };
 
-TileKind tile_for(int M) { return M <= 32 ? kNarrow : (M <= 128 ? kDecode : kWide); }
+TileKind tile_for(int M) { return M <= 32 ? kNarrow : (M <= 64 ? kDecode : kWide); }
 
 int target_for(int M, bool partial) {
     if (partial) return M <= 128 ? 512 : 256;
-    return M <= 64 ? 256 : 1;
+    return M <= 32 ? 256 : 1;
 }
 
 Plan plan_for(int M, int count, const int* N, const int* K, bool partial) {

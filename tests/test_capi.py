@@ -112,12 +112,12 @@ def test_gemm_host_side_errors(lib):
 def test_gemm_scratch_bound(lib):
     """rwkv7_gemm_decode_noalloc keeps split-K partials in a static scratch of
     RWKV7_GEMM_SCRATCH_FLOATS floats.  The split plan (a host computation) splits
-    K only at M <= 64 rows, to about 256 blocks of at most 64 x 64 outputs, so no
-    problem set needs more than 510 * 64 * 64 floats: swept here over every
+    K only at M <= 32 rows, to about 256 blocks of at most 32 x 32 outputs, so no
+    problem set needs more than 510 * 32 * 32 floats: swept here over every
     column count of one to eight problems on a 32-column grid, row counts 1 .. 64
-    and deep K, and no plan above 64 rows splits at all."""
+    and deep K, and no plan above 32 rows splits at all."""
     scratch = 1 << 21   # RWKV7_GEMM_SCRATCH_FLOATS in include/rwkv7_hip.h
-    bound = 510 * 64 * 64
+    bound = 510 * 32 * 32
     assert bound <= scratch
     worst = 0
     arr = lambda xs: (ctypes.c_int * len(xs))(*xs)
@@ -127,7 +127,7 @@ def test_gemm_scratch_bound(lib):
                 need = lib.rwkv7_gemm_decode_workspace(M, count, arr([n] * count), arr([16384] * count))
                 assert need >= 0
                 worst = max(worst, need)
-                if M > 64:
+                if M > 32:
                     assert need == 0, (M, n, count)
     assert 0 < worst <= bound
 

@@ -57,11 +57,11 @@ def _no_alloc(M, probs, st):
 
 def test_noalloc_equals_workspace_entry_point(gpu_device):
     dev = gpu_device
-    # call 1: the 1.5B decode step's FFN value (2048 x 8192, split K 8 ways) at
-    # 64 rows with a sigmoid LoRA down (256 x 2048, 4 ways); call 2: a smaller set
-    # (32 rows, a 7.2B-like output projection and a tanh LoRA down, 2 ways each)
-    calls = [(64, [(2048, 8192, 0), (256, 2048, 3)], 11),
-             (32, [(4096, 4096, 0), (128, 4096, 2)], 12)]
+    # call 1: the 1.5B decode step's FFN value (2048 x 8192) at 32 rows with a
+    # sigmoid LoRA down (256 x 2048), both split K; call 2: a smaller set (16 rows,
+    # a 7.2B-like output projection and a tanh LoRA down)
+    calls = [(32, [(2048, 8192, 0), (256, 2048, 3)], 11),
+             (16, [(4096, 4096, 0), (128, 4096, 2)], 12)]
     for i, (M, shapes, seed) in enumerate(calls):
         print(f"[case] no-alloc call {i + 1}: M={M}, shapes {shapes}", flush=True)
         ref = _problems(dev, M, shapes, seed)
