@@ -118,7 +118,8 @@ extern "C" int rwkv7s_forward(int dtype, int64_t B, int64_t T, int64_t C, int64_
     if (C != H * RWKV7_HEAD)
         return fail(RWKV7_ERR_INVALID, "rwkv7s_forward: C=%lld != H*64 (H=%lld)", (long long)C, (long long)H);
     if (B == 0 || T == 0) return ok();
-    if (B * T > kMaxInt || B * H > kMaxInt || B * T * C > (int64_t)1 << 40)
+    // the token-serial kernel runs four blocks per (sequence, head)
+    if (B * T > kMaxInt || 4 * B * H > kMaxInt || B * T * C > (int64_t)1 << 40)
         return fail(RWKV7_ERR_INVALID, "rwkv7s_forward: problem too large");
     if (any_null(state, r, w, k, v, a, b, y)) return fail(RWKV7_ERR_INVALID, "rwkv7s_forward: null pointer");
     if (misaligned(dtype, state, r, w, k, v, a, b))
@@ -140,7 +141,7 @@ extern "C" int rwkv7_wkv_decode(int dtype, int64_t B, int64_t H, float* state_po
     if (B == 0) return ok();
     if (slot_idx == nullptr && pool_slots < B)
         return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_decode: identity slots need pool_slots >= B");
-    if (B * H > kMaxInt || pool_slots > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_decode: too large");
+    if (4 * B * H > kMaxInt || pool_slots > kMaxInt) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_decode: too large");
     if (any_null(state_pool, r, w, k, v, a, b, y)) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_decode: null pointer");
     if (misaligned(dtype, state_pool, r, w, k, v, a, b))
         return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_decode: inputs must be aligned to 4 elements, the state to 16 bytes");
@@ -162,7 +163,7 @@ extern "C" int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t tot
     if (cu_seqlens == nullptr) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: cu_seqlens is required");
     if (slot_idx == nullptr && pool_slots < nseq)
         return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: identity slots need pool_slots >= nseq");
-    if (nseq * H > kMaxInt || total_tokens > kMaxInt || pool_slots > kMaxInt)
+    if (4 * nseq * H > kMaxInt || total_tokens > kMaxInt || pool_slots > kMaxInt)
         return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: too large");
     if (any_null(state_pool, r, w, k, v, a, b, y)) return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_prefill: null pointer");
     if (misaligned(dtype, state_pool, r, w, k, v, a, b))

@@ -144,41 +144,14 @@ __device__ __forceinline__ float lane_xor32(float x) {
     return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
 }
 
-// Reduce-scatter over the 16 lanes of a DPP row.  Every lane of the row holds
-// 16 partial sums p[0..15]; on return, lane c of the row holds
-// sum over the row's 16 lanes of p[c].  The four butterfly partners
-// (c^15, c^7, c^2, c^1) flip bits 3, 2, 1, 0 of c in turn and together span all
-// 16 lanes; at each stage a lane keeps the half of its remaining values whose
-// index bit equals its own lane bit and sends the other half.
-__device__ __forceinline__ float row16_reduce_scatter(const float (&p)[16], int c) {
-    float q8[8];
-    const bool b3 = (c >> 3) & 1;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        float keep = b3 ? p[8 + k] : p[k];
-        float send = b3 ? p[k] : p[8 + k];
-        q8[k] = keep + dpp_xor15(send);
-    }
-    float q4[4];
-    const bool b2 = (c >> 2) & 1;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        float keep = b2 ? q8[4 + k] : q8[k];
-        float send = b2 ? q8[k] : q8[4 + k];
-        q4[k] = keep + dpp_xor7(send);
-    }
-    float q2[2];
-    const bool b1 = (c >> 1) & 1;
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        float keep = b1 ? q4[2 + k] : q4[k];
-        float send = b1 ? q4[k] : q4[2 + k];
-        q2[k] = keep + dpp_xor2(send);
-    }
-    const bool b0 = c & 1;
-    float keep = b0 ? q2[1] : q2[0];
-    float send = b0 ? q2[0] : q2[1];
-    return keep + dpp_xor1(send);
+// Sum over the 16 lanes of a DPP row, returned in every lane of the row (the
+// partners c^1, c^2, c^7, c^15 double the covered lanes at each step).
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_xor1(v);
+    v += dpp_xor2(v);
+    v += dpp_xor7(v);
+    v += dpp_xor15(v);
+    return v;
 }
 
 __device__ __forceinline__ float fast_dot4(f32x4 a, f32x4 b) {

@@ -473,15 +473,6 @@ __global__ __launch_bounds__(kThreads) void tmix_prep_kernel(
     b_op[off] = tr::from_f32(o.b_op);
 }
 
-// Sum over the 16 lanes of a DPP row, returned in every lane of the row.
-__device__ __forceinline__ float row16_sum(float v) {
-    v += dpp_xor1(v);
-    v += dpp_xor2(v);
-    v += dpp_xor7(v);
-    v += dpp_xor15(v);
-    return v;
-}
-
 __device__ __forceinline__ f32x4 ld4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
 
 // Prefill prep, four channels per thread with 8-byte (16-bit I/O) or 16-byte
@@ -595,15 +586,19 @@ __global__ __launch_bounds__(kThreads) void tmix_post_kernel(
     out[off] = tr::from_f32((yn + bonus * tr::to_f32(v_op[off])) * tr::to_f32(g[off]));
 }
 
-// Decode: one token per row, fused prep + WKV step + post.  One 64-lane wave
-// per block and per (row, head), block index = row * H + head, so consecutive
-// blocks stream consecutive 16 KB states of the pool, and single-wave blocks
-// fill every free wave slot (measured on MI355X: 75% of HBM peak at 256 rows x
-// 32 heads, against 69% for four-wave blocks).  The state of (slot, head) is
-// streamed with the same coalesced layout as the stand-alone decode kernel:
-// lane l = 16g + c holds S[4m+g][4c..4c+3] for m = 0..15.
+// Decode: one token per row, fused prep + WKV step + post.  One 256-thread
+// block per (row, head), block index = row * H + head, so consecutive blocks
+// stream consecutive 16 KB states of the pool.  Wave q owns state rows
+// 16q .. 16q+15 (the contiguous 4 KB [4096q, 4096q+4096) of the head's state):
+// lane l = 16g + c holds S[16q + 4m + g][4c..4c+3] for m = 0..3, streamed with
+// coalesced, non-temporal 128-bit accesses.  Quarter-head waves keep more state
+// loads in flight per CU than one wave per head (57 against 125 VGPRs: eight
+// waves per SIMD instead of four; 74% -> 75-76% of HBM peak at 256 rows x 32
+// heads).  Every wave computes the element-wise prep of the head's 64 channels
+// (lane l = channel l: the rows' dot products need all of them); the GroupNorm
+// over the head's 64 outputs takes the waves' y through LDS and one barrier.
 template <typename IO>
-__global__ __launch_bounds__(64) void tmix_decode_kernel(
+__global__ __launch_bounds__(256) void tmix_decode_kernel(
     int M, int H, int layer0, const IO* __restrict__ r, const IO* __restrict__ k,
     const IO* __restrict__ v, const IO* __restrict__ wl, const IO* __restrict__ al,
     const IO* __restrict__ vl, const IO* __restrict__ g, float* __restrict__ vfirst, TmixParams P,
@@ -611,83 +606,91 @@ __global__ __launch_bounds__(64) void tmix_decode_kernel(
     IO* __restrict__ out)
 {
     typedef io_traits<IO> tr;
-    __shared__ float sh[7][64];
+    __shared__ float sh[4][6][64];  // per wave: r, decay, k', -kk, kk*a, v of the head's channels
+    __shared__ float yh[64];        // y of the head's 64 rows
     const int m = blockIdx.x / H;
     const int h = blockIdx.x - m * H;
-    const int l = threadIdx.x;
+    const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
     const int C = H * RWKV7_HEAD;
     const size_t base = (size_t)m * C + (size_t)h * RWKV7_HEAD;
     int slot = row_slot[m];
     if (slot >= pool_slots) slot = -1;
-    if (slot < 0) {  // no sequence on this row
-        out[base + l] = tr::from_f32(0.f);
+    if (slot < 0) {  // no sequence on this row (the whole block returns)
+        if (wave == 0) out[base + l] = tr::from_f32(0.f);
         return;
     }
     // state loads first, so their latency overlaps the element-wise prep
-    f32x4* sp = reinterpret_cast<f32x4*>(state + ((size_t)slot * H + h) * (RWKV7_HEAD * RWKV7_HEAD));
-    f32x4 S[16];
+    f32x4* sp = reinterpret_cast<f32x4*>(state + ((size_t)slot * H + h) * (RWKV7_HEAD * RWKV7_HEAD)) + 256 * wave;
+    f32x4 S[4];
 #pragma unroll
-    for (int mm = 0; mm < 16; ++mm) S[mm] = stream_load(sp + 64 * mm + l);
+    for (int mm = 0; mm < 4; ++mm) S[mm] = stream_load(sp + 64 * mm + l);
 
-    // element-wise prep, lane l = element l of the head
-    const int chl = h * RWKV7_HEAD + l;
-    const PrepOut o = tmix_prep_elem(layer0, base + l, chl, r, k, v, wl, al, vl, vfirst, P);
-    const float bonus = wave_sum(o.rkr);
-    sh[0][l] = tr::to_f32(r[base + l]);
-    sh[1][l] = expf(-expf(o.w_raw));  // decay (wkv7s.cu:27)
-    sh[2][l] = o.k;
-    sh[3][l] = o.a_op;
-    sh[4][l] = o.b_op;
-    sh[5][(l & 3) * 16 + (l >> 2)] = o.v;  // sh[5][gg*16+mm] = v[4mm+gg]
-    wave_sync();  // single-wave block: a wave barrier orders the LDS exchange
+    // element-wise prep, lane l = channel l of the head (wave 0 records v_first)
+    const size_t off = base + l;
+    const int ch = h * RWKV7_HEAD + l;
+    const float rj = tr::to_f32(r[off]);
+    const float kj = tr::to_f32(k[off]);
+    float vj = tr::to_f32(v[off]);
+    // w = -softplus(-(w0 + w_lin)) - 0.5        (model.py:227)
+    const float w_raw = -softplusf_(-(P.w0[ch] + tr::to_f32(wl[off]))) - 0.5f;
+    // value residual: layer 0 records v_first, later layers mix towards it (model.py:215-218)
+    if (layer0) {
+        if (wave == 0) vfirst[off] = vj;
+    } else {
+        const float mixv = sigmoidf_(P.v0[ch] + tr::to_f32(vl[off]));
+        vj = vj + (vfirst[off] - vj) * mixv;
+    }
+    const float aj = sigmoidf_(P.a0[ch] + tr::to_f32(al[off]));  // model.py:220
+    const float kkr = kj * P.k_k[ch];                              // model.py:223
+    const float kk = kkr / fmaxf(sqrtf(wave_sum(kkr * kkr)), 1e-12f);  // F.normalize, eps 1e-12
+    const float kn = kj * (1.0f + (aj - 1.0f) * P.k_a[ch]);        // model.py:225
+    float* s = &sh[wave][0][0];
+    s[0 * 64 + l] = rj;
+    s[1 * 64 + l] = expf(-expf(w_raw));  // decay (wkv7s.cu:27)
+    s[2 * 64 + l] = kn;
+    s[3 * 64 + l] = -kk;                 // a operand (model.py:246)
+    s[4 * 64 + l] = kk * aj;             // b operand
+    s[5 * 64 + l] = vj;
+    const float rkr = rj * kn * P.r_k[ch];  // bonus term (model.py:267)
+    wave_sync();  // the exchange stays inside the wave
 
-    const int gq = l >> 4;
-    const int c = l & 15;
-    const f32x4 r4 = *reinterpret_cast<const f32x4*>(&sh[0][4 * c]);
-    const f32x4 w4 = *reinterpret_cast<const f32x4*>(&sh[1][4 * c]);
-    const f32x4 k4 = *reinterpret_cast<const f32x4*>(&sh[2][4 * c]);
-    const f32x4 a4 = *reinterpret_cast<const f32x4*>(&sh[3][4 * c]);
-    const f32x4 b4 = *reinterpret_cast<const f32x4*>(&sh[4][4 * c]);
-
-    float p[16];
+    const int gq = l >> 4, c = l & 15;
+    const f32x4 r4 = *reinterpret_cast<const f32x4*>(&s[0 * 64 + 4 * c]);
+    const f32x4 w4 = *reinterpret_cast<const f32x4*>(&s[1 * 64 + 4 * c]);
+    const f32x4 k4 = *reinterpret_cast<const f32x4*>(&s[2 * 64 + 4 * c]);
+    const f32x4 a4 = *reinterpret_cast<const f32x4*>(&s[3 * 64 + 4 * c]);
+    const f32x4 b4 = *reinterpret_cast<const f32x4*>(&s[4 * 64 + 4 * c]);
+    float yq[4];
 #pragma unroll
-    for (int mm = 0; mm < 16; ++mm) p[mm] = fast_dot4(a4, S[mm]);
-    sh[6][gq * 16 + c] = row16_reduce_scatter(p, c);  // sa[4c+gq]
-    wave_sync();
-
-    const f32x4* vq = reinterpret_cast<const f32x4*>(&sh[5][gq * 16]);
-    const f32x4* sq = reinterpret_cast<const f32x4*>(&sh[6][gq * 16]);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const f32x4 vv = vq[q];
-        const f32x4 ss = sq[q];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int mm = 4 * q + e;
-            const float vi = vv[e];
-            const float si = ss[e];
-            f32x4 x = S[mm];
-            x.x = fmaf(si, b4.x, fmaf(k4.x, vi, x.x * w4.x));
-            x.y = fmaf(si, b4.y, fmaf(k4.y, vi, x.y * w4.y));
-            x.z = fmaf(si, b4.z, fmaf(k4.z, vi, x.z * w4.z));
-            x.w = fmaf(si, b4.w, fmaf(k4.w, vi, x.w * w4.w));
-            S[mm] = x;
-            p[mm] = fast_dot4(x, r4);
-        }
+    for (int mm = 0; mm < 4; ++mm) {
+        const int i = 16 * wave + 4 * mm + gq;
+        const float si = row16_sum(fast_dot4(a4, S[mm]));  // sa_i
+        const float vi = s[5 * 64 + i];
+        f32x4 x = S[mm];
+        x.x = fmaf(si, b4.x, fmaf(k4.x, vi, x.x * w4.x));
+        x.y = fmaf(si, b4.y, fmaf(k4.y, vi, x.y * w4.y));
+        x.z = fmaf(si, b4.z, fmaf(k4.z, vi, x.z * w4.z));
+        x.w = fmaf(si, b4.w, fmaf(k4.w, vi, x.w * w4.w));
+        S[mm] = x;
+        yq[mm] = fast_dot4(x, r4);
     }
 #pragma unroll
-    for (int mm = 0; mm < 16; ++mm) stream_store(sp + 64 * mm + l, S[mm]);
-
-    // y of row i = 4c + gq, then GroupNorm over the head, bonus and gate
-    const int i = 4 * c + gq;
-    const float yi = row16_reduce_scatter(p, c);
-    const float mean = wave_sum(yi) * (1.0f / 64.0f);
-    const float d = yi - mean;
+    for (int mm = 0; mm < 4; ++mm) stream_store(sp + 64 * mm + l, S[mm]);
+#pragma unroll
+    for (int mm = 0; mm < 4; ++mm) {
+        const float yi = row16_sum(yq[mm]);
+        if (c == 0) yh[16 * wave + 4 * mm + gq] = yi;
+    }
+    const float bonus = wave_sum(rkr);
+    __syncthreads();
+    if (wave != 0) return;
+    // GroupNorm over the head (lane l = row l), bonus and gate (model.py:262-270)
+    const float yl = yh[l];
+    const float mean = wave_sum(yl) * (1.0f / 64.0f);
+    const float d = yl - mean;
     const float var = wave_sum(d * d) * (1.0f / 64.0f);
-    const int chi = h * RWKV7_HEAD + i;
-    const float yn = d / sqrtf(var + 64e-5f) * P.lnx_w[chi] + P.lnx_b[chi];
-    const float vi = sh[5][(i & 3) * 16 + (i >> 2)];
-    out[base + i] = tr::from_f32((yn + bonus * vi) * tr::to_f32(g[base + i]));
+    const float yn = d / sqrtf(var + 64e-5f) * P.lnx_w[ch] + P.lnx_b[ch];
+    out[off] = tr::from_f32((yn + bonus * vj) * tr::to_f32(g[off]));
 }
 
 }  // namespace
@@ -829,7 +832,7 @@ hipError_t launch_tmix_decode(int M, int H, int layer0, const void* r, const voi
                               float* vfirst, const float* const* params, float* state, int pool_slots,
                               const int32_t* row_slot, void* out, hipStream_t st)
 {
-    hipLaunchKernelGGL(tmix_decode_kernel<IO>, dim3((unsigned)M * (unsigned)H), dim3(64), 0, st, M, H, layer0,
+    hipLaunchKernelGGL(tmix_decode_kernel<IO>, dim3((unsigned)M * (unsigned)H), dim3(256), 0, st, M, H, layer0,
                        (const IO*)r, (const IO*)k, (const IO*)v, (const IO*)wl, (const IO*)al,
                        (const IO*)vl, (const IO*)g, vfirst, make_params(params), state, pool_slots,
                        row_slot, (IO*)out);
