@@ -40,7 +40,6 @@ assignment, slot count or polling cadence.
 from __future__ import annotations
 
 import time
-from dataclasses import dataclass, field
 from typing import Dict, List, Optional, Sequence
 
 import torch
@@ -66,14 +65,53 @@ def seq_keys(seed: int, n: int) -> torch.Tensor:
     return (q * 0x2545F4914F6CDD1D + base) & 0x3FFFFFFFFFFFFFFF
 
 
-@dataclass
 class RolloutResult:
-    tokens: List[List[int]]            # generated ids per sequence
-    logps: List[List[float]]           # sampling log-probabilities per token
-    steps: List[List[int]]             # decode step that produced each token (0 = prefill)
-    n_decode_steps: int
-    timings: Dict[str, float] = field(default_factory=dict)
-    prompt_tokens: int = 0
+    """A run's output: ``ngen[q]`` tokens of sequence q in row q of the host
+    tensors ``tok`` (int32), ``logp`` (float32) and ``step`` (int32, the decode
+    step that produced each token, 0 = prefill), each ``[n, maxlen]``.  The
+    per-sequence lists ``tokens``, ``logps`` and ``steps`` are built on first
+    use, so a caller that needs only the ids pays for no Python lists."""
+
+    def __init__(self, ngen: Sequence[int], tok: Optional[torch.Tensor], logp: Optional[torch.Tensor],
+                 step: Optional[torch.Tensor], n_decode_steps: int, timings: Optional[Dict[str, float]] = None,
+                 prompt_tokens: int = 0):
+        self.ngen = [int(g) for g in ngen]
+        self.tok, self.logp, self.step = tok, logp, step
+        self.n_decode_steps = n_decode_steps
+        self.timings = {} if timings is None else timings
+        self.prompt_tokens = prompt_tokens
+        self._lists = {}
+
+    def _rows(self, name: str, t: Optional[torch.Tensor]) -> list:
+        if name not in self._lists:
+            self._lists[name] = [t[q, :g].tolist() for q, g in enumerate(self.ngen)] if t is not None else []
+        return self._lists[name]
+
+    @property
+    def tokens(self) -> List[List[int]]:
+        """Generated ids per sequence."""
+        return self._rows("tokens", self.tok)
+
+    @property
+    def logps(self) -> List[List[float]]:
+        """Sampling log-probabilities per token."""
+        return self._rows("logps", self.logp)
+
+    @property
+    def steps(self) -> List[List[int]]:
+        """Decode step that produced each token (0 = prefill)."""
+        return self._rows("steps", self.step)
+
+    def padded_ids(self):
+        """(ids, mask): int64 ``[n, L]`` ids, zero past each sequence's end, and the
+        bool mask of the generated positions, L = the longest sequence (1 when
+        nothing was generated)."""
+        n, L = len(self.ngen), max(self.ngen, default=0)
+        if L == 0 or self.tok is None:
+            ids = torch.zeros((n, 1), dtype=torch.long)
+            return ids, torch.zeros_like(ids, dtype=torch.bool)
+        mask = torch.arange(L)[None, :] < torch.tensor(self.ngen)[:, None]
+        return self.tok[:, :L].long().masked_fill_(~mask, 0), mask
 
 
 def _i32(x, dev):
@@ -193,7 +231,7 @@ class RolloutEngine:
         else:
             max_new = [int(x) for x in max_new_tokens]
         if n == 0:
-            return RolloutResult([], [], [], 0)
+            return RolloutResult([], None, None, None, 0)
         if min(max_new) < 1:
             raise ValueError("max_new_tokens must be >= 1")
         # a sequence whose first token cannot finish it makes at least one decode step
@@ -363,22 +401,20 @@ class RolloutEngine:
         t3 = time.perf_counter()
         timings["decode_s"] = t3 - t2
 
-        # 4. collect
+        # 4. collect: host copies of the output tables (the context's buffers are
+        # reused by the next run); the per-sequence lists are built on demand
         ng = c.seq_ngen.cpu().tolist()
         ot = c.out_tok.cpu()
         ol = c.out_lp.cpu()
         os_ = c.out_step.cpu()
         n_dec = int(c.counters[C_STEP].item())
-        toks = [ot[q, :ng[q]].tolist() for q in range(n)]
-        lps = [ol[q, :ng[q]].tolist() for q in range(n)]
-        stp = [os_[q, :ng[q]].tolist() for q in range(n)]
         t4 = time.perf_counter()
         timings["collect_s"] = t4 - t3
         timings["total_s"] = t4 - t0
         timings["decode_steps_issued"] = n_steps
         if key is None:
             self._ctx = None  # uncached: drop its buffers and graphs
-        return RolloutResult(toks, lps, stp, n_dec, timings, prompt_tokens=sum(plen))
+        return RolloutResult(ng, ot, ol, os_, n_dec, timings, prompt_tokens=sum(plen))
 
 
 class _DecodeCtx:

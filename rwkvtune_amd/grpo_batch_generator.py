@@ -107,7 +107,7 @@ class GRPOBatchGenerator:
                       decode_rule=RULE_BATCH, first_can_finish=False, chunk_size=self.chunk_size,
                       max_seqs_per_forward=max(0, self.max_prefill_batch_size), seed=seed)
         wall = time.time() - t0
-        gen = sum(len(t) for t in res.tokens)
+        gen = sum(res.ngen)
         tm = res.timings
         # the reference's own throughput definitions (grpo_batch_generator.py:327-349)
         self.last_stats = {
@@ -120,20 +120,16 @@ class GRPOBatchGenerator:
             print(f"[GRPOBatchGenerator] {total} sequences ({len(uniq)} unique prompts, "
                   f"{res.prompt_tokens} prompt tokens): generated {gen} tokens in {res.n_decode_steps} decode "
                   f"steps; prefill {tm['prefill_s']:.3f}s, decode {tm['decode_s']:.3f}s, total {wall:.3f}s")
-        return self._collect_results(res.tokens)
+        return self._collect_results(res)
 
-    def _collect_results(self, tokens: List[List[int]]) -> Dict[str, Any]:
-        max_len = max((len(t) for t in tokens), default=0)
-        completions = [decode_tokens(self.tokenizer, t) for t in tokens]
-        if max_len == 0:
-            ids = torch.zeros((len(tokens), 1), dtype=torch.long)
+    def _collect_results(self, res) -> Dict[str, Any]:
+        """completions (decoded text), completion_ids ``[total, L]`` (zero past each
+        sequence's end) and masks, as the reference returns them
+        (``grpo_batch_generator.py:680-750``)."""
+        ids, masks = res.padded_ids()
+        if self.tokenizer is None:
+            completions = [""] * len(res.ngen)
         else:
-            ids = torch.zeros((len(tokens), max_len), dtype=torch.long)
-            for i, t in enumerate(tokens):
-                if t:
-                    ids[i, :len(t)] = torch.tensor(t, dtype=torch.long)
-        masks = torch.zeros_like(ids, dtype=torch.bool)
-        for i, t in enumerate(tokens):
-            masks[i, :len(t)] = True
+            completions = [decode_tokens(self.tokenizer, t) for t in res.tokens]
         return {"completions": completions, "completion_ids": ids.to(self.device),
                 "masks": masks.to(self.device)}
