@@ -203,7 +203,7 @@ int rwkv7_tmix_post(int dtype, int64_t M, int64_t H, const void *y, const void *
 
 /* Single-token fused path: rwkv7_tmix_prep + one WKV step on
  * state_pool[row_slot[m]] (float32 [pool_slots, H, 64, 64], in place) +
- * rwkv7_tmix_post, one wave per (row, head).  Rows with a negative slot get
+ * rwkv7_tmix_post, one four-wave block per (row, head).  Rows with a negative slot get
  * out = 0 and touch no state.  Replaces model.py:215-269 for T = 1 together
  * with the decode call of the WKV operator (model.py:229-250 -> wkv7s.cu:5-54). */
 int rwkv7_tmix_decode(int dtype, int64_t M, int64_t H, int layer0, const void *r, const void *k,

@@ -11,8 +11,8 @@
 //   tmix_prep     decay / a / value-residual / kk-normalise / k update: the
 //                 six WKV operands of a prefill chunk     (model.py:215-227, 246-247)
 //   tmix_post     GroupNorm(H) + (r*k*r_k).sum*v bonus + gate   (model.py:258-269)
-//   tmix_decode   single-token fused path: prep + WKV step + post in one wave per
-//                 (row, head), state streamed from the slot pool
+//   tmix_decode   single-token fused path: prep + WKV step + post in one four-wave
+//                 block per (row, head), state streamed from the slot pool
 //   final_norm    residual add + ln_out on selected rows  (model.py:494)
 //
 // All element-wise arithmetic is fp32 (the reference rounds every op to the
