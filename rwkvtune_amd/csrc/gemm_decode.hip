@@ -417,7 +417,6 @@ Plan make_plan(int bm, int bn, int M, int count, const int* N, const int* K, int
     const int want = (int)((target + total - 1) / total);
     for (int i = 0; i < count; ++i) {
         const int n_tiles = (N[i] + bn - 1) / bn;
-        const int64_t nt = (int64_t)mt * n_tiles;
         int si = force_splits > 0 ? force_splits : want;
         if (force_splits <= 0) {
             const int max_by_k = K[i] / min_k;

@@ -43,19 +43,6 @@ __device__ __forceinline__ float wave_sum(float v) {
     return (r0 + r1) + (r2 + r3);
 }
 
-// Sum over the 256-thread block; `red` is kWaves floats of LDS.  Safe to call
-// back to back (the leading barrier protects the previous call's reads).
-__device__ __forceinline__ float block_sum(float v, float* red) {
-    v = wave_sum(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) s += red[i];
-    return s;
-}
-
 template <typename IO>
 struct ResidualSrc {
     const float* x_in;      // [M, C] fp32 residual, or null when tokens/emb are used

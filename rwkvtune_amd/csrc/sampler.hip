@@ -127,7 +127,6 @@ __device__ __forceinline__ float wave_reduce_max(float v) {
 
 struct Red {
     float f[kWMax];
-    unsigned u[kWMax];
 };
 
 __device__ float block_sum_f(float v, Red* red) {
@@ -149,17 +148,6 @@ __device__ float block_max_f(float v, Red* red) {
     float s = -INFINITY;
 #pragma unroll
     for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s = fmaxf(s, red->f[i]);
-    return s;
-}
-
-__device__ unsigned block_sum_u(unsigned v, Red* red) {
-    v = wave_reduce_sum(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red->u[threadIdx.x >> 6] = v;
-    __syncthreads();
-    unsigned s = 0;
-#pragma unroll
-    for (int i = 0; i < (int)(blockDim.x >> 6); ++i) s += red->u[i];
     return s;
 }
 
