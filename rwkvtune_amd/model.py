@@ -355,8 +355,6 @@ class _LayerPack:
         # LoRA pairs zero-padded to a common rank D (padded down-columns give 0,
         # whose activation meets zero up-rows, so padding adds nothing).
         with torch.no_grad():
-            self._set("w_rkv", torch.stack([att.receptance.weight.detach().t(), att.key.weight.detach().t(),
-                                            att.value.weight.detach().t()]).contiguous(), alloc)
             downs = [att.w1, att.a1, att.g1] + ([] if self.layer0 else [att.v1])
             ups = [att.w2, att.a2, att.g2] + ([] if self.layer0 else [att.v2])
             if alloc:
@@ -658,10 +656,14 @@ class RWKV7Model(nn.Module):
                 wl, al, g = up[0], up[1], up[2]
                 vl = up[3] if l > 0 else None
             else:
-                # batched library GEMMs: r/k/v in one, the LoRA downs in one (with
-                # tanh on w and sigmoid on g between), the LoRA ups in one
-                rkv = torch.bmm(mixes[0:3], pk.w_rkv)
-                r, k, v = rkv.unbind(0)
+                # library GEMMs: r / k / v as three products on the [out][in]
+                # weights (faster than one batched product over transposed
+                # copies: 1.33 against 1.52 ms at 69,567 rows of a 1.5B layer), the
+                # LoRA downs in one batched product (with tanh on w and sigmoid on
+                # g between), the LoRA ups in one
+                r = self._lin(xr, att.receptance.weight)
+                k = self._lin(xk, att.key.weight)
+                v = self._lin(xv, att.value.weight)
                 nl = pk.lora_down.shape[0]
                 h = torch.bmm(mixes[3:3 + nl], pk.lora_down)
                 _lib.call("rwkv7_activation", code, 0, h[0].numel(), P(h[0]), st)
