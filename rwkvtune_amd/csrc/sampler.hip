@@ -267,7 +267,6 @@ __global__ __launch_bounds__(kT) void sample_kernel(
     const uint8_t* __restrict__ active, uint64_t seed, const int64_t* __restrict__ rng_key,
     const int32_t* __restrict__ rng_ctr, int64_t* __restrict__ out_tok, float* __restrict__ out_logp)
 {
-    typedef io_traits<LT> tr;
     __shared__ Red red;
     __shared__ unsigned long long bins[kBins];
     __shared__ unsigned long long wsum[kWMax];
