@@ -591,6 +591,7 @@ def cpu_baseline_rollout(model, prompts, paths=256, decode_steps=2):
     t2 = time.perf_counter()
     wall = t2 - t0
     return {"value": generated / wall, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "prefill_tok_s": len(p) / (t1 - t0), "decode_tok_s": paths * decode_steps / (t2 - t1),
             "sample": (f"GRPO rollout sample on the restated reference CPU path (fp32): prefill of one "
                        f"{len(p)}-token prompt ({t1 - t0:.1f} s), fork to {paths} paths, first token + "
                        f"{decode_steps} lockstep decode steps ({t2 - t1:.1f} s); {generated} generated tokens "
@@ -662,7 +663,12 @@ def main():
         if not a.no_cpu_baseline:
             log("[bench] cpu baseline (restated reference rollout, bounded sample) ...")
             cpu = cpu_baseline_rollout(model, prompts)
-            log(f"[bench] cpu: {cpu['sample']}")
+            # the sample's two rates applied to this run's token mix (its prompt and
+            # generated token counts): an estimate of the CPU path on the whole cfg4
+            # job, reported beside the measured sample rate, never as `value`
+            gen, ptok = ro["tokens"] // steps, sum(len(p) for p in prompts)
+            cpu["cfg4_mix_estimate_tok_s"] = gen / (ptok / cpu["prefill_tok_s"] + gen / cpu["decode_tok_s"])
+            log(f"[bench] cpu: {cpu['sample']}; cfg4 mix estimate {cpu['cfg4_mix_estimate_tok_s']:.0f} tok/s")
         c5 = None
         if not a.no_cfg5:
             del model
