@@ -544,7 +544,7 @@ def train_leg(dev, steps, warmup, B=8, T=4096, H=32):
     bgbs = units * TRAIN_BWD_BYTES / (bwd * 1e-3) / 1e9
     return {"fwd_ms": fwd, "bwd_ms": bwd, "tokens_per_s": B * T / ((fwd + bwd) * 1e-3), "fwd_GBs": fgbs,
             "bwd_GBs": bgbs, "B": B, "T": T, "H": H,
-            "kernels": "wkv7_train_fwd_kernel<bf16>, wkv7_train_bwd_kernel<bf16>"}
+            "kernels": "wkv7_chunk2_kernel<bf16, train> (chunked forward), wkv7_train_bwd_kernel<bf16>"}
 
 
 def cpu_baseline_train(T=64, H=32):

@@ -109,7 +109,9 @@ int rwkv7_wkv_prefill(int dtype, int64_t nseq, int64_t H, int64_t total_tokens,
  * [64][64] (row = value index) after every 16th token and after the last one,
  * [B, H, ceil(T/16), 64, 64] (rwkv7_wkv_train_ckpt_floats floats, 16-byte
  * aligned).  s0: initial state [B, H, 64, 64] float32 (NULL: zero); s_out
- * (nullable, may alias s0) receives the final state.
+ * (nullable, may alias s0) receives the final state.  16-bit inputs aligned to
+ * 4 elements run in 32-token chunks on the matrix cores (float32-accumulated
+ * hi / lo bf16 operand parts); float32 or unaligned inputs token by token.
  * backward: from dy and the forward's ckpt and sa, the gradients dr, dw (w.r.t.
  * the raw w), dk, dv, da, db; ds_in (nullable) is the gradient of the final
  * state, ds0 (nullable) receives the initial state's.  The state is stepped

@@ -531,6 +531,10 @@ hipError_t launch_wkv7_train_bwd(int B, int T, int H, const void* r, const void*
                                  const void* a, const void* b, const void* dy, const float* ckpt, const float* sa,
                                  const float* ds_in, void* dr, void* dw, void* dk, void* dv, void* da, void* db,
                                  float* ds0, hipStream_t st);
+template <typename IO>
+hipError_t launch_wkv7_chunk_train(int B, int T, int H, const void* r, const void* w, const void* k, const void* v,
+                                   const void* a, const void* b, void* y, const float* s0, float* s_out, float* ckpt,
+                                   float* sa, hipStream_t stream);
 
 namespace {
 int train_sizes(const char* fn, int64_t B, int64_t T, int64_t H) {
@@ -561,6 +565,17 @@ extern "C" int rwkv7_wkv_train_forward(int dtype, int64_t B, int64_t T, int64_t 
     if (f32_misaligned(ckpt) || f32_misaligned(s0) || f32_misaligned(s_out))
         return fail(RWKV7_ERR_INVALID, "rwkv7_wkv_train_forward: checkpoints and states must be 16-byte aligned");
     hipError_t e;
+    // 16-bit inputs aligned to 4 elements run the chunked kernel (32-token matrix
+    // form on the matrix cores); float32 inputs keep the token-serial kernel
+    if (dtype != RWKV7_DTYPE_F32 && B * T <= kMaxInt && !misaligned(dtype, nullptr, r, w, k, v, a, b)) {
+        if (dtype == RWKV7_DTYPE_F16)
+            e = launch_wkv7_chunk_train<f16_t>((int)B, (int)T, (int)H, r, w, k, v, a, b, y, s0, s_out, ckpt, sa,
+                                               (hipStream_t)stream);
+        else
+            e = launch_wkv7_chunk_train<bf16_t>((int)B, (int)T, (int)H, r, w, k, v, a, b, y, s0, s_out, ckpt, sa,
+                                                (hipStream_t)stream);
+        return launch_status(e, "wkv7_chunk2_kernel (training)");
+    }
     RWKV7_DISPATCH(dtype, (launch_wkv7_train_fwd<IO>((int)B, (int)T, (int)H, r, w, k, v, a, b, y, s0, s_out, ckpt,
                                                      sa, (hipStream_t)stream)));
     return launch_status(e, "wkv7_train_fwd_kernel");

@@ -382,6 +382,7 @@ struct __attribute__((aligned(16))) ChunkLds2 {
     uint16_t Sp[2][NH][NH];   // state hi / lo planes, rows i, K = j (spswz)
     float tot[4][NH];   // per wave: log2-decay sums over its 8 tokens  [w][j]
     float DL[NH];       // decay over the whole chunk
+    float D15[NH];      // decay over the chunk's first 16 tokens (training checkpoints)
     alignas(16) int slow[4];  // per wave: a token of the chunk decays below the floor
     int pick;                 // the block's sequence (ragged batches, longest first)
 };
@@ -557,12 +558,18 @@ __device__ __forceinline__ void split1(float x, uint16_t& hi, uint16_t& lo) {
     lo = (uint16_t)l;
 }
 
-template <typename IO>
+// TRAIN: the training operator's forward over B uniform sequences of T_uniform
+// tokens (cu_seqlens and slot_idx null): the initial state comes from s_init (zero
+// when null) and the final one goes to `state` (skipped when null), and the
+// kernel also writes every token's sa_t = S_{t-1} a_t (float32, [tokens][H][64])
+// and the state after every 16th token of a sequence and after its last one
+// (ckpt [B][H][ceil(T/16)][64][64]), the layout the training backward reads.
+template <typename IO, bool TRAIN = false>
 __global__ __launch_bounds__(256, (std::is_same<IO, bf16_t>::value ? 2 : 1)) void wkv7_chunk2_kernel(
     int H, int T_uniform, const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ slot_idx, int pool_slots,
     int total_tokens, float* __restrict__ state, const IO* __restrict__ r, const IO* __restrict__ w,
     const IO* __restrict__ k, const IO* __restrict__ v, const IO* __restrict__ a, const IO* __restrict__ b,
-    IO* __restrict__ y)
+    IO* __restrict__ y, const float* __restrict__ s_init, float* __restrict__ ckpt, float* __restrict__ sa_out)
 {
     typedef io_traits<IO> tr;
     // bf16 inputs are exact as bf16 MFMA operands: V (unscaled) has no lo plane, and
@@ -611,7 +618,10 @@ __global__ __launch_bounds__(256, (std::is_same<IO, bf16_t>::value ? 2 : 1)) voi
     if (slot < 0 || slot >= pool_slots) return;
 
     const int C = H * NH;
-    float* gS = state + ((size_t)slot * H + h) * (NH * NH);
+    float* gS = state != nullptr ? state + ((size_t)slot * H + h) * (NH * NH) : nullptr;
+    // training checkpoints of this (sequence, head): ceil(T / 16) states of 64 x 64
+    const int nck = TRAIN ? (T_uniform + 15) / 16 : 0;
+    float* gCk = TRAIN ? ckpt + (size_t)(s * H + h) * nck * (NH * NH) : nullptr;
 
     // The float32 state: wave w holds the tile of value rows 32*ir_t .. and keys
     // 32*jt_t .. (ir_t = w / 2, jt_t = w % 2), lane l row 32*ir_t + l%32 and keys
@@ -633,8 +643,23 @@ __global__ __launch_bounds__(256, (std::is_same<IO, bf16_t>::value ? 2 : 1)) voi
             }
         }
     };
-    tile_io(gS, NH, false);
+    if constexpr (TRAIN) {
+        if (s_init != nullptr)
+            tile_io(const_cast<float*>(s_init) + ((size_t)s * H + h) * (NH * NH), NH, false);
+        else
+            tile = f32x16{0.f};
+    } else {
+        tile_io(gS, NH, false);
+    }
     store_state_planes(&sm.Sp[0][0][0], ir_t, jt_t, tile, lane);
+    // a 64 x 64 state in the tiles' layout, one 16-byte store per group
+    auto put_state = [&](float* base, const f32x16& x) {
+        const int i = 32 * ir_t + (lane & 31);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            *reinterpret_cast<f32x4*>(base + i * NH + 32 * jt_t + 8 * g + 4 * (lane >> 5)) =
+                f32x4{x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3]};
+    };
 
     // phase-A mapping: tokens 2*tp, 2*tp+1 of the chunk, channels 4*c4 .. +3; the 16
     // lanes of a row read one 128-byte token row of the head
@@ -664,6 +689,7 @@ __global__ __launch_bounds__(256, (std::is_same<IO, bf16_t>::value ? 2 : 1)) voi
 
     for (int t0 = tb; t0 < te; t0 += L) {
         const int n = min(L, te - t0);
+        [[maybe_unused]] const int ci = (t0 - tb) / L;  // chunk of the sequence: checkpoints 2 ci, 2 ci + 1
         // ---- A1: log2-decays of the thread's two tokens, their prefix over the chunk
         // (pair sums scanned over the wave's 4 lane rows = tokens 8w .. 8w+7 by lane
         // swaps, then the four wave totals through LDS), strong-decay test ---------
@@ -745,6 +771,10 @@ __global__ __launch_bounds__(256, (std::is_same<IO, bf16_t>::value ? 2 : 1)) voi
                     *reinterpret_cast<uint2*>(&sm.u.pa.Bh[0][t][j0]) = bw[e][0];
                     *reinterpret_cast<uint2*>(&sm.u.pa.Bh[1][t][j0]) = bw[e][1];
                 }
+                if constexpr (TRAIN) {
+                    // D after token 15 (decay 1 past the chunk's last token)
+                    if (tp == 7) *reinterpret_cast<f32x4*>(&sm.D15[j0]) = Dprev;
+                }
                 // channel c of tokens 2tp, 2tp+1 as one word, from the two tokens' words
                 auto tword = [](const uint2& w0, const uint2& w1, int c) -> uint32_t {
                     const uint32_t a = c < 2 ? w0.x : w0.y, b = c < 2 ? w1.x : w1.y;
@@ -797,6 +827,14 @@ __global__ __launch_bounds__(256, (std::is_same<IO, bf16_t>::value ? 2 : 1)) voi
                 yi += __shfl_xor(yi, 1, 64);
                 yi += __shfl_xor(yi, 2, 64);
                 if (q == 0) y[off + i] = tr::from_f32(yi);
+                if constexpr (TRAIN) {
+                    if (q == 0) sa_out[off + i] = sa;
+                    if (t == 15 || t == n - 1) {  // checkpoint 2 ci (after token 15) or 2 ci + 1
+                        float* ck = gCk + (size_t)(2 * ci + (t >= 16 ? 1 : 0)) * (NH * NH) + i * NH + q * 16;
+#pragma unroll
+                        for (int c = 0; c < 16; ++c) ck[c] = sm.u.Sf[i][q * 16 + c];
+                    }
+                }
             }
             __syncthreads();
             // back to the registers, and the hi/lo planes
@@ -922,7 +960,9 @@ __global__ __launch_bounds__(256, (std::is_same<IO, bf16_t>::value ? 2 : 1)) voi
                     for (int m = g + 1; m < L / 4; ++m)
                         nx[m] = *reinterpret_cast<const f32x4*>(AT + (4 * m + q) * TP + 4 * (g + 1));
                 }
-                if (g >= 1 && g <= 6) tile_mfma(g - 1);
+                // (TRAIN: only the first 16 tokens' three here; phase D takes the
+                // rest after it has stored the state after token 15)
+                if (g >= 1 && g <= (TRAIN ? 3 : 6)) tile_mfma(g - 1);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float sat = quad_bcast(pq[g], e);  // sa_t, t = 4g + e, from lane e
@@ -938,6 +978,11 @@ __global__ __launch_bounds__(256, (std::is_same<IO, bf16_t>::value ? 2 : 1)) voi
                 const int o = saswz(i, 4 * m + q);
                 split1(pq[m], SA[o], SA[SA_PLANE + o]);
             }
+            if constexpr (TRAIN) {
+#pragma unroll
+                for (int m = 0; m < 8; ++m)
+                    if (4 * m + q < n) sa_out[(size_t)(t0 + 4 * m + q) * C + h * NH + i] = pq[m];
+            }
         }
         __syncthreads();
 
@@ -946,18 +991,38 @@ __global__ __launch_bounds__(256, (std::is_same<IO, bf16_t>::value ? 2 : 1)) voi
         // the raw registers are free from here to the next phase A: fetch the next chunk
         if (t0 + L < te) fetch(t0 + L);
         const uint16_t* SA = &sm.u.pb.SA[0][0][0];
-        for (int k0 = 0; k0 < L; k0 += 16) {
-            const bf16x8_t s0 = fragSA(SA, 32 * ir_t, k0, lane), s1 = fragSA(SA + SA_PLANE, 32 * ir_t, k0, lane);
+        auto d_step = [&](int k0) {  // tokens k0 .. k0 + 15 of b^^T SA
+            const bf16x8_t sa0 = fragSA(SA, 32 * ir_t, k0, lane), sa1 = fragSA(SA + SA_PLANE, 32 * ir_t, k0, lane);
             const bf16x8_t b0 = fragT(&sm.BhT[0][0][0], 32 * jt_t, k0, lane);
             const bf16x8_t b1 = fragT(&sm.BhT[1][0][0], 32 * jt_t, k0, lane);
-            tile = mfma3(tile, b0, b1, s0, s1);
+            tile = mfma3(tile, b0, b1, sa0, sa1);
+        };
+        d_step(0);
+        if constexpr (TRAIN) {
+            // the state after token 15 (or after the chunk's last token when n <= 16, the later
+            // tokens adding nothing): (S + the first 16 tokens' k^^T V + b^^T SA) diag(D_15)
+            f32x16 mid;
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const f32x4 dv = *reinterpret_cast<const f32x4*>(&sm.D15[32 * jt_t + 8 * g + 4 * (lane >> 5)]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) mid[4 * g + e] = tile[4 * g + e] * dv[e];
+            }
+            put_state(gCk + (size_t)(2 * ci) * (NH * NH), mid);
+            tile_mfma(3);
+            tile_mfma(4);
+            tile_mfma(5);
         }
+        d_step(16);
         // S' = (S + k^^T V + b^^T SA) diag(D_L)
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const f32x4 dv = *reinterpret_cast<const f32x4*>(&sm.DL[32 * jt_t + 8 * g + 4 * (lane >> 5)]);
 #pragma unroll
             for (int e = 0; e < 4; ++e) tile[4 * g + e] *= dv[e];
+        }
+        if constexpr (TRAIN) {
+            if (n > 16) put_state(gCk + (size_t)(2 * ci + 1) * (NH * NH), tile);  // after the chunk's last token
         }
         store_state_planes(&sm.Sp[0][0][0], ir_t, jt_t, tile, lane);
         if (wave >= 2) {
@@ -982,7 +1047,7 @@ __global__ __launch_bounds__(256, (std::is_same<IO, bf16_t>::value ? 2 : 1)) voi
         // reads the state planes written here after two of them).
     }
     // the final state, straight from the registers
-    tile_io(gS, NH, true);
+    if (gS != nullptr) tile_io(gS, NH, true);
 }
 
 }  // namespace
@@ -997,10 +1062,26 @@ hipError_t launch_wkv7_chunk(int nseq, int H, int T_uniform, const int32_t* cu_s
                            T_uniform, cu_seqlens, slot_idx, pool_slots, total_tokens, state, (const IO*)r,
                            (const IO*)w, (const IO*)k, (const IO*)v, (const IO*)a, (const IO*)b, (IO*)y);
     } else {
-        hipLaunchKernelGGL(wkv7_chunk2_kernel<IO>, dim3((unsigned)nseq * (unsigned)H), dim3(256), 0, stream, H,
-                           T_uniform, cu_seqlens, slot_idx, pool_slots, total_tokens, state, (const IO*)r,
-                           (const IO*)w, (const IO*)k, (const IO*)v, (const IO*)a, (const IO*)b, (IO*)y);
+        hipLaunchKernelGGL((wkv7_chunk2_kernel<IO, false>), dim3((unsigned)nseq * (unsigned)H), dim3(256), 0, stream,
+                           H, T_uniform, cu_seqlens, slot_idx, pool_slots, total_tokens, state, (const IO*)r,
+                           (const IO*)w, (const IO*)k, (const IO*)v, (const IO*)a, (const IO*)b, (IO*)y, nullptr,
+                           nullptr, nullptr);
     }
+    return hipGetLastError();
+}
+
+// The training operator's forward in chunked form (16-bit I/O): B sequences of T
+// tokens, initial state s0 (zero when null), final state s_out (not written when
+// null), checkpoints and sa as the token-serial training forward writes them.
+template <typename IO>
+hipError_t launch_wkv7_chunk_train(int B, int T, int H, const void* r, const void* w, const void* k, const void* v,
+                                   const void* a, const void* b, void* y, const float* s0, float* s_out, float* ckpt,
+                                   float* sa, hipStream_t stream)
+{
+    static_assert(sizeof(IO) == 2, "16-bit inputs");
+    hipLaunchKernelGGL((wkv7_chunk2_kernel<IO, true>), dim3((unsigned)B * (unsigned)H), dim3(256), 0, stream, H, T,
+                       nullptr, nullptr, B, B * T, s_out, (const IO*)r, (const IO*)w, (const IO*)k, (const IO*)v,
+                       (const IO*)a, (const IO*)b, (IO*)y, s0, ckpt, sa);
     return hipGetLastError();
 }
 
@@ -1013,3 +1094,9 @@ template hipError_t launch_wkv7_chunk<bf16_t>(int, int, int, const int32_t*, con
 template hipError_t launch_wkv7_chunk<f16_t>(int, int, int, const int32_t*, const int32_t*, int, int, float*, const void*,
                                              const void*, const void*, const void*, const void*, const void*, void*,
                                              hipStream_t);
+template hipError_t launch_wkv7_chunk_train<bf16_t>(int, int, int, const void*, const void*, const void*, const void*,
+                                                    const void*, const void*, void*, const float*, float*, float*,
+                                                    float*, hipStream_t);
+template hipError_t launch_wkv7_chunk_train<f16_t>(int, int, int, const void*, const void*, const void*, const void*,
+                                                   const void*, const void*, void*, const float*, float*, float*,
+                                                   float*, hipStream_t);

@@ -39,6 +39,13 @@ def close(got, ref, frac):
     return float((got.double().cpu() - ref).abs().max()) <= frac * float(ref.abs().max()) + 1e-12
 
 
+def y_close(y, ref, dtype):
+    """A 16-bit output: within one ulp of its type + 2e-3 of the largest magnitude."""
+    ref = ref.double().cpu()
+    err = (y.double().cpu() - ref).abs()
+    return bool((err <= torch.finfo(dtype).eps * ref.abs() + 2e-3 * float(ref.abs().max())).all())
+
+
 @pytest.mark.parametrize("T,with_state,lo,hi,tol", [(32, False, -6.0, -2.0, 1e-4), (21, True, -6.0, -2.0, 1e-4),
                                                     (48, True, -3.5, -0.5, 2e-3)])
 def test_train_kernels_fp32(gpu_device, T, with_state, lo, hi, tol):
@@ -184,3 +191,59 @@ def test_train_kernels_fp16(gpu_device):
     assert close(y, y_o, 2e-3) and close(sa, sa_o, 1e-4) and close(ck, ck_o, 1e-4)
     for name, got, ref in zip(("dr", "dw", "dk", "dv", "da", "db"), (dr, dw, dk, dv, da, db), grads_o[:6]):
         assert got.dtype == torch.float16 and close(got, ref, 2e-3), name
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("T,with_state,strong", [(1, False, False), (10, True, False), (16, False, False),
+                                                 (17, True, False), (32, False, False), (45, True, True),
+                                                 (100, False, False), (64, True, True)])
+def test_chunked_training_forward(gpu_device, dtype, T, with_state, strong):
+    """16-bit inputs run the training forward in 32-token chunks on the matrix cores
+    (one chunk = one set of contractions; the state after token 15 of a chunk and
+    after its last token are the checkpoints).  Against the float64 oracle on the
+    rounded inputs: y within one ulp of its type + 2e-3 of max|y|; sa, every
+    checkpoint and the final state within 1e-4 of their largest magnitude.  T = 1,
+    10, 17, 45, 100 end in partial chunks (and 10, 45 in partial 16-token segments);
+    `strong` puts a log-decay below the kernel's matrix-form floor in one chunk,
+    which that chunk then runs token by token."""
+    print(f"[case] chunked training forward {dtype} T={T} state={with_state} strong={strong}", flush=True)
+    B, H = 2, 3
+    xs = inputs(B, T, H, -6.0, -0.5, seed=100 + T)
+    if strong:
+        xs[1][1, min(T - 1, 40), 2, 5] = 1.0  # decay exp(-e) per token, below the floor
+    xs = [x.to(dtype) for x in xs]
+    g = torch.Generator().manual_seed(200 + T)
+    s0 = torch.randn(B, H, 64, 64, generator=g) * 0.1 if with_state else None
+    r, w, k, v, a, b = (x.float() for x in xs)
+    y_o, sa_o, ck_o, S_o = otr.train_forward(r, w, k, v, a, b, s0=s0)
+    rd, wd, kd, vd, ad, bd = (x.to(gpu_device).contiguous() for x in xs)
+    s_out = torch.empty(B, H, 64, 64, device=gpu_device) if with_state else None
+    y, ck, sa = ops._train_forward(wd, rd, kd, vd, ad, bd, s0=None if s0 is None else s0.to(gpu_device),
+                                   s_out=s_out)
+    torch.cuda.synchronize()
+    assert y.dtype == dtype and ck.shape == ck_o.shape
+    assert y_close(y, y_o, dtype)
+    assert close(sa, sa_o, 1e-4) and close(ck, ck_o, 1e-4)
+    if with_state:
+        assert close(s_out, S_o, 1e-4)
+
+
+def test_training_forward_misaligned_inputs_token_serial(gpu_device):
+    """Inputs not aligned to 4 elements take the token-serial forward: same
+    results as the oracle (bf16, T = 21)."""
+    print("[case] training forward misaligned bf16", flush=True)
+    B, T, H = 1, 21, 2
+    xs = [x.bfloat16() for x in inputs(B, T, H, -6.0, -1.0, seed=77)]
+    r, w, k, v, a, b = (x.float() for x in xs)
+    y_o, sa_o, ck_o, _ = otr.train_forward(r, w, k, v, a, b)
+
+    def shifted(x):  # the same values one element past an aligned start
+        buf = torch.empty(x.numel() + 1, dtype=x.dtype, device=gpu_device)
+        buf[1:] = x.reshape(-1).to(gpu_device)
+        return buf[1:].view(x.shape)
+
+    rd, wd, kd, vd, ad, bd = (shifted(x) for x in xs)
+    y, ck, sa = ops._train_forward(wd, rd, kd, vd, ad, bd)
+    torch.cuda.synchronize()
+    assert y_close(y, y_o, torch.bfloat16)
+    assert close(sa, sa_o, 1e-4) and close(ck, ck_o, 1e-4)
