@@ -22,14 +22,16 @@
 // gradient of the final state and returns the initial state's gradient.)
 //
 // Layout (CDNA, not the reference's one-thread-per-row): a 512-thread block per
-// (b, h); thread (i, q) = (tid / 8, tid % 8) holds 8 columns j = 8q .. 8q+7 of
-// row i (forward) or of row i and column i (backward), so a sum over j is 8 FMAs
-// (two chains) and a three-step DPP reduction over the row's 8 lanes; two waves
-// per SIMD hide each other's LDS and reduction latency.  Inputs [B, T, H, 64] in
-// the I/O dtype move through LDS 16 tokens (one checkpoint segment) at a time,
-// double-buffered: the next segment's global loads (12 or 16 per thread, issued
-// together) are in flight while the current one computes, so the memory latency
-// is paid once per segment, not once per token.
+// (b, h) in the forward, two 512-thread halves in the backward (one for row i of
+// the state gradient, one for column i of the state and of its gradient);
+// thread (i, q) = (t / 8, t % 8) of a half holds 8 columns j = 8q .. 8q+7, so a
+// sum over j is 8 FMAs (two chains) and a three-step DPP reduction over the
+// row's 8 lanes, and two (forward) or four (backward) waves per SIMD hide each
+// other's LDS and reduction latency.  Inputs [B, T, H, 64] in the I/O dtype move
+// through LDS 16 tokens (one checkpoint segment) at a time, double-buffered: the
+// next segment's global loads (8 to 16 per thread, issued together) are in
+// flight while the current one computes, so the memory latency is paid once per
+// segment, not once per token.
 #include "common.hpp"
 
 namespace {
@@ -170,8 +172,18 @@ __global__ __launch_bounds__(TH) void wkv7_train_fwd_kernel(
 // ---------------------------------------------------------------------------
 // backward
 // ---------------------------------------------------------------------------
+// The backward runs two 512-thread halves per (sequence, head).  The row half
+// carries dS[i][j] (row i of the state gradient) and produces dv and dsa; the
+// column half carries S[j][i] and dS[j][i] (column i) and produces dr, dw, dk,
+// db and da.  The column half needs every dsa_j of a token, which the row half
+// hands over through LDS behind the token's one barrier; the row half needs
+// nothing from the column half.  Thread (i, q) of a half = (t / 8, t % 8) holds
+// j = 8q .. 8q+7, as in the forward; with both halves a CU runs four waves per
+// SIMD, which hide the row reductions' and the barrier's latency.
+constexpr int TH2 = 2 * TH;
+
 template <typename IO>
-__global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
+__global__ __launch_bounds__(TH2) void wkv7_train_bwd_kernel(
     int T, int H, const IO* __restrict__ r, const IO* __restrict__ w, const IO* __restrict__ k,
     const IO* __restrict__ v, const IO* __restrict__ a, const IO* __restrict__ b, const IO* __restrict__ dy,
     const float* __restrict__ ckpt, const float* __restrict__ sa_in, const float* __restrict__ ds_in,
@@ -188,34 +200,34 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
     const int bh = blockIdx.x;
     const int bb = bh / H, hh = bh - bb * H;
     const int tid = threadIdx.x;
-    const int i = tid / TPR, q = tid % TPR, j0 = JPT * q;
+    const bool col = tid >= TH;  // wave-uniform: waves 8 .. 15
+    const int ht = tid & (TH - 1);
+    const int i = ht / TPR, q = ht % TPR, j0 = JPT * q;
     const int nck = (T + SEG - 1) / SEG;
 
-    float sT[JPT], dS[JPT], dST[JPT];  // S[j][i], dS[i][j], dS[j][i] for j = j0 + jj
+    // row half: dS[i][j]; column half: sT = S[j][i] and dS[j][i], for j = j0 + jj
+    float sT[JPT], dS[JPT];
     if (ds_in != nullptr) {
         const float* p = ds_in + (size_t)bh * NH * NH;
 #pragma unroll
-        for (int jj = 0; jj < JPT; ++jj) {
-            dS[jj] = p[i * NH + j0 + jj];
-            dST[jj] = p[(j0 + jj) * NH + i];
-        }
+        for (int jj = 0; jj < JPT; ++jj) dS[jj] = col ? p[(j0 + jj) * NH + i] : p[i * NH + j0 + jj];
     } else {
 #pragma unroll
-        for (int jj = 0; jj < JPT; ++jj) dS[jj] = dST[jj] = 0.f;
+        for (int jj = 0; jj < JPT; ++jj) dS[jj] = 0.f;
     }
 
-    // staging of a segment: flat element f = tid + TH m (m < NL) is element
+    // staging of a segment: flat element f = tid + TH2 m (m < NL) is element
     // f % 64 of token f / 64 % 16 of input array f / 1024 (r, w, k, v, a, b, dy,
     // sa); w also yields the log-decay and inverse-decay arrays.  Rows past T are
     // loaded clamped and staged as zero inputs with decay 1, which leave the state,
     // its gradient and every carried sum unchanged, so each segment runs all 16
     // tokens without a branch.
-    constexpr int NL = 8 * SEG * NH / TH;
+    constexpr int NL = 8 * SEG * NH / TH2;
     float xr[NL];
     auto fetch = [&](int c) {
 #pragma unroll
         for (int m = 0; m < NL; ++m) {
-            const int f = tid + TH * m, arr = f >> 10, t = c * SEG + ((f >> 6) & (SEG - 1)), e = f & 63;
+            const int f = tid + TH2 * m, arr = f >> 10, t = c * SEG + ((f >> 6) & (SEG - 1)), e = f & 63;
             const size_t idx = (((size_t)bb * T + min(t, T - 1)) * H + hh) * NH + e;
             if (arr == 7) {
                 xr[m] = sa_in[idx];
@@ -226,8 +238,9 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
             }
         }
     };
-    float ckn[JPT];  // S[j][i] after segment c (its checkpoint), loaded one segment ahead
+    float ckn[JPT];  // column half: S[j][i] after segment c (its checkpoint), loaded one segment ahead
     auto fetch_ck = [&](int c) {
+        if (!col) return;
         const float* p = ckpt + ((size_t)bh * nck + c) * NH * NH;
 #pragma unroll
         for (int jj = 0; jj < JPT; ++jj) ckn[jj] = p[(j0 + jj) * NH + i];
@@ -239,7 +252,7 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
         const int buf = c & 1;
 #pragma unroll
         for (int m = 0; m < NL; ++m) {
-            const int f = tid + TH * m, arr = f >> 10, u = (f >> 6) & (SEG - 1), e = f & 63;
+            const int f = tid + TH2 * m, arr = f >> 10, u = (f >> 6) & (SEG - 1), e = f & 63;
             const bool ok = c * SEG + u < T;
             if (arr == 1) {
                 const float lw = ok ? -expf(xr[m]) : 0.f;
@@ -251,14 +264,18 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
                 in[buf][arr][u][e] = ok ? xr[m] : 0.f;
             }
         }
+        if (col) {
 #pragma unroll
-        for (int jj = 0; jj < JPT; ++jj) sT[jj] = ckn[jj];
+            for (int jj = 0; jj < JPT; ++jj) sT[jj] = ckn[jj];
+        }
         __syncthreads();
         if (c > 0) {
             fetch(c - 1);
             fetch_ck(c - 1);
         }
-        float keep[6][SEG / TPR];  // dr, dw, dk, dv, db, da of tokens q + 8m (this lane's row)
+        // tokens q + 8m of the segment (this lane's row): column half dr, dw, dk, db,
+        // da; row half dv in keep[0]
+        float keep[5][SEG / TPR];
 #pragma unroll
         for (int u = SEG - 1; u >= 0; --u) {
             const int par = (SEG - 1 - u) & 1;  // dsa_sh buffer of this token
@@ -270,70 +287,91 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
             const float* bv = in[buf][5][u];
             const float* dyv = in[buf][6][u];
             const float* sav = in[buf][7][u];
-            float g1 = 0.f, g2 = 0.f;  // dr_i
-#pragma unroll
-            for (int jj = 0; jj < JPT; jj += 2) {
-                g1 = fmaf(sT[jj], dyv[j0 + jj], g1);
-                g2 = fmaf(sT[jj + 1], dyv[j0 + jj + 1], g2);
-            }
-            const float g = row_sum(g1 + g2);
-            const float ri = rr[i], ki = kk[i], bi = bv[i], dyi = dyv[i], ai = aa[i], wi = dec[i];
-            const float iwi = in[buf][9][u][i];
-            float gw = 0.f, gk = 0.f, gv = 0.f, gsa = 0.f, gb = 0.f;
-#pragma unroll
-            for (int jj = 0; jj < JPT; ++jj) {
-                const int j = j0 + jj;
-                sT[jj] = (sT[jj] - ki * vv[j] - bi * sav[j]) * iwi;
-                dS[jj] = fmaf(dyi, rr[j], dS[jj]);
-                dST[jj] = fmaf(ri, dyv[j], dST[jj]);
-                gw = fmaf(dST[jj], sT[jj], gw);
-                gk = fmaf(dST[jj], vv[j], gk);
-                gv = fmaf(dS[jj], kk[j], gv);
-                gsa = fmaf(dS[jj], bv[j], gsa);
-                gb = fmaf(dST[jj], sav[j], gb);
-            }
-            gw = row_sum(gw);
-            gk = row_sum(gk);
-            gv = row_sum(gv);
-            gsa = row_sum(gsa);
-            gb = row_sum(gb);
             const int ku = u / TPR;
             const bool mine = q == u % TPR;
-            keep[0][ku] = mine ? g : keep[0][ku];
-            keep[1][ku] = mine ? gw * wi * in[buf][8][u][i] : keep[1][ku];
-            keep[2][ku] = mine ? gk : keep[2][ku];
-            keep[3][ku] = mine ? gv : keep[3][ku];
-            keep[4][ku] = mine ? gb : keep[4][ku];
-            dsa_sh[par][i] = gsa;  // the row's 8 lanes store the same value
+            float gsa = 0.f;
+            if (col) {
+                float g1 = 0.f, g2 = 0.f;  // dr_i
+#pragma unroll
+                for (int jj = 0; jj < JPT; jj += 2) {
+                    g1 = fmaf(sT[jj], dyv[j0 + jj], g1);
+                    g2 = fmaf(sT[jj + 1], dyv[j0 + jj + 1], g2);
+                }
+                const float g = row_sum(g1 + g2);
+                const float ri = rr[i], ki = kk[i], bi = bv[i], wi = dec[i];
+                const float iwi = in[buf][9][u][i];
+                float gw = 0.f, gk = 0.f, gb = 0.f;
+#pragma unroll
+                for (int jj = 0; jj < JPT; ++jj) {
+                    const int j = j0 + jj;
+                    sT[jj] = (sT[jj] - ki * vv[j] - bi * sav[j]) * iwi;
+                    dS[jj] = fmaf(ri, dyv[j], dS[jj]);
+                    gw = fmaf(dS[jj], sT[jj], gw);
+                    gk = fmaf(dS[jj], vv[j], gk);
+                    gb = fmaf(dS[jj], sav[j], gb);
+                }
+                gw = row_sum(gw);
+                gk = row_sum(gk);
+                gb = row_sum(gb);
+                keep[0][ku] = mine ? g : keep[0][ku];
+                keep[1][ku] = mine ? gw * wi * in[buf][8][u][i] : keep[1][ku];
+                keep[2][ku] = mine ? gk : keep[2][ku];
+                keep[3][ku] = mine ? gb : keep[3][ku];
+            } else {
+                const float dyi = dyv[i];
+                float gv = 0.f;
+#pragma unroll
+                for (int jj = 0; jj < JPT; ++jj) {
+                    const int j = j0 + jj;
+                    dS[jj] = fmaf(dyi, rr[j], dS[jj]);
+                    gv = fmaf(dS[jj], kk[j], gv);
+                    gsa = fmaf(dS[jj], bv[j], gsa);
+                }
+                gv = row_sum(gv);
+                gsa = row_sum(gsa);
+                keep[0][ku] = mine ? gv : keep[0][ku];
+                dsa_sh[par][i] = gsa;  // the row's 8 lanes store the same value
+            }
             // one barrier per token: dsa_sh alternates, so the next token's write
             // goes to the other buffer, read by nobody until after this barrier
             __syncthreads();
-            const float* ds = dsa_sh[par];
-            float a1 = 0.f, a2 = 0.f;
+            if (col) {
+                const float* ds = dsa_sh[par];
+                const float ai = aa[i], wi = dec[i];
+                float a1 = 0.f, a2 = 0.f;
 #pragma unroll
-            for (int jj = 0; jj < JPT; jj += 2) {
-                a1 = fmaf(sT[jj], ds[j0 + jj], a1);
-                a2 = fmaf(sT[jj + 1], ds[j0 + jj + 1], a2);
-            }
-            const float ga = row_sum(a1 + a2);
-            keep[5][ku] = mine ? ga : keep[5][ku];
+                for (int jj = 0; jj < JPT; jj += 2) {
+                    a1 = fmaf(sT[jj], ds[j0 + jj], a1);
+                    a2 = fmaf(sT[jj + 1], ds[j0 + jj + 1], a2);
+                }
+                const float ga = row_sum(a1 + a2);
+                keep[4][ku] = mine ? ga : keep[4][ku];
 #pragma unroll
-            for (int jj = 0; jj < JPT; ++jj) {
-                const int j = j0 + jj;
-                dS[jj] = fmaf(dS[jj], dec[j], gsa * aa[j]);
-                dST[jj] = fmaf(dST[jj], wi, ai * ds[j]);
+                for (int jj = 0; jj < JPT; ++jj) dS[jj] = fmaf(dS[jj], wi, ai * ds[j0 + jj]);
+            } else {
+#pragma unroll
+                for (int jj = 0; jj < JPT; ++jj) dS[jj] = fmaf(dS[jj], dec[j0 + jj], gsa * aa[j0 + jj]);
             }
         }
+        if (col) {
 #pragma unroll
-        for (int x = 0; x < 6; ++x)
+            for (int m = 0; m < SEG / TPR; ++m) {
+                gout[0][q + TPR * m][i] = keep[0][m];
+                gout[1][q + TPR * m][i] = keep[1][m];
+                gout[2][q + TPR * m][i] = keep[2][m];
+                gout[4][q + TPR * m][i] = keep[3][m];
+                gout[5][q + TPR * m][i] = keep[4][m];
+            }
+        } else {
 #pragma unroll
-            for (int m = 0; m < SEG / TPR; ++m) gout[x][q + TPR * m][i] = keep[x][m];
+            for (int m = 0; m < SEG / TPR; ++m) gout[3][q + TPR * m][i] = keep[0][m];
+        }
         __syncthreads();
         // the segment's gradients, each token's 64 values contiguous
         const int n = min(SEG, T - c * SEG);
 #pragma unroll
-        for (int m = 0; m < SEG * NH / TH; ++m) {
-            const int e = tid + TH * m, u = e >> 6, ii = e & 63;
+        for (int m = 0; m < SEG * NH / TH2; ++m) {
+            const int e = tid + TH2 * m, u = e >> 6, ii = e & 63;
             if (u < n) {
                 const size_t o = (((size_t)bb * T + c * SEG + u) * H + hh) * NH + ii;
                 dr[o] = tr::from_f32(gout[0][u][ii]);
@@ -345,7 +383,7 @@ __global__ __launch_bounds__(TH) void wkv7_train_bwd_kernel(
             }
         }
     }
-    if (ds0 != nullptr) {
+    if (ds0 != nullptr && !col) {
         float* p = ds0 + ((size_t)bh * NH + i) * NH + j0;
 #pragma unroll
         for (int c = 0; c < JPT / 4; ++c)
@@ -376,7 +414,7 @@ hipError_t launch_wkv7_train_bwd(int B, int T, int H, const void* r, const void*
                                  const float* ds_in, void* dr, void* dw, void* dk, void* dv, void* da, void* db,
                                  float* ds0, hipStream_t st)
 {
-    hipLaunchKernelGGL(wkv7_train_bwd_kernel<IO>, dim3((unsigned)(B * H)), dim3(TH), 0, st, T, H, (const IO*)r,
+    hipLaunchKernelGGL(wkv7_train_bwd_kernel<IO>, dim3((unsigned)(B * H)), dim3(TH2), 0, st, T, H, (const IO*)r,
                        (const IO*)w, (const IO*)k, (const IO*)v, (const IO*)a, (const IO*)b, (const IO*)dy, ckpt, sa,
                        ds_in, (IO*)dr, (IO*)dw, (IO*)dk, (IO*)dv, (IO*)da, (IO*)db, ds0);
     return hipGetLastError();
