@@ -632,7 +632,7 @@ def main():
     a = ap.parse_args()
     if a.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {a.gpus}): this build measures one GPU's "
-              "share; the rollout shards by sequence with no cross-GPU exchange (see DESIGN.md)",
+              "share; the rollout shards by sequence with no cross-GPU exchange",
               file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
