@@ -316,7 +316,10 @@ __global__ __launch_bounds__(kT) void sample_kernel(
     float s = 0.f;
 #pragma unroll
     for (int j = 0; j < kVPT; ++j) {
-        const float q = (x[j] == -INFINITY) ? 0.f : fminf(fast_exp(x[j] - mx), 1.0f);
+        // a NaN logit stays NaN here (the compare is false), so Z turns NaN and
+        // the row takes the uniform fallback, as the reference's isnan(probs) does
+        const float e = fast_exp(x[j] - mx);
+        const float q = (x[j] == -INFINITY) ? 0.f : (e > 1.0f ? 1.0f : e);
         key[j] = __float_as_uint(q);
         s += q;
     }

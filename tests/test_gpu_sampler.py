@@ -149,6 +149,48 @@ def test_bias_and_ban(gpu_device):
     assert not bool((tok >= 65530).any())
 
 
+def test_bias_clamp(gpu_device):
+    """logit_bias is clamped to +-100 (core.py:90-95, 198-204): two tokens of equal
+    logit with biases +150 and +100 are equiprobable; unclamped, the first would
+    take every draw."""
+    print("[case] logit bias clamp", flush=True)
+    row = torch.full((V,), -60.0)
+    row[100] = row[101] = 0.0
+    n = 8192
+    for rule in (osm.RULE_BATCH, osm.RULE_SINGLE):
+        tok, lp = draws(gpu_device, row, n, temperature=1.0, top_p=1.0, top_k=0, rule=rule,
+                        logit_bias={"100": 150.0, "101": 100.0})
+        assert bool(((tok == 100) | (tok == 101)).all())
+        c = int((tok == 100).sum())
+        assert abs(c - n / 2) < 5 * math.sqrt(n / 4), c  # binomial(n, 1/2) within 5 sigma
+        assert torch.allclose(lp, torch.full_like(lp, math.log(0.5)), atol=1e-4)
+
+
+@pytest.mark.parametrize("bad", ["nan", "posinf", "allneginf"])
+def test_non_finite_row_is_uniform(gpu_device, bad):
+    """TokenSampler.sample (core.py:102-108): a softmax holding NaN or inf falls back
+    to the uniform distribution over the vocabulary.  65,536 draws of one row,
+    binned into 64 id ranges of 1024, pass a chi-square test against the uniform
+    distribution (the draws are a fixed function of the seed), under top-p and
+    without; logp = log(1/V + 1e-10)."""
+    print(f"[case] non-finite row {bad}", flush=True)
+    row = peaked_row(11)
+    if bad == "nan":
+        row[12345] = float("nan")
+    elif bad == "posinf":
+        row[777] = float("inf")
+    else:
+        row[:] = float("-inf")
+    n = 65536
+    for top_p in (1.0, 0.9):
+        tok, lp = draws(gpu_device, row, n, temperature=1.0, top_p=top_p, top_k=0, rule=osm.RULE_SINGLE)
+        assert bool(((tok >= 0) & (tok < V)).all())
+        counts = torch.bincount(tok // 1024, minlength=64).double()
+        stat = float(((counts - n / 64) ** 2 / (n / 64)).sum())
+        assert stat < chi2.ppf(0.999, 63), stat
+        assert torch.allclose(lp, torch.full_like(lp, math.log(1.0 / V + 1e-10)), atol=1e-4)
+
+
 def test_token_sampler_api(gpu_device):
     print("[case] TokenSampler API", flush=True)
     dsm.TokenSampler._max_valid_token_id = 65529

@@ -273,19 +273,30 @@ def test_key_update_by_a():
 
 def test_bonus_term():
     """out += (sum_head r * k * r_k) * v (model.py:267-268): with the GroupNorm
-    affine at zero only the bonus reaches the output; r = k = v = x and r_k = 1
-    give out_head = |x_head|^2 x_head."""
+    affine at zero only the bonus reaches the output.  r, k and v are three
+    different diagonal scalings of x (r = e_r x, k = e_k x, v = e_v x) and r_k = 1,
+    so out_head = (sum_head e_r e_k x^2) e_v x.  The three factors are not
+    parallel, so multiplying the sum by k or r, or summing r * v, gives another
+    vector."""
     sd = tiny_sd(20, L=1)
     C = 256
     H = C // N
     p = _transparent(sd, 0, C)
+    g = torch.Generator().manual_seed(21)
+    e = {n: 0.5 + torch.rand(C, generator=g, dtype=torch.float64) for n in ("receptance", "key", "value")}
+    for n, d in e.items():
+        sd[p + n + ".weight"] = torch.diag(d)
     sd[p + "r_k"] = torch.ones_like(sd[p + "r_k"])
     sd[p + "ln_x.weight"] = torch.zeros(C, dtype=torch.float64)
-    g = torch.Generator().manual_seed(21)
     x = torch.randn(1, 1, C, generator=g, dtype=torch.float64)
     y, _, _, _ = _run_time_mix(sd, 0, x)
     xh = x[0, 0].view(H, N)
-    assert torch.allclose(y[0, 0].view(H, N), (xh * xh).sum(-1, keepdim=True) * xh, rtol=1e-12, atol=1e-12)
+    er, ek, ev = (e[n].view(H, N) for n in ("receptance", "key", "value"))
+    expect = (er * ek * xh * xh).sum(-1, keepdim=True) * (ev * xh)
+    assert torch.allclose(y[0, 0].view(H, N), expect, rtol=1e-12, atol=1e-12)
+    # the wrong factor is far from it
+    wrong = (er * ek * xh * xh).sum(-1, keepdim=True) * (ek * xh)
+    assert not torch.allclose(wrong, expect, rtol=1e-3, atol=1e-3)
 
 
 def test_token_shift_lerp_direction():

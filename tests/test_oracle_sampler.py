@@ -42,6 +42,16 @@ def test_temperature_ban_and_bias():
     assert torch.allclose(d[:3], e / e.sum()) and d[3] == 0
     d = osm.distribution(x, logit_bias={"0": 500.0})  # clamped to +100
     assert d[0] > 0.999999
+    # the clamp itself: equal logits with biases +150 and +100 both reach +100,
+    # so the two tokens stay equiprobable (unclamped, token 0 would take ~all)
+    for rule in (osm.RULE_BATCH, osm.RULE_SINGLE):
+        d = osm.distribution(L(0.0, 0.0, 0.0), logit_bias={"0": 150.0, "1": 100.0, "2": -250.0}, rule=rule)
+        assert torch.allclose(d, L(0.5, 0.5, 0.0))
+        d = osm.distribution(L(0.0, 0.0, 0.0), logit_bias={"0": -150.0, "1": -100.0}, rule=rule)
+        assert torch.allclose(d, L(0.0, 0.0, 1.0))
+        # below the clamp a bias is added as given
+        d = osm.distribution(L(0.0, 0.0, 0.0), logit_bias={"0": math.log(3.0)}, rule=rule)
+        assert torch.allclose(d, L(0.6, 0.2, 0.2))
     assert osm.greedy(x, max_valid_id=2)[0] == 2
     t, lp = osm.greedy(L(1.0, 5.0, 5.0))
     assert t == 1 and math.isclose(lp, math.log(math.exp(5) / (math.exp(1) + 2 * math.exp(5))))
@@ -97,3 +107,21 @@ def test_generate_rule_top_k_then_nucleus_keeping_crossing():
     d = osm.distribution(x, temperature=0.5, rule=osm.RULE_MIXIN)
     q = L(0.16, 0.09, 0.04, 0.01)
     assert torch.allclose(d, q / q.sum())
+
+
+def test_non_finite_probabilities_fall_back_to_uniform():
+    """TokenSampler.sample (core.py:102-108): a softmax holding NaN or inf, from a
+    NaN logit, a +inf logit or a row of -inf, is replaced by the uniform
+    distribution over the vocabulary, before top-k / top-p (whose ties then keep
+    every token)."""
+    V = 6
+    rows = [L(1.0, float("nan"), 2.0, 0.0, 0.0, 0.0),
+            L(1.0, float("inf"), 2.0, 0.0, 0.0, 0.0),
+            torch.full((V,), float("-inf"), dtype=torch.float64)]
+    for x in rows:
+        for kw in ({}, {"top_p": 0.5}, {"top_k": 2}):
+            d = osm.distribution(x, rule=osm.RULE_SINGLE, **kw)
+            assert torch.allclose(d, torch.full((V,), 1.0 / V, dtype=torch.float64)), (x, kw)
+    # a finite row keeps its softmax
+    d = osm.distribution(L(0.0, math.log(2.0), 0.0), rule=osm.RULE_SINGLE)
+    assert torch.allclose(d, L(0.25, 0.5, 0.25))
