@@ -32,9 +32,14 @@ Used by the drop-in front ends (``GRPOBatchGenerator``, ``SchedulerCore``,
    steps follow the last finished sequence.
 4. **Collect**: one copy of the token table back to the host.
 
-Every sequence's tokens depend only on its prompt state and its own
-(sequence, position) random stream, so results do not depend on slot
-assignment, slot count or polling cadence.
+Every sequence's tokens depend only on its prompt state, the logits of its
+rows and its own (sequence, position) random stream, so results do not depend
+on slot assignment or polling cadence.  Float32 models give the same tokens for
+any slot count.  For 16-bit models the decode projections' plan (tile and K
+split of the packed-weight GEMM, and the library GEMM of the head) is chosen by
+the step's row bucket, so float32 summation order, and with it a sampled token
+now and then, can differ between runs with different slot counts; runs of one
+configuration are bit-identical.
 """
 
 from __future__ import annotations
@@ -133,6 +138,14 @@ class RolloutEngine:
         self.poll_every = max(1, int(poll_every))
         self.dev = model.device
         self.pool = None
+
+    def release(self):
+        """Drop the cached decode context (prompt store, slot pool, sequence
+        tables, captured graphs and their memory pool); the next ``run`` builds
+        a new one.  Between rollouts the context holds
+        ``(n_slots + distinct prompts) x`` a slot's state (1.5B: 13 MB, 7.2B:
+        34 MB per slot) plus the token tables."""
+        self._ctx = None
 
     # -- prefill ---------------------------------------------------------------
 

@@ -48,8 +48,12 @@ from .sampler import RULE_BATCH, RULE_SINGLE, TokenSampler
 
 class GRPOBatchGenerator:
     def __init__(self, model, tokenizer, chunk_size: int = 2048, max_prefill_batch_size: int = -1,
-                 max_decode_batch_size: int = -1, eos_token_id: Optional[int] = None, *, verbose: bool = True):
+                 max_decode_batch_size: int = -1, eos_token_id: Optional[int] = None, *, verbose: bool = True,
+                 keep_decode_context: bool = True):
         self.model = model
+        # False: release the decode context (slot pool, prompt store, graphs)
+        # after every generate, so the trainer's forward / backward can use the memory
+        self.keep_decode_context = keep_decode_context
         # the caller's module (e.g. GRPOTrainer's training model) runs through a
         # wrapper that shares its parameters; packed copies follow their updates
         self._hip = as_hip_model(model)
@@ -84,6 +88,9 @@ class GRPOBatchGenerator:
                  temperature: float = 0.9, top_p: float = 0.9, top_k: int = 0, repetition_penalty: float = 1.0,
                  logit_bias: Optional[dict] = None, *, max_new_tokens_per_seq: Optional[Sequence[int]] = None,
                  seed: Optional[int] = None) -> Dict[str, Any]:
+        # the trainer may have replaced parameters (or wrapped linears with LoRA)
+        # since the last call: re-bind the same wrapper to its current ones
+        self._hip = as_hip_model(self.model)
         B = len(input_ids)
         G = num_generations
         total = B * G
@@ -106,6 +113,8 @@ class GRPOBatchGenerator:
                       logit_bias=logit_bias, repetition_penalty=repetition_penalty, first_rule=RULE_SINGLE,
                       decode_rule=RULE_BATCH, first_can_finish=False, chunk_size=self.chunk_size,
                       max_seqs_per_forward=max(0, self.max_prefill_batch_size), seed=seed)
+        if not self.keep_decode_context:
+            eng.release()
         wall = time.time() - t0
         gen = sum(res.ngen)
         tm = res.timings
@@ -121,6 +130,11 @@ class GRPOBatchGenerator:
                   f"{res.prompt_tokens} prompt tokens): generated {gen} tokens in {res.n_decode_steps} decode "
                   f"steps; prefill {tm['prefill_s']:.3f}s, decode {tm['decode_s']:.3f}s, total {wall:.3f}s")
         return self._collect_results(res)
+
+    def release(self):
+        """Free the decode contexts kept for the next call (see ``RolloutEngine.release``)."""
+        for eng in self._engines.values():
+            eng.release()
 
     def _collect_results(self, res) -> Dict[str, Any]:
         """completions (decoded text), completion_ids ``[total, L]`` (zero past each

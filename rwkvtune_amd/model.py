@@ -395,7 +395,12 @@ class RWKV7Model(nn.Module):
         self._packs = None
         self._packs_key = None
         self._packs_struct = None
-        self._packs_gen = 0  # bumped whenever the packs are rebuilt (new buffers)
+        # bumped whenever the packs are rebuilt (new buffers) or a parameter's
+        # storage moved: captured decode graphs hold both kinds of address
+        self._packs_gen = 0
+        # called before the parameter check of every packs(): refreshes the
+        # merged weights of a caller's LoRA-wrapped linears (as_hip_model)
+        self._pre_pack = None
         # decode rows of a bf16 model run their projections on the library's
         # grouped MFMA GEMM over packed weights: r, k, v and the LoRA downs (tanh /
         # sigmoid fused) in one launch, the LoRA ups in one, the FFN key (relu^2
@@ -464,10 +469,13 @@ class RWKV7Model(nn.Module):
         """The kernels' parameter packs, rebuilt or refreshed whenever a parameter
         changed since they were made (no ``invalidate()`` needed after an
         optimizer step that updates the parameters in place)."""
+        if self._pre_pack is not None:
+            self._pre_pack()
         key = self._param_key()
         if self._packs is not None and key == self._packs_key:
             return self._packs
         self._check_device()
+        old = self._packs_key
         C = self.config.n_embd
         with torch.no_grad():
             if self._packs is not None and self._struct_key() == self._packs_struct:
@@ -481,6 +489,9 @@ class RWKV7Model(nn.Module):
                                 self.ln_out.bias.detach().float().contiguous())
                 self._packs_struct = self._struct_key()
                 self._packs_gen += 1
+        if old is not None and [k[0] for k in key] != [k[0] for k in old]:
+            # the embedding and the head are read in place by the decode step
+            self._packs_gen += 1
         self._packs_key = key
         return self._packs
 
@@ -944,42 +955,149 @@ def _config_of_params(params, src_config=None) -> RWKV7Config:
                        dim_gate_lora=int(dg), dim_mv_lora=int(dv))
 
 
-def as_hip_model(module: nn.Module) -> RWKV7Model:
-    """An ``RWKV7Model`` running ``module``'s own parameters on the HIP library.
+def _lora_linears(module: nn.Module) -> dict:
+    """Sub-modules wrapping an ``nn.Linear`` with a LoRA adapter the way the
+    reference's ``LoraLinear`` does (``rwkvtune/peft/lora/layer.py:15-199``):
+    ``base_layer``, ``lora_A [r, in]``, ``lora_B [out, r]``, ``scaling`` and the
+    ``merged`` / ``disabled`` flags; the layer computes
+    ``base_layer(x) + (x A^T) B^T * scaling`` unless merged or disabled."""
+    out = {}
+    for name, sub in module.named_modules():
+        base = getattr(sub, "base_layer", None)
+        if (isinstance(base, nn.Linear) and isinstance(getattr(sub, "lora_A", None), torch.Tensor)
+                and isinstance(getattr(sub, "lora_B", None), torch.Tensor)):
+            out[name] = sub
+    return out
 
-    ``module`` is any ``nn.Module`` with the reference ``RWKV7Model``'s parameter
-    names (``emb.weight``, ``blocks.{i}.att.receptance.weight``, ...) - the
-    training model ``GRPOTrainer`` hands its rollout generator
-    (``rwkvtune/training/grpo/lightning_module.py:708-750``).  The returned model
-    registers the *same* ``Parameter`` objects (nothing is copied), so parameter
-    updates are seen; its packed copies are refreshed when a parameter's version
-    or storage changes.  One wrapper is kept per module.  An ``RWKV7Model`` is
-    returned unchanged.  A module with parameters the architecture does not have
-    (e.g. adapter weights not merged into the base weights) is rejected."""
-    if isinstance(module, RWKV7Model):
-        return module
-    hit = _HIP_MODELS.get(module)
-    if hit is not None:
-        return hit
+
+class _LoraMerge:
+    """Keeps the wrapper's own weight of each LoRA-wrapped linear equal to
+    ``W + scaling * B A`` (``W`` alone when the adapter is merged into ``W`` or
+    disabled, ``layer.py:127-170``): recomputed, in float32 and rounded once to
+    the weight's dtype, when the base weight, ``lora_A`` or ``lora_B`` changed
+    (version or storage), or the scaling or flags did.  The result is copied into
+    the same tensor, so the packs see a version bump and captured graphs keep
+    their addresses."""
+
+    def __init__(self):
+        self.entries = []  # (lora module, destination parameter)
+        self.keys = []
+
+    def bind(self, entries):
+        self.entries = list(entries)
+        self.keys = [None] * len(self.entries)
+
+    @staticmethod
+    def _key(lm):
+        W, A, B = lm.base_layer.weight, lm.lora_A, lm.lora_B
+        return (W.data_ptr(), W._version, A.data_ptr(), A._version, B.data_ptr(), B._version,
+                float(getattr(lm, "scaling", 1.0)), bool(getattr(lm, "merged", False)),
+                bool(getattr(lm, "disabled", False)))
+
+    @torch.no_grad()
+    def __call__(self):
+        for i, (lm, dst) in enumerate(self.entries):
+            key = self._key(lm)
+            if key == self.keys[i]:
+                continue
+            W = lm.base_layer.weight
+            if key[-2] or key[-1]:
+                dst.copy_(W)
+            else:
+                A, B = lm.lora_A.detach().float(), lm.lora_B.detach().float()
+                dst.copy_(W.detach().float() + (B @ A) * key[-3])
+            self.keys[i] = key
+
+
+def _bind(m: RWKV7Model, module: nn.Module):
+    """Point ``m``'s parameters at ``module``'s (the same ``Parameter`` objects),
+    with a merged weight of its own for every LoRA-wrapped linear."""
+    lora = _lora_linears(module)
     params = dict(module.named_parameters())
-    cfg = _config_of_params(params, getattr(module, "config", None))
-    with torch.device("meta"):
-        m = RWKV7Model(cfg)
     ours = dict(m.named_parameters())
-    extra = sorted(set(params) - set(ours))
-    missing = sorted(set(ours) - set(params))
+    expect = set(ours)
+    for name in lora:
+        expect.discard(name + ".weight")
+        expect |= {name + ".base_layer.weight", name + ".lora_A", name + ".lora_B"}
+    extra = sorted(set(params) - expect)
+    missing = sorted(expect - set(params))
     if extra or missing:
         raise ValueError(f"{type(module).__name__} does not carry the RWKV-7 parameter set: "
                          f"missing {missing[:4]}, unexpected {extra[:4]}")
     devs = {p.device for p in params.values()}
     if len(devs) != 1:
         raise ValueError(f"parameters on several devices: {sorted(map(str, devs))}")
+    merges = []
     for name, p in ours.items():
+        owner, _, leaf = name.rpartition(".")
+        if leaf == "weight" and owner in lora:
+            lm = lora[owner]
+            W = lm.base_layer.weight
+            r = lm.lora_A.shape[0]
+            if (tuple(W.shape) != tuple(p.shape) or tuple(lm.lora_A.shape) != (r, W.shape[1])
+                    or tuple(lm.lora_B.shape) != (W.shape[0], r)):
+                raise ValueError(f"{owner}: LoRA shapes W {tuple(W.shape)}, A {tuple(lm.lora_A.shape)}, "
+                                 f"B {tuple(lm.lora_B.shape)} do not fit {tuple(p.shape)}")
+            if lm.base_layer.bias is not None:
+                raise ValueError(f"{owner}: the architecture's linears have no bias")
+            own = p if getattr(p, "_lora_merged", False) and p.device == W.device and p.dtype == W.dtype \
+                else None
+            if own is None:
+                own = nn.Parameter(torch.empty_like(W, memory_format=torch.contiguous_format), requires_grad=False)
+                own._lora_merged = True
+                m.get_submodule(owner)._parameters[leaf] = own
+            merges.append((lm, own))
+            continue
         src = params[name]
         if tuple(src.shape) != tuple(p.shape):
             raise ValueError(f"{name}: shape {tuple(src.shape)}, expected {tuple(p.shape)}")
-        owner, _, leaf = name.rpartition(".")
         m.get_submodule(owner)._parameters[leaf] = src
+    if merges:
+        if m._pre_pack is None:
+            m._pre_pack = _LoraMerge()
+        m._pre_pack.bind(merges)
+        m._pre_pack()
+    else:
+        m._pre_pack = None
+    m._src_params = list(module.parameters())
+
+
+def as_hip_model(module: nn.Module) -> RWKV7Model:
+    """An ``RWKV7Model`` running ``module``'s own parameters on the HIP library.
+
+    ``module`` is any ``nn.Module`` with the reference ``RWKV7Model``'s parameter
+    names (``emb.weight``, ``blocks.{i}.att.receptance.weight``, ...) - the
+    training model ``GRPOTrainer`` hands its rollout generator
+    (``rwkvtune/training/grpo/lightning_module.py:708-750``), also after
+    ``get_peft_model`` (``rwkvtune/training/grpo_trainer.py:381-393``) replaced
+    some of its linears by LoRA layers (``base_layer`` + ``lora_A`` / ``lora_B``).
+    The returned model registers the *same* ``Parameter`` objects (nothing is
+    copied), so parameter updates are seen; a LoRA-wrapped linear gets a weight
+    of its own, ``W + scaling * B A``, recomputed when ``W``, ``A`` or ``B``
+    change.  Packed copies are refreshed when a parameter's version or storage
+    changes.  One wrapper is kept per module; each call checks that ``module``
+    still holds the same ``Parameter`` objects and re-binds the ones it replaced
+    (``load_state_dict(assign=True)``, a LoRA layer added later).  An
+    ``RWKV7Model`` is returned unchanged.  A module with parameters the
+    architecture does not have is rejected."""
+    if isinstance(module, RWKV7Model):
+        return module
+    hit = _HIP_MODELS.get(module)
+    if hit is not None:
+        cur = list(module.parameters())
+        old = hit._src_params
+        if len(cur) != len(old) or any(a is not b for a, b in zip(cur, old)):
+            _bind(hit, module)
+        return hit
+    params = dict(module.named_parameters())
+    lora = _lora_linears(module)
+    if lora:
+        for name in lora:
+            params[name + ".weight"] = lora[name].base_layer.weight
+    cfg = _config_of_params(params, getattr(module, "config", None))
+    with torch.device("meta"):
+        m = RWKV7Model(cfg)
+    _bind(m, module)
     try:
         src_block0 = module.get_submodule("blocks.0")
     except AttributeError:

@@ -272,6 +272,8 @@ class SchedulerCore:
         """One scheduling step: admit, decode the running sequences, prefill the
         next chunks; returns the step's new ``(seq_id, token_id)`` pairs."""
         with torch.no_grad():
+            # re-bind the wrapper if the caller replaced parameters since the last step
+            self._hip = as_hip_model(self.model)
             decode_batch, prefill_batch = self._schedule()
             if not decode_batch and not prefill_batch:
                 return []

@@ -149,3 +149,127 @@ def test_trainer_model_dropin_follows_optimizer_steps(gpu_device, dtype):
     after = run()
     assert after == _greedy_paths(_fresh(src, dtype), prompts)
     assert after != before
+
+
+def test_storage_swap_and_parameter_replacement_rebuild_graphs(gpu_device):
+    """A parameter whose storage is swapped (``p.data = ...``, as FSDP / ZeRO-3
+    gathers do) between two ``generate`` calls makes the captured decode graphs
+    stale (they read the embedding and the head in place): the pack generation
+    moves, the graphs are rebuilt, and the paths equal a fresh model's.  The same
+    holds when the module's ``Parameter`` objects are replaced
+    (``load_state_dict(assign=True)``): the wrapper re-binds to the new ones."""
+    print("[case] storage swap / parameter replacement", flush=True)
+    dtype = torch.bfloat16
+    src = _plain_module(tiny(dtype, 51))
+    g = torch.Generator().manual_seed(52)
+    prompts = [torch.randint(0, V - 3, (n,), generator=g).tolist() for n in (7, 19)]
+    gen = GRPOBatchGenerator(src, _Tok(), chunk_size=16, max_decode_batch_size=4, verbose=False)
+
+    def run():
+        out = gen.generate(prompts, 10, num_generations=2, temperature=0.0, top_p=1.0)
+        ids, masks = out["completion_ids"].cpu(), out["masks"].cpu()
+        return [ids[q, :int(masks[q].sum())].tolist() for q in range(ids.shape[0])]
+
+    before = run()
+    gen0 = gen._hip._packs_gen
+    gw = torch.Generator(device=gpu_device).manual_seed(53)
+    with torch.no_grad():
+        for name in ("emb.weight", "head.weight", "blocks.1.ffn.key.weight"):
+            p = src.get_parameter(name)
+            p.data = (p.data.float() + 0.3 * torch.randn(p.shape, generator=gw, device=gpu_device)
+                      * p.data.float().std()).to(dtype)
+    after = run()
+    assert gen._hip._packs_gen > gen0
+    assert after == _greedy_paths(_fresh(src, dtype), prompts)
+    assert after != before
+    # new Parameter objects: the wrapper follows them
+    hip = gen._hip
+    sd = {k: (v.detach().float() * 1.25).to(dtype) for k, v in src.state_dict().items()}
+    src.load_state_dict(sd, assign=True)
+    again = run()
+    assert gen._hip is hip
+    assert again == _greedy_paths(_fresh(src, dtype), prompts)
+
+
+class _LoraLinear(nn.Module):
+    """A linear wrapped with a LoRA adapter under the attribute names of the
+    reference's ``LoraLinear`` (``rwkvtune/peft/lora/layer.py:15-199``)."""
+
+    def __init__(self, weight, r, alpha):
+        super().__init__()
+        out_f, in_f = weight.shape
+        self.base_layer = nn.Linear(in_f, out_f, bias=False, device=weight.device, dtype=weight.dtype)
+        with torch.no_grad():
+            self.base_layer.weight.copy_(weight)
+        self.base_layer.weight.requires_grad_(False)
+        self.r, self.scaling = r, alpha / r
+        g = torch.Generator(device=weight.device).manual_seed(out_f * 31 + in_f)
+        self.lora_A = nn.Parameter((torch.rand(r, in_f, generator=g, device=weight.device) - 0.5)
+                                   .mul(2 / in_f ** 0.5).to(weight.dtype))
+        self.lora_B = nn.Parameter(torch.zeros(out_f, r, device=weight.device, dtype=weight.dtype))
+        self.merged = False
+        self.disabled = False
+
+
+LORA_TARGETS = ("att.receptance", "att.key", "att.value", "att.output", "ffn.key", "ffn.value")
+
+
+def _merged_state(src, dtype):
+    """The plain model a LoRA-wrapped module computes: W + scaling * B A per
+    wrapped linear (float32, rounded once)."""
+    sd = {}
+    for name, mod in src.named_modules():
+        if isinstance(mod, _LoraLinear):
+            W = mod.base_layer.weight.detach().float()
+            if not (mod.merged or mod.disabled):
+                W = W + (mod.lora_B.detach().float() @ mod.lora_A.detach().float()) * mod.scaling
+            sd[name + ".weight"] = W.to(dtype)
+    for name, p in src.named_parameters():
+        if ".base_layer." not in name and not name.endswith(("lora_A", "lora_B")):
+            sd[name] = p.detach()
+    return sd
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_trainer_model_dropin_with_lora(gpu_device, dtype):
+    """The call site in LoRA mode (``GRPOTrainer`` wraps its model with
+    ``get_peft_model``, ``rwkvtune/training/grpo_trainer.py:381-393``, and hands it
+    to the generator, ``grpo/lightning_module.py:708-750``): greedy paths equal a
+    fresh model built from the merged weights, before and after an optimizer
+    step on ``lora_A`` / ``lora_B`` only, and with the adapters disabled."""
+    print(f"[case] LoRA drop-in {dtype}", flush=True)
+    src = _plain_module(tiny(dtype, 55))
+    for name, mod in list(src.named_modules()):
+        if name.endswith(LORA_TARGETS) and name.count(".") == 3:
+            parent = src.get_submodule(name.rpartition(".")[0])
+            setattr(parent, name.rpartition(".")[2], _LoraLinear(mod.weight.detach(), 16, 32))
+    lora_params = [p for n, p in src.named_parameters() if n.endswith(("lora_A", "lora_B"))]
+    assert len(lora_params) == 2 * 6 * 2
+    g = torch.Generator().manual_seed(56)
+    prompts = [torch.randint(0, V - 3, (n,), generator=g).tolist() for n in (6, 21, 13)]
+    gen = GRPOBatchGenerator(src, _Tok(), chunk_size=16, max_decode_batch_size=4, verbose=False)
+
+    def run():
+        out = gen.generate(prompts, 10, num_generations=2, temperature=0.0, top_p=1.0)
+        ids, masks = out["completion_ids"].cpu(), out["masks"].cpu()
+        return [ids[q, :int(masks[q].sum())].tolist() for q in range(ids.shape[0])]
+
+    def fresh():
+        m = tiny(dtype, 0)
+        m.load_state_dict({k: v.clone() for k, v in _merged_state(src, dtype).items()})
+        return m
+
+    before = run()  # B = 0: the base model
+    assert before == _greedy_paths(fresh(), prompts)
+    opt = torch.optim.SGD(lora_params, lr=1.0)
+    for i, p in enumerate(lora_params):
+        gg = torch.Generator(device=p.device).manual_seed(100 + i)
+        p.grad = (torch.randn(p.shape, generator=gg, device=p.device) * 0.05).to(p.dtype)
+    opt.step()
+    after = run()
+    assert after == _greedy_paths(fresh(), prompts)
+    assert after != before
+    for mod in src.modules():
+        if isinstance(mod, _LoraLinear):
+            mod.disabled = True
+    assert run() == before

@@ -76,6 +76,40 @@ def test_train_kernels_fp32(gpu_device, T, with_state, lo, hi, tol):
         assert close(ds0, grads_o[6], tol)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_train_kernels_16bit_multichunk_strong_decay(gpu_device, dtype):
+    """16-bit training op over T = 160 (five 32-token chunks of the chunked
+    forward, ten 16-token segments of the backward) with raw decays in
+    [-6, -0.5] (per-token decays down to 0.55, where the backward's step-back
+    from the forward's checkpoints amplifies their error most), an initial state
+    and a final-state gradient, against the float64 oracle on the rounded
+    inputs.  y within one ulp + 2e-3 of max|y|; sa, checkpoints, final state and
+    every gradient within 2e-2 of their largest magnitude."""
+    print(f"[case] train kernels {dtype} T=160 strong decay", flush=True)
+    B, T, H = 2, 160, 2
+    xs = [x.to(dtype) for x in inputs(B, T, H, -6.0, -0.5, seed=77)]
+    g = torch.Generator().manual_seed(78)
+    dy = torch.randn(B, T, H, 64, generator=g).to(dtype)
+    s0 = torch.randn(B, H, 64, 64, generator=g) * 0.1
+    ds_in = torch.randn(B, H, 64, 64, generator=g) * 0.1
+    r, w, k, v, a, b = (x.double() for x in xs)
+    y_o, sa_o, ck_o, S_o = otr.train_forward(r, w, k, v, a, b, s0=s0.double())
+    grads_o = otr.train_backward(r, w, k, v, a, b, dy.double(), ck_o, sa_o, ds_in=ds_in.double())
+
+    d = lambda x: x.to(gpu_device).contiguous()
+    rd, wd, kd, vd, ad, bd = (d(x) for x in xs)
+    s_out = torch.empty(B, H, 64, 64, device=gpu_device)
+    y, ck, sa = ops._train_forward(wd, rd, kd, vd, ad, bd, s0=d(s0), s_out=s_out)
+    dw, dr, dk, dv, da, db, ds0 = ops._train_backward(wd, rd, kd, vd, ad, bd, d(dy), ck, sa, ds_in=d(ds_in),
+                                                      want_ds0=True)
+    torch.cuda.synchronize()
+    assert y_close(y, y_o, dtype)
+    assert close(sa, sa_o, 2e-2) and close(ck, ck_o, 2e-2) and close(s_out, S_o, 2e-2)
+    for name, got, ref in zip(("dr", "dw", "dk", "dv", "da", "db"), (dr, dw, dk, dv, da, db), grads_o[:6]):
+        assert close(got, ref, 2e-2), name
+    assert close(ds0, grads_o[6], 2e-2)
+
+
 def test_standard_training_operator_bf16(gpu_device):
     """load_wkv_operator('cuda', for_inference=False): RUN_CUDA_RWKV7g semantics
     (bf16 cast, [B, T, C] in and out, T % 16 asserted) and autograd gradients of
