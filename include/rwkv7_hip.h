@@ -362,12 +362,28 @@ int rwkv7_rollout_first(int64_t n, int64_t maxlen, const int64_t *tok, const flo
                         int32_t *out_tok, float *out_logp, int32_t *out_step, int64_t eos,
                         int first_can_finish, int32_t *counters, void *stream);
 
+/* Prefill in the slot: record the first tokens of the m sequences seq_idx[i]
+ * (tok[i] / logp[i], sampled from the logits of their prompts' last tokens once
+ * the prompts were prefilled into their slots), as rwkv7_rollout_first does for
+ * all n; indices outside [0, n) are skipped.  The next rwkv7_rollout_commit gives
+ * each such slot a row fed with that token, or frees it when the first token
+ * finished the sequence.  With the commit's rule that a slot whose sequence has
+ * no token yet holds no row, this is the reference SchedulerCore's "admit into a
+ * free slot, prefill there, then decode" (rwkvtune/inference/scheduler_core.py:
+ * 250-299, 513-600) without a host read of each step's tokens. */
+int rwkv7_rollout_activate(int64_t m, const int32_t *seq_idx, int64_t n, int64_t maxlen,
+                           const int64_t *tok, const float *logp, const int32_t *seq_max_new,
+                           int32_t *seq_ngen, uint8_t *seq_done, int32_t *out_tok, float *out_logp,
+                           int32_t *out_step, int64_t eos, int first_can_finish, int32_t *counters,
+                           void *stream);
+
 /* One block: with have_sample, append tok[r] / logp[r] of the row r the slot
  * ran in to the sequence in slot s, finish it on EOS or its cap; then every free
- * slot takes the next waiting, unfinished sequence (index order) and lists the
- * state copy it needs; finally the row table is rebuilt (compacted when slot_row
- * is non-NULL; slot_row must then start as all -1 with every slot free).
- * S <= 1024. */
+ * slot (or slot whose sequence finished at its first token) takes the next
+ * waiting, unfinished sequence (index order) and lists the state copy it needs;
+ * finally the row table is rebuilt over the live slots - those whose sequence
+ * has at least one token (compacted when slot_row is non-NULL; slot_row must
+ * then start as all -1 with every slot free).  S <= 1024. */
 int rwkv7_rollout_commit(int64_t S, int64_t n, int64_t maxlen, int have_sample, const int64_t *tok,
                          const float *logp, int32_t *slot_seq, int32_t *row_slot, int32_t *slot_row,
                          int64_t *tok_in,

@@ -46,6 +46,7 @@ SIGNATURES = {
                             ctypes.c_uint64, _P, _P, _P, _P, _P]),
     "rwkv7_repetition_penalty": (_I32, [_I64, _I64, _P, _I64, ctypes.c_float] + [_P] * 7 + [_P]),
     "rwkv7_rollout_first": (_I32, [_I64, _I64] + [_P] * 8 + [_I64, _I32, _P, _P]),
+    "rwkv7_rollout_activate": (_I32, [_I64, _P, _I64, _I64] + [_P] * 8 + [_I64, _I32, _P, _P]),
     "rwkv7_rollout_commit": (_I32, [_I64, _I64, _I64, _I32] + [_P] * 13 + [_I64, _P, _P, _P, _P]),
     "rwkv7_rollout_prepare": (_I32, [_I64, _I64] + [_P] * 20 + [_P]),
     "rwkv7_admit_copy": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64] + [_P] * 6 + [_P]),

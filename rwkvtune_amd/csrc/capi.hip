@@ -423,10 +423,10 @@ extern "C" int rwkv7_repetition_penalty(int64_t M, int64_t V, float* logits, int
 // Slot table (slots.hip)
 // ---------------------------------------------------------------------------
 
-hipError_t launch_rollout_first(int n, int maxlen, const int64_t* tok, const float* logp, const int32_t* seq_max_new,
-                                int32_t* seq_ngen, uint8_t* seq_done, int32_t* out_tok, float* out_logp,
-                                int32_t* out_step, int64_t eos, int first_can_finish, int32_t* counters,
-                                hipStream_t st);
+hipError_t launch_rollout_first(int n, const int32_t* seq_idx, int n_seq, int maxlen, const int64_t* tok,
+                                const float* logp, const int32_t* seq_max_new, int32_t* seq_ngen, uint8_t* seq_done,
+                                int32_t* out_tok, float* out_logp, int32_t* out_step, int64_t eos,
+                                int first_can_finish, int32_t* counters, hipStream_t st);
 hipError_t launch_rollout_commit(int S, int n, int maxlen, int have_sample, const int64_t* tok, const float* logp,
                                  int32_t* slot_seq, int32_t* row_slot, int32_t* slot_row, int64_t* tok_in,
                                  const int32_t* seq_prompt,
@@ -454,8 +454,25 @@ extern "C" int rwkv7_rollout_first(int64_t n, int64_t maxlen, const int64_t* tok
     if (n == 0) return ok();
     if (!tok || !logp || !seq_max_new || !seq_ngen || !seq_done || !out_tok || !out_logp || !counters)
         return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_first: null pointer");
-    return launch_status(launch_rollout_first((int)n, (int)maxlen, tok, logp, seq_max_new, seq_ngen, seq_done, out_tok,
-                                              out_logp, out_step, eos, first_can_finish, counters,
+    return launch_status(launch_rollout_first((int)n, nullptr, (int)n, (int)maxlen, tok, logp, seq_max_new, seq_ngen,
+                                              seq_done, out_tok, out_logp, out_step, eos, first_can_finish, counters,
+                                              (hipStream_t)stream),
+                         "rollout_first_kernel");
+}
+
+extern "C" int rwkv7_rollout_activate(int64_t m, const int32_t* seq_idx, int64_t n, int64_t maxlen,
+                                      const int64_t* tok, const float* logp, const int32_t* seq_max_new,
+                                      int32_t* seq_ngen, uint8_t* seq_done, int32_t* out_tok, float* out_logp,
+                                      int32_t* out_step, int64_t eos, int first_can_finish, int32_t* counters,
+                                      void* stream) {
+    if (m < 0 || m > kMaxInt || n < 0 || n > kMaxInt || maxlen < 1 || maxlen > kMaxInt ||
+        n * maxlen > ((int64_t)1 << 40))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_activate: bad sizes");
+    if (m == 0) return ok();
+    if (!seq_idx || !tok || !logp || !seq_max_new || !seq_ngen || !seq_done || !out_tok || !out_logp || !counters)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_rollout_activate: null pointer");
+    return launch_status(launch_rollout_first((int)m, seq_idx, (int)n, (int)maxlen, tok, logp, seq_max_new, seq_ngen,
+                                              seq_done, out_tok, out_logp, out_step, eos, first_can_finish, counters,
                                               (hipStream_t)stream),
                          "rollout_first_kernel");
 }

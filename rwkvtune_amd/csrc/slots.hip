@@ -27,25 +27,37 @@
 // Admission takes waiting sequences in index order (sequences finished at their
 // first token are skipped); a sequence's tokens depend only on its own state and
 // its (sequence, position) random stream, never on which slot or row it runs in.
+//
+// Prefill in the slot (inline mode): a sequence may be admitted before it has a
+// token (seq_ngen == 0: its prompt is prefilled into the slot afterwards).  Such
+// a slot holds no row until rollout_first_kernel, given the sequence's index,
+// records its first token; the next commit then gives it a row with that token
+// as input, or, if the first token finished it, frees the slot for the next
+// waiting sequence.
 #include "common.hpp"
 
 namespace {
 
 enum { C_NEXT = 0, C_DONE = 1, C_STEP = 2, C_NADMIT = 3, C_LIVE = 4 };
 
-// First generated token of every sequence (sampled from its prompt's logits).
-__global__ void rollout_first_kernel(int n, int maxlen, const int64_t* __restrict__ tok,
+// First generated token of every sequence (sampled from its prompt's logits), or
+// with seq_idx of the n sequences seq_idx[0 .. n-1] (indices outside [0, n_seq)
+// are skipped).
+__global__ void rollout_first_kernel(int n, const int32_t* __restrict__ seq_idx, int n_seq, int maxlen,
+                                     const int64_t* __restrict__ tok,
                                      const float* __restrict__ logp, const int32_t* __restrict__ seq_max_new,
                                      int32_t* __restrict__ seq_ngen, uint8_t* __restrict__ seq_done,
                                      int32_t* __restrict__ out_tok, float* __restrict__ out_logp,
                                      int32_t* __restrict__ out_step, int64_t eos, int first_can_finish,
                                      int32_t* __restrict__ counters)
 {
-    const int q = blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= n) return;
-    const int64_t t = tok[q];
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const int q = seq_idx != nullptr ? seq_idx[i] : i;
+    if (q < 0 || q >= n_seq) return;
+    const int64_t t = tok[i];
     out_tok[(size_t)q * maxlen] = (int32_t)t;
-    out_logp[(size_t)q * maxlen] = logp[q];
+    out_logp[(size_t)q * maxlen] = logp[i];
     if (out_step != nullptr) out_step[(size_t)q * maxlen] = 0;
     seq_ngen[q] = 1;
     const bool fin = first_can_finish && ((eos >= 0 && t == eos) || seq_max_new[q] <= 1 || maxlen <= 1);
@@ -74,9 +86,15 @@ __global__ __launch_bounds__(1024) void rollout_commit_kernel(
     if (s < S) {
         const int q = slot_seq[s];
         const int row = compact ? slot_row[s] : s;  // the row this slot ran in
-        bool admit = q < 0;
-        if (q >= 0) next_tok = (row >= 0) ? tok_in[row] : 0;
-        if (q >= 0 && have_sample && row >= 0) {
+        // a free slot, or one whose sequence finished at its first token
+        bool admit = q < 0 || seq_done[q];
+        if (q >= 0 && !admit) {
+            // the row's input, or for a slot without a row (its sequence got its
+            // first token since the last commit) that token
+            const int last = seq_ngen[q] - 1;
+            next_tok = (row >= 0) ? tok_in[row] : (last >= 0 ? out_tok[(size_t)q * maxlen + last] : 0);
+        }
+        if (q >= 0 && !admit && have_sample && row >= 0) {
             const int64_t t = tok[row];
             const int pos = seq_ngen[q];
             if (pos < maxlen) {
@@ -115,16 +133,20 @@ __global__ __launch_bounds__(1024) void rollout_commit_kernel(
     }
     // every thread has read its row's tok_in before any row is rewritten
     __syncthreads();
+    // live: the slot's sequence has a token to feed (a sequence admitted before
+    // its prefill has none yet)
     if (!compact) {
         if (s < S) {
-            const bool live = slot_seq[s] >= 0;
+            const int q = slot_seq[s];
+            const bool live = q >= 0 && seq_ngen[q] > 0;
             row_slot[s] = live ? s : -1;
             tok_in[s] = live ? next_tok : 0;
         }
     } else {
         // rank of each live slot among the live slots: ballot within the wave,
         // wave totals through LDS
-        const bool live = s < S && slot_seq[s] >= 0;
+        const int q = s < S ? slot_seq[s] : -1;
+        const bool live = q >= 0 && seq_ngen[q] > 0;
         const unsigned long long bal = __ballot(live);
         const int lane = s & 63, w = s >> 6;
         const int in_wave = __popcll(bal & ((1ull << lane) - 1ull));
@@ -232,14 +254,14 @@ __global__ __launch_bounds__(256) void admit_copy_kernel(
 
 }  // namespace
 
-hipError_t launch_rollout_first(int n, int maxlen, const int64_t* tok, const float* logp, const int32_t* seq_max_new,
-                                int32_t* seq_ngen, uint8_t* seq_done, int32_t* out_tok, float* out_logp,
-                                int32_t* out_step, int64_t eos, int first_can_finish, int32_t* counters,
-                                hipStream_t st)
+hipError_t launch_rollout_first(int n, const int32_t* seq_idx, int n_seq, int maxlen, const int64_t* tok,
+                                const float* logp, const int32_t* seq_max_new, int32_t* seq_ngen, uint8_t* seq_done,
+                                int32_t* out_tok, float* out_logp, int32_t* out_step, int64_t eos,
+                                int first_can_finish, int32_t* counters, hipStream_t st)
 {
-    hipLaunchKernelGGL(rollout_first_kernel, dim3((n + 255) / 256), dim3(256), 0, st, n, maxlen, tok, logp,
-                       seq_max_new, seq_ngen, seq_done, out_tok, out_logp, out_step, eos, first_can_finish,
-                       counters);
+    hipLaunchKernelGGL(rollout_first_kernel, dim3((n + 255) / 256), dim3(256), 0, st, n, seq_idx, n_seq, maxlen,
+                       tok, logp, seq_max_new, seq_ngen, seq_done, out_tok, out_logp, out_step, eos,
+                       first_can_finish, counters);
     return hipGetLastError();
 }
 

@@ -225,6 +225,73 @@ class RolloutEngine:
         self._ctx = ctx
         return ctx
 
+    def _commit(self, c, have_sample: bool, n: int, maxlen: int, U: int):
+        """The slot table's commit (append the step's samples, retire, admit into
+        free slots, pack the live rows) and the admissions' state copies."""
+        P = _lib.ptr
+        cfg = self.model.config
+        st = _lib.stream_of(c.counters)  # the stream current at call time (graph capture changes it)
+        S = self.n_slots
+        pool = c.pool
+        _lib.call("rwkv7_rollout_commit", S, n, maxlen, int(have_sample), P(c.s_tok), P(c.s_lp),
+                  P(c.slot_seq), P(c.row_slot), P(c.slot_row), P(c.tok_in), P(c.sp), P(c.seq_max_new),
+                  P(c.seq_ngen), P(c.seq_done), P(c.out_tok), P(c.out_lp), P(c.out_step), self.eos,
+                  P(c.counters), P(c.admit_slot), P(c.admit_src), st)
+        _lib.call("rwkv7_admit_copy", P(c.counters), P(c.admit_slot), P(c.admit_src), cfg.n_layer, S, U,
+                  cfg.n_head * 64 * 64, cfg.n_embd, P(c.store.kv), P(c.store.att_x), P(c.store.ffn_x),
+                  P(pool.kv), P(pool.att_x), P(pool.ffn_x), st)
+
+    def _step_body(self, c, Mb: int, n: int, maxlen: int, U: int, decode_rule: int, pen, per_seq):
+        """One decode step over the leading ``Mb`` rows: the model's fused
+        single-token forward, the sampler's per-row inputs, (the repetition
+        penalty), the sampler, the commit."""
+        P = _lib.ptr
+        m = self.model
+        S = self.n_slots
+        logits = m.forward_pooled(c.tok_in[:Mb], c.row_slot[:Mb], c.row_last[:Mb], c.pool, decode=True)
+        st = _lib.stream_of(c.counters)
+        buf = c.buf
+        s_temp, s_topp, s_topk = per_seq
+        if pen is not None:
+            penalty, flat, p_start, p_len, h_start, h_len, h2_start, h2_len = pen
+            _lib.call("rwkv7_rollout_prepare", S, maxlen, P(c.row_slot), P(c.slot_seq), P(c.seq_key),
+                      P(c.seq_ngen), P(c.sp), P(p_start), P(p_len), P(c.active), P(buf.rng_key),
+                      P(buf.rng_ctr), P(h_start), P(h_len), P(h2_start), P(h2_len), P(s_temp), P(s_topp),
+                      P(s_topk), P(buf.temperature), P(buf.top_p), P(buf.top_k), st)
+            logits = logits.float()
+            repetition_penalty_(logits, penalty, flat, h_start, h_len, c.out_tok.view(-1),
+                                h2_start, h2_len, c.active)
+        else:
+            _lib.call("rwkv7_rollout_prepare", S, maxlen, P(c.row_slot), P(c.slot_seq), P(c.seq_key),
+                      P(c.seq_ngen), None, None, None, P(c.active), P(buf.rng_key), P(buf.rng_ctr), None, None,
+                      None, None, P(s_temp), P(s_topp), P(s_topk), P(buf.temperature), P(buf.top_p),
+                      P(buf.top_k), st)
+        sample_rows(logits, buf, rule=decode_rule, max_valid_id=self.max_valid_id, seed=0,
+                    out_tok=c.s_tok, out_logp=c.s_lp, active=c.active)
+        self._commit(c, True, n, maxlen, U)
+
+    def _decode_step(self, c, bound: int, buckets, n: int, maxlen: int, U: int, decode_rule: int, pen, per_seq):
+        """Run one decode step on the smallest row bucket covering ``bound`` live
+        rows: the bucket's captured graph, captured on its second use (the first
+        runs eagerly, so lazy allocations happen outside capture)."""
+        ws = RWKV7Model.gemm_workspace(self.dev)
+        if ws.ws.data_ptr() != c.ws_ptr:
+            # the split-K workspace was reallocated: the captured graphs hold the old one
+            c.graphs.clear()
+            c.ws_ptr = ws.ws.data_ptr()
+        Mb = next(b for b in buckets if b >= bound)
+        g = c.graphs.get(Mb)
+        if g is None and self.use_graph and Mb in c.warm:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=c.graph_pool):
+                self._step_body(c, Mb, n, maxlen, U, decode_rule, pen, per_seq)
+            c.graphs[Mb] = g
+        if g is not None:
+            g.replay()
+        else:
+            self._step_body(c, Mb, n, maxlen, U, decode_rule, pen, per_seq)
+            c.warm.add(Mb)
+
     @torch.no_grad()
     def run(self, prompts: Sequence[Sequence[int]], seq_prompt: Sequence[int], max_new_tokens,
             *, temperature: float = 1.0, top_p: float = 1.0, top_k: int = 0, logit_bias: Optional[dict] = None,
@@ -328,42 +395,9 @@ class RolloutEngine:
         del last_logits
 
         # 3. decode
-        cfg = m.config
-        kv_elems = cfg.n_head * 64 * 64
-        pool = c.pool
-
-        def commit(have_sample):
-            st = cur()
-            _lib.call("rwkv7_rollout_commit", S, n, maxlen, int(have_sample), P(c.s_tok), P(c.s_lp),
-                      P(c.slot_seq), P(c.row_slot), P(c.slot_row), P(c.tok_in), P(c.sp), P(c.seq_max_new),
-                      P(c.seq_ngen), P(c.seq_done), P(c.out_tok), P(c.out_lp), P(c.out_step), self.eos,
-                      P(c.counters), P(c.admit_slot), P(c.admit_src), st)
-            _lib.call("rwkv7_admit_copy", P(c.counters), P(c.admit_slot), P(c.admit_src), cfg.n_layer, S, U,
-                      kv_elems, cfg.n_embd, P(c.store.kv), P(c.store.att_x), P(c.store.ffn_x), P(pool.kv),
-                      P(pool.att_x), P(pool.ffn_x), st)
-
-        def step(Mb):
-            logits = m.forward_pooled(c.tok_in[:Mb], c.row_slot[:Mb], c.row_last[:Mb], pool, decode=True)
-            st = cur()
-            buf = c.buf
-            if use_pen:
-                _lib.call("rwkv7_rollout_prepare", S, maxlen, P(c.row_slot), P(c.slot_seq), P(c.seq_key),
-                          P(c.seq_ngen), P(c.sp), P(p_start), P(p_len), P(c.active), P(buf.rng_key),
-                          P(buf.rng_ctr), P(h_start), P(h_len), P(h2_start), P(h2_len), P(s_temp), P(s_topp),
-                          P(s_topk), P(buf.temperature), P(buf.top_p), P(buf.top_k), st)
-                logits = logits.float()
-                repetition_penalty_(logits, repetition_penalty, flat, h_start, h_len, c.out_tok.view(-1),
-                                    h2_start, h2_len, c.active)
-            else:
-                _lib.call("rwkv7_rollout_prepare", S, maxlen, P(c.row_slot), P(c.slot_seq), P(c.seq_key),
-                          P(c.seq_ngen), None, None, None, P(c.active), P(buf.rng_key), P(buf.rng_ctr), None, None,
-                          None, None, P(s_temp), P(s_topp), P(s_topk), P(buf.temperature), P(buf.top_p),
-                          P(buf.top_k), st)
-            sample_rows(logits, buf, rule=decode_rule, max_valid_id=self.max_valid_id, seed=0,
-                        out_tok=c.s_tok, out_logp=c.s_lp, active=c.active)
-            commit(True)
-
-        commit(False)  # initial admission
+        pen = (repetition_penalty, flat, p_start, p_len, h_start, h_len, h2_start, h2_len) if use_pen else None
+        per_seq = (s_temp, s_topp, s_topk)
+        self._commit(c, False, n, maxlen, U)  # initial admission
         torch.cuda.synchronize(dev)
         t2 = time.perf_counter()
         timings["first_token_s"] = t2 - t1
@@ -377,24 +411,8 @@ class RolloutEngine:
         finished = 0  # sequences known to be finished (from the last completed poll)
         while not done and n_steps < cap:
             for _ in range(self.poll_every):
-                if ws.ws.data_ptr() != c.ws_ptr:
-                    # the split-K workspace was reallocated: the captured graphs hold the old one
-                    c.graphs.clear()
-                    c.ws_ptr = ws.ws.data_ptr()
                 # rows needed: the live rows are at most the sequences not known to be finished
-                bound = min(S, n - finished)
-                Mb = next(b for b in buckets if b >= bound)
-                g = c.graphs.get(Mb)
-                if g is None and self.use_graph and Mb in c.warm:
-                    g = torch.cuda.CUDAGraph()
-                    with torch.cuda.graph(g, pool=c.graph_pool):
-                        step(Mb)
-                    c.graphs[Mb] = g
-                if g is not None:
-                    g.replay()
-                else:
-                    step(Mb)  # the first step of a bucket runs eagerly (lazy allocations happen outside capture)
-                    c.warm.add(Mb)
+                self._decode_step(c, min(S, n - finished), buckets, n, maxlen, U, decode_rule, pen, per_seq)
                 n_steps += 1
             # read the counters copied one polling period ago (already complete
             # unless the GPU is behind), then queue a fresh copy
@@ -428,6 +446,206 @@ class RolloutEngine:
         if key is None:
             self._ctx = None  # uncached: drop its buffers and graphs
         return RolloutResult(ng, ot, ol, os_, n_dec, timings, prompt_tokens=sum(plen))
+
+
+    @torch.no_grad()
+    def run_inline(self, prompts: Sequence[Sequence[int]], max_new_tokens, *, temperature: float = 1.0,
+                   top_p: float = 1.0, top_k: int = 0, logit_bias: Optional[dict] = None,
+                   first_rule: int = RULE_SINGLE, decode_rule: int = RULE_SINGLE, chunk_size: int = 512,
+                   max_batch_tokens: int = 8192, seed: int = 0, per_seq_sampling=None) -> RolloutResult:
+        """Continuous batching with every prompt prefilled in its own slot, for
+        queues longer than the slot pool (``SchedulerCore`` semantics,
+        ``rwkvtune/inference/scheduler_core.py:250-299, 445-600``): sequence q
+        continues ``prompts[q]``; its first token may finish it.
+
+        * The decode step's commit kernel admits waiting sequences (index order)
+          into freed slots on the device and zeroes their state; an admitted
+          sequence holds no row until it has a token.
+        * The host learns of admissions from its asynchronous poll (no step waits
+          for it) and prefills the admitted prompts straight into their slots,
+          ``chunk_size`` tokens per sequence and at most ``max_batch_tokens`` per
+          forward, one ragged forward between polling periods of decode steps.
+        * When a prompt is complete, its first token is drawn from the prompt's
+          last logits and recorded on the device (``rwkv7_rollout_activate``); the
+          next commit gives the slot a row, or frees it if that token finished
+          the sequence.
+        Memory is the slot pool and the token tables, whatever the queue length.
+        Tokens depend only on each sequence's prompt and (sequence, position)
+        random stream, as in ``run``."""
+        m = self.model
+        dev = self.dev
+        n = len(prompts)
+        S = self.n_slots
+        if isinstance(max_new_tokens, int):
+            max_new = [int(max_new_tokens)] * n
+        else:
+            max_new = [int(x) for x in max_new_tokens]
+        if n == 0:
+            return RolloutResult([], None, None, None, 0)
+        if min(max_new) < 1:
+            raise ValueError("max_new_tokens must be >= 1")
+        lens = [len(p) for p in prompts]
+        if min(lens) < 1:
+            raise ValueError("empty prompts are not supported")
+        maxlen = max(max_new)
+        chunk = max(1, int(chunk_size))
+        budget = max(1, int(max_batch_tokens))
+        bias = tuple(sorted((int(k), float(v)) for k, v in (logit_bias or {}).items()))
+        m.packs()
+        ws = RWKV7Model.gemm_workspace(dev)
+        # one zero store entry: admission zeroes the slot (the prompt is prefilled there)
+        key = None if per_seq_sampling is not None else (
+            "inline", S, n, maxlen, self.eos, decode_rule, self.max_valid_id, bias, m._packs_gen, ws.ws.data_ptr())
+        timings = {}
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        c = self._context(key, n, maxlen, 1, bias)
+        c.reset([0] * n, max_new, seq_keys(seed, n), temperature, top_p, top_k)
+        if per_seq_sampling is not None:
+            s_temp = torch.tensor(per_seq_sampling[0], dtype=torch.float32).to(dev)
+            s_topp = torch.tensor(per_seq_sampling[1], dtype=torch.float32).to(dev)
+            s_topk = torch.tensor(per_seq_sampling[2], dtype=torch.int32).to(dev)
+        else:
+            s_temp = s_topp = s_topk = None
+        per_seq = (s_temp, s_topp, s_topk)
+        # first-token sampler inputs for up to S sequences at a time (bias tables built once)
+        fbuf = SamplerBuffers(S, dev)
+        fbuf.set_uniform(temperature, top_p, top_k)
+        fbuf.set_bias(logit_bias, S)
+        fbuf.rng_ctr.zero_()
+        f_tok = torch.empty(S, dtype=torch.int64, device=dev)
+        f_lp = torch.empty(S, dtype=torch.float32, device=dev)
+        P = _lib.ptr
+        st = lambda: _lib.stream_of(c.counters)
+
+        # host view of the sequences: 0 not seen admitted, 1 prefilling, 2 first token recorded
+        hstate = [0] * n
+        slot_of = [-1] * n
+        pf_off = [0] * n
+        pend: List[int] = []
+        activated = 0
+
+        def take(snapshot):
+            new = [(int(q), sl) for sl, q in enumerate(snapshot) if q >= 0 and hstate[int(q)] == 0]
+            for q, sl in sorted(new):
+                hstate[q] = 1
+                slot_of[q] = sl
+                pend.append(q)
+
+        def pinned(vals, dtype):
+            t = torch.tensor(vals, dtype=dtype).pin_memory()
+            return t.to(dev, non_blocking=True)
+
+        def prefill_pass():
+            """One ragged forward over the next chunks of the prefilling prompts
+            (admission order), then the first tokens of the completed ones."""
+            nonlocal activated
+            room = budget
+            batch = []
+            for q in pend:
+                k = min(chunk, lens[q] - pf_off[q], room)
+                if k <= 0:
+                    break
+                batch.append((q, k))
+                room -= k
+                if room <= 0:
+                    break
+            toks, row_slot, row_last, seq_slot, logit_rows, done_q = [], [], [], [], [], []
+            cu = [0]
+            for q, k in batch:
+                base = cu[-1]
+                toks.extend(prompts[q][pf_off[q]:pf_off[q] + k])
+                row_slot.extend([slot_of[q]] * k)
+                row_last.extend([base + k - 1] + [-1] * (k - 1))
+                cu.append(base + k)
+                seq_slot.append(slot_of[q])
+                if pf_off[q] + k == lens[q]:
+                    logit_rows.append(base + k - 1)
+                    done_q.append(q)
+            logits = m.forward_pooled(pinned(toks, torch.int64), pinned(row_slot, torch.int32),
+                                      pinned(row_last, torch.int32), c.pool, decode=False,
+                                      cu_seqlens=pinned(cu, torch.int32), seq_slot=pinned(seq_slot, torch.int32),
+                                      logit_rows=pinned(logit_rows, torch.int32),
+                                      n_logit_rows=len(done_q))
+            for q, k in batch:
+                pf_off[q] += k
+            if not done_q:
+                return
+            for q in done_q:
+                hstate[q] = 2
+                pend.remove(q)
+            k = len(done_q)
+            idx = pinned(done_q, torch.int32)
+            sub = SamplerBuffers.__new__(SamplerBuffers)
+            if s_temp is not None:
+                il = idx.long()
+                sub.temperature, sub.top_p, sub.top_k = s_temp[il], s_topp[il], s_topk[il]
+            else:
+                sub.temperature, sub.top_p, sub.top_k = fbuf.temperature[:k], fbuf.top_p[:k], fbuf.top_k[:k]
+            sub.rng_key = c.seq_key.index_select(0, idx.long())
+            sub.rng_ctr = fbuf.rng_ctr[:k]
+            sub.bias_off = fbuf.bias_off[: k + 1] if fbuf.bias_off is not None else None
+            sub.bias_ids, sub.bias_val = fbuf.bias_ids, fbuf.bias_val
+            sample_rows(logits, sub, rule=first_rule, max_valid_id=self.max_valid_id, seed=0,
+                        out_tok=f_tok[:k], out_logp=f_lp[:k])
+            _lib.call("rwkv7_rollout_activate", k, P(idx), n, maxlen, P(f_tok), P(f_lp), P(c.seq_max_new),
+                      P(c.seq_ngen), P(c.seq_done), P(c.out_tok), P(c.out_lp), P(c.out_step), self.eos, 1,
+                      P(c.counters), st())
+            # rows for the new sequences; slots their first token finished are refilled
+            self._commit(c, False, n, maxlen, 1)
+            activated += k
+
+        # initial admission (every slot free), read back once
+        self._commit(c, False, n, maxlen, 1)
+        take(c.slot_seq.cpu().tolist())
+        buckets = row_buckets(S)
+        snap = torch.zeros(3 + S, dtype=torch.int32).pin_memory()
+        cap = n * maxlen + sum((L + chunk - 1) // chunk for L in lens) + 16
+        n_steps = n_prefill = idle = 0
+        pending_evt = None
+        finished = 0
+        t_prefill = 0.0
+        while finished < n:
+            progressed = False
+            if pend:
+                tp = time.perf_counter()
+                prefill_pass()
+                t_prefill += time.perf_counter() - tp
+                n_prefill += 1
+                progressed = True
+            live_bound = min(S, activated - finished)
+            if live_bound > 0:
+                for _ in range(self.poll_every):
+                    self._decode_step(c, live_bound, buckets, n, maxlen, 1, decode_rule, None, per_seq)
+                    n_steps += 1
+                progressed = True
+            if pending_evt is not None:
+                pending_evt.synchronize()
+                finished = int(snap[1])
+                take(snap[3:].tolist())
+            snap[0:3].copy_(c.counters[0:3], non_blocking=True)
+            snap[3:].copy_(c.slot_seq, non_blocking=True)
+            pending_evt = torch.cuda.Event()
+            pending_evt.record()
+            idle = 0 if progressed else idle + 1
+            if n_steps + n_prefill > cap or idle > 64:
+                raise RuntimeError(f"rollout did not finish: {finished}/{n} sequences after {n_steps} decode "
+                                   f"steps and {n_prefill} prefill passes")
+        torch.cuda.synchronize(dev)
+        t3 = time.perf_counter()
+        timings["prefill_host_s"] = t_prefill
+        timings["decode_s"] = t3 - t0
+        timings["prefill_passes"] = n_prefill
+        ng = c.seq_ngen.cpu().tolist()
+        ot, ol, os_ = c.out_tok.cpu(), c.out_lp.cpu(), c.out_step.cpu()
+        n_dec = int(c.counters[C_STEP].item())
+        t4 = time.perf_counter()
+        timings["collect_s"] = t4 - t3
+        timings["total_s"] = t4 - t0
+        timings["decode_steps_issued"] = n_steps
+        if key is None:
+            self._ctx = None
+        return RolloutResult(ng, ot, ol, os_, n_dec, timings, prompt_tokens=sum(lens))
 
 
 class _DecodeCtx:

@@ -273,3 +273,82 @@ def test_row_buckets_greedy_parity_and_graph_reuse(tiny):
     fresh = GRPOBatchGenerator(m, TinyTok(), chunk_size=16, max_decode_batch_size=96, verbose=False)
     assert sampled(fresh, 6) == b
     assert sampled(gen, 5) == a and a != b
+
+
+def test_inline_prefill_in_slots_greedy(tiny):
+    """Prompts prefilled in their own slots (``RolloutEngine.run_inline``, the path
+    of BatchGenerator): 60 sequences through 5 slots, prompts of 1..40 tokens in
+    chunks of 7 under a 23-token forward budget, per-sequence caps 1..9 (a cap of
+    1 finishes a sequence at its first token, which frees its slot at once) and
+    an EOS: every sequence equals the per-sequence reference loop
+    (``scheduler_core.py:250-299, 445-600``).  A second run on the same engine
+    (cached context, replayed graphs) gives the same tokens."""
+    print("[case] inline prefill: 60 sequences / 5 slots greedy", flush=True)
+    m, sd = tiny
+    ps = prompts(60, 60, 1, 40)
+    g = torch.Generator().manual_seed(61)
+    caps = torch.randint(1, 10, (60,), generator=g).tolist()
+    free = orl.scheduler_rollout(sd, ps, 9, max_valid_id=V - 4)
+    eos = free[3][2]
+    full = orl.scheduler_rollout(sd, ps, 9, eos=eos, max_valid_id=V - 4)
+    ref = [r[:c] for r, c in zip(full, caps)]
+    assert any(c == 1 for c in caps)
+    assert any(r[-1] == eos and len(r) < c for r, c in zip(ref, caps)), "EOS path not exercised"
+    eng = RolloutEngine(m, 5, eos_token_id=eos, max_valid_id=V - 4)
+    for _ in range(2):
+        res = eng.run_inline(ps, caps, temperature=0.0, chunk_size=7, max_batch_tokens=23, seed=3)
+        assert res.tokens == ref
+        assert res.timings["prefill_passes"] >= sum(len(p) for p in ps) // 23
+
+
+def test_inline_sampled_streams_independent_of_slots_and_budget(tiny):
+    """Sampled tokens of the inline path depend only on each sequence's prompt
+    and (sequence, position) stream: 3, 17 and 40 slots with different chunk
+    sizes and forward budgets (so different admission and prefill timing, row
+    buckets and graph replays) give identical tokens; every sequence reaches its
+    cap (no EOS)."""
+    print("[case] inline prefill: sampled invariance", flush=True)
+    m, _ = tiny
+    ps = prompts(62, 40, 1, 30)
+    runs = []
+    for slots, chunk, budget in ((3, 5, 11), (17, 64, 4096), (40, 3, 7)):
+        eng = RolloutEngine(m, slots, max_valid_id=V - 4)
+        res = eng.run_inline(ps, 12, temperature=0.9, top_p=0.9, chunk_size=chunk, max_batch_tokens=budget, seed=7)
+        runs.append(res.tokens)
+    assert runs[0] == runs[1] == runs[2]
+    assert all(len(t) == 12 for t in runs[0])
+
+
+def test_batch_generator_bounded_memory_long_queue(tiny):
+    """BatchGenerator over 2000 distinct prompts with 64 slots: the prompts are
+    prefilled in the slots, so peak device memory does not grow with the queue
+    (a prefilled state per prompt would add ~264 MB); greedy ids equal the
+    reference loop on every 40th sequence."""
+    print("[case] BatchGenerator 2000 prompts / 64 slots", flush=True)
+    m, sd = tiny
+
+    class Cfg:
+        generation_max_batch_size = 64
+
+    bg = BatchGenerator(m, TinyTok(), config=Cfg())
+
+    def peak_for(n, seed):
+        ps = prompts(seed, n, 2, 6)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        res = bg.generate(input_ids=ps, generation_config=GenerationConfig(max_length=3, temperature=0.0,
+                                                                          chunk_size=4, max_batch_tokens=64))
+        torch.cuda.synchronize()
+        return ps, res, torch.cuda.max_memory_allocated() - base
+
+    _, _, peak_small = peak_for(200, 40)
+    ps, res, peak_big = peak_for(2000, 41)
+    print(f"  peak extra memory: 200 prompts {peak_small / 2**20:.1f} MiB, 2000 prompts {peak_big / 2**20:.1f} MiB",
+          flush=True)
+    assert peak_big <= peak_small + (8 << 20)
+    assert bool((res["masks"].sum(1) == 3).all())
+    sub = list(range(0, 2000, 40))
+    ref = orl.scheduler_rollout(sd, [ps[i] for i in sub], 3, max_valid_id=V - 4)
+    for i, r in zip(sub, ref):
+        assert res["completion_ids"][i].cpu().tolist() == r, i
