@@ -1,7 +1,8 @@
 #!/usr/bin/env python3
 """Benchmark of rwkvtune's batched-generation hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload rollout|cfg5|decode|prefill|tmix|gemm|logprob|train]
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+                    [--workload rollout|cfg5|scheduler|decode|prefill|tmix|gemm|logprob|train]
 
 Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a message.
 
@@ -19,6 +20,11 @@ cfg5               rollout on RWKV-7 7.2B (L=32, C=4096, H=64), bf16: 128 random
     prompts, chunked prefill (chunk 256), up to 1024 sampled tokens (temperature 1.0,
     top_p 0.95) with Geometric(mean 600) stops, 128 slots; value = generated
     tokens / wall time of the rollout.  No CPU baseline (7.2B in fp32 on the host).
+scheduler          cfg4's 512 sequences (the same prompts x 8 copies and stop caps)
+    through ``BatchGenerator`` with 256 slots: no prompt sharing, each copy's prompt
+    prefilled in its own slot when the device admits it into a freed slot
+    (``RolloutEngine.run_inline``), ``TokenSampler.sample`` rules; value = generated
+    tokens / wall time (prefill of every copy included).
 logprob            GRPO log-prob recompute after a cfg4 rollout (RWKV-7 1.5B, bf16):
     512 sequences of 1024 prompt + 512 completion tokens through
     ``compute_per_token_logps``; a step is one whole batch; value = forward
@@ -383,6 +389,49 @@ def rollout(steps, warmup, dev):
                                   "ms_per_step": total_s / steps * 1e3, "runs": stats}
 
 
+def scheduler_rollout(steps, warmup, dev, max_batch_tokens=16384, chunk_size=2048):
+    """cfg4's 512 sequences (64 prompts x 8 copies, the same caps) through
+    ``BatchGenerator`` with 256 slots: every copy's prompt is prefilled in its own
+    slot as it is admitted (the reference's BatchGenerator / SchedulerCore
+    semantics, no prompt sharing), ``TokenSampler.sample`` rules, temp 1.0,
+    top_p 0.95."""
+    from rwkvtune_amd.batch_generator import BatchGenerator, GenerationConfig
+    from rwkvtune_amd.model import build_model, config_from_preset
+    cfg = config_from_preset("rwkv7-1.5b")
+    log("[bench] building RWKV-7 1.5B (bf16, seeded dense init) ...")
+    model = build_model(cfg, dtype=torch.bfloat16, device=dev, seed=1234)
+    prompts, caps = cfg4_workload()
+
+    class Cfg:
+        generation_max_batch_size = 256
+
+    bg = BatchGenerator(model, NullTokenizer(), config=Cfg())
+    gc = GenerationConfig(max_length=512, temperature=1.0, top_p=0.95, num_generations=8,
+                          max_batch_tokens=max_batch_tokens, chunk_size=chunk_size)
+    bg.generate(input_ids=prompts[:2], generation_config=GenerationConfig(max_length=8, temperature=1.0, top_p=0.95,
+                                                                          num_generations=4))
+    for i in range(warmup):
+        log(f"[bench] scheduler warm-up {i + 1}/{warmup}")
+        bg.generate(input_ids=prompts, generation_config=gc, max_new_tokens_per_seq=caps)
+    total_gen, total_s, stats = 0, 0.0, []
+    for i in range(steps):
+        torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        out = bg.generate(input_ids=prompts, generation_config=gc, max_new_tokens_per_seq=caps)
+        torch.cuda.synchronize(dev)
+        dt = time.perf_counter() - t0
+        n_gen = int(out["masks"].sum())
+        total_gen += n_gen
+        total_s += dt
+        st = dict(bg.last_stats)
+        stats.append(st)
+        log(f"[bench] scheduler rollout {i + 1}/{steps}: {n_gen} tokens in {dt:.3f} s = {n_gen / dt:.0f} tok/s "
+            f"({st['prompt_tokens']} prompt tokens prefilled in {st['prefill_passes']} passes, "
+            f"{st['decode_steps']} decode steps)")
+    return {"tokens": total_gen, "seconds": total_s, "value": total_gen / total_s,
+            "ms_per_step": total_s / steps * 1e3, "runs": stats, "prompt_tokens": stats[-1]["prompt_tokens"]}
+
+
 def rollout_roofline(model, ro, n_paths):
     """Algorithmic HBM bytes of the rollout's decode steps over their measured
     time: every step reads each decode weight once (the packed projections and
@@ -625,7 +674,8 @@ def main():
     ap.add_argument("--steps", type=int, default=None)
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="rollout",
-                    choices=["rollout", "cfg5", "decode", "prefill", "tmix", "gemm", "logprob", "train"])
+                    choices=["rollout", "cfg5", "scheduler", "decode", "prefill", "tmix", "gemm", "logprob",
+                             "train"])
     ap.add_argument("--rows", type=int, default=256, help="rows of the gemm workload")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cfg5", action="store_true", help="skip the 7.2B rollout leg of the default workload")
@@ -705,6 +755,27 @@ def main():
             "wkv7_prefill_cfg3": {k: pf[k] for k in ("us_per_launch", "tokens_per_s", "mfma_bf16_TFLOPs",
                                                      "mfma_frac", "GBs", "hbm_frac", "speedup_vs_token_serial")},
             "cpu_baseline": cpu,
+        }
+    elif a.workload == "scheduler":
+        steps = 2 if a.steps is None else a.steps
+        warmup = 1 if a.warmup is None else a.warmup
+        sc = scheduler_rollout(steps, warmup, dev)
+        run = sc["runs"][-1]
+        out = {
+            "metric": METRIC, "value": sc["value"], "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+            "warmup": warmup, "ms_per_step": sc["ms_per_step"], "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16 weights/activations, fp32 WKV state and element-wise",
+            "data": "synthetic (random prompts, seeded dense random-init weights)",
+            "config": {"workload": "cfg4's 512 sequences (64 prompts U(256,2048) x 8 copies, geometric(300) stops, "
+                                   "max 512 new) through BatchGenerator with 256 slots: each copy's prompt "
+                                   "prefilled in its own slot on admission (16,384 tokens per forward, chunks of "
+                                   "2,048), temp 1.0, top_p 0.95",
+                       "global_batch": 512, "seq_len": 2048 + 512, "parallelism": "none (1 GPU)",
+                       "generated_tokens": sc["tokens"] // steps, "prompt_tokens": sc["prompt_tokens"],
+                       "decode_steps": run["decode_steps"], "prefill_passes": run["prefill_passes"],
+                       "prefill_host_s": run["prefill_host_s"], "total_s": run["total_s"]},
+            "roofline": None,
+            "cpu_baseline": None,
         }
     elif a.workload == "cfg5":
         steps = 1 if a.steps is None else a.steps
