@@ -18,8 +18,14 @@ full-size rollouts with property checks.
   bit for bit: the decode GEMM's K-split plan depends on the row count, so the
   float32 summation order - and, at temperature 1 on random weights, the drawn
   tokens - can differ in the last bits.
+* Two 7.2B layers also decode 32, 64 and 96 rows: the three other plans of the
+  decode GEMM at C = 4096 (32 x 32 tile with split K and the reduction launch;
+  64 x 64; 128 x 64 over a partial row tile).
 * cfg5's model (RWKV-7 7.2B, all 32 layers) on a reduced rollout (8 prompts x
-  2048 tokens, chunk 256): the same properties with 8 (twice) and 3 slots.
+  2048 tokens, chunk 256): the same properties with 8 (twice) and 3 slots; and at
+  its real slot count on the bench's own 128 x 2048-token prompts with the stop
+  lengths cut to at most 128 tokens: two runs with 128 slots are bit-identical,
+  every path has exactly its stop length and only valid ids.
 """
 
 import pytest
@@ -57,7 +63,9 @@ def to_f64(states):
     return [{k: v.double() for k, v in s.items()} for s in states]
 
 
-@pytest.mark.parametrize("preset,rows,steps", [("rwkv7-1.5b", 256, 2), ("rwkv7-7.2b", 128, 1)])
+@pytest.mark.parametrize("preset,rows,steps", [("rwkv7-1.5b", 256, 2), ("rwkv7-7.2b", 128, 1),
+                                               ("rwkv7-7.2b", 32, 1), ("rwkv7-7.2b", 64, 1),
+                                               ("rwkv7-7.2b", 96, 1)])
 def test_decode_layers_at_benchmark_shape(gpu_device, preset, rows, steps):
     print(f"[case] bf16 decode, two layers of {preset}, {rows} rows, {steps} steps", flush=True)
     cfg = config_from_preset(preset, n_layer=2, vocab_size=1000)
@@ -135,10 +143,15 @@ def test_cfg4_rollout_full_size_properties(gpu_device):
     assert [p[0] for p in runs[0]] == [p[0] for p in runs[2]]
 
 
-def test_cfg5_model_rollout_properties(gpu_device):
-    print("[case] cfg5 model (7.2B, 32 layers): 8 x 2048-token prompts, chunk 256, 8 vs 3 slots", flush=True)
+@pytest.fixture(scope="module")
+def model_7b(gpu_device):
     cfg = config_from_preset("rwkv7-7.2b")
-    m = build_model(cfg, dtype=torch.bfloat16, device="cuda", seed=7272)
+    return build_model(cfg, dtype=torch.bfloat16, device="cuda", seed=7272)
+
+
+def test_cfg5_model_rollout_properties(model_7b):
+    print("[case] cfg5 model (7.2B, 32 layers): 8 x 2048-token prompts, chunk 256, 8 vs 3 slots", flush=True)
+    m = model_7b
     prompts, _ = cfg5_workload(n=8)
     caps = [c % 48 + 1 for c in cfg5_workload(n=8)[1]]
     runs = []
@@ -148,3 +161,17 @@ def test_cfg5_model_rollout_properties(gpu_device):
         _check_paths(runs[-1], caps)
     assert runs[0] == runs[1]
     assert [p[0] for p in runs[0]] == [p[0] for p in runs[2]]
+
+
+def test_cfg5_rollout_128_slots_properties(model_7b):
+    print("[case] cfg5 rollout at 128 slots: 128 x 2048-token prompts, chunk 256, caps <= 128, twice", flush=True)
+    prompts, caps5 = cfg5_workload()
+    caps = [min(c, 128) for c in caps5]
+    assert len(prompts) == 128 and any(c < 128 for c in caps)
+    gen = GRPOBatchGenerator(model_7b, _Tok(), chunk_size=256, max_decode_batch_size=128, verbose=False)
+    runs = []
+    for _ in range(2):
+        runs.append(_rollout(gen, prompts, 128, 1, caps, seed=11))
+        print(f"  {sum(len(p) for p in runs[-1])} tokens, {gen.last_stats['decode_steps']} decode steps", flush=True)
+        _check_paths(runs[-1], caps)
+    assert runs[0] == runs[1]
