@@ -42,7 +42,8 @@ from typing import Any, Dict, Iterator, List, Optional, Tuple, Union
 import torch
 
 from ._common import max_valid_token_id
-from .model import StatePool, as_hip_model
+from .engine import row_buckets
+from .model import RWKV7Model, StatePool, as_hip_model
 from .sampler import RULE_SINGLE, SamplerBuffers, TokenSampler, sample_rows
 
 
@@ -88,6 +89,90 @@ class SequenceState:
         return len(self.generated_tokens) >= self.max_new_tokens
 
 
+class _DecodeGraphs:
+    """The decode step of a ``SchedulerCore`` on static row buffers, captured in
+    one HIP graph per row bucket: rows 0 .. R-1 are the running sequences (their
+    slot, input token and sampling inputs copied in before each replay from
+    pinned host memory), rows R .. bucket-1 are inactive (slot -1).  A bucket's
+    first step runs eagerly (lazy allocations happen outside capture), later
+    ones replay its graph.  The graphs bake in the model's packed weights, the
+    shared split-K workspace, the sampler's seed and id ban; a change of any of
+    them drops them."""
+
+    def __init__(self, S: int, dev):
+        self.S = S
+        self.tok = torch.zeros(S, dtype=torch.int64, device=dev)
+        self.slot = torch.full((S,), -1, dtype=torch.int32, device=dev)
+        self.last = torch.arange(S, dtype=torch.int32, device=dev)
+        self.active = torch.zeros(S, dtype=torch.uint8, device=dev)
+        self.buf = SamplerBuffers(S, dev)
+        self.out_tok = torch.zeros(S, dtype=torch.int64, device=dev)
+        self.out_lp = torch.zeros(S, dtype=torch.float32, device=dev)
+        self.h_i64 = torch.zeros((2, S), dtype=torch.int64).pin_memory()    # token, random-stream key
+        self.h_i32 = torch.zeros((3, S), dtype=torch.int32).pin_memory()    # slot, top_k, position
+        self.h_f32 = torch.zeros((2, S), dtype=torch.float32).pin_memory()  # temperature, top_p
+        self.h_u8 = torch.zeros(S, dtype=torch.uint8).pin_memory()          # active
+        self.buckets = row_buckets(S)
+        self.graphs = {}
+        self.warm = set()
+        self.graph_pool = torch.cuda.graph_pool_handle()
+        self.key = None
+
+    def load(self, batch):
+        """Stage the rows of ``batch`` (running sequences) and copy them to the
+        device on the current stream; returns the bucket to run."""
+        R = len(batch)
+        Mb = next(b for b in self.buckets if b >= R)
+        self.h_i64.zero_()
+        self.h_i32[0].fill_(-1)
+        self.h_i32[1:].zero_()
+        self.h_f32.fill_(1.0)
+        self.h_u8.zero_()
+        self.h_i64[0, :R] = torch.tensor([s.last_token_id for s in batch], dtype=torch.int64)
+        self.h_i64[1, :R] = torch.tensor([s._rng_key for s in batch], dtype=torch.int64)
+        self.h_i32[0, :R] = torch.tensor([s.slot_id for s in batch], dtype=torch.int32)
+        self.h_i32[1, :R] = torch.tensor([int(s.top_k) for s in batch], dtype=torch.int32)
+        self.h_i32[2, :R] = torch.tensor([len(s.generated_tokens) for s in batch], dtype=torch.int32)
+        self.h_f32[0, :R] = torch.tensor([float(s.temperature) for s in batch], dtype=torch.float32)
+        self.h_f32[1, :R] = torch.tensor([float(s.top_p) for s in batch], dtype=torch.float32)
+        self.h_u8[:R] = 1
+        for dst, src in ((self.tok, self.h_i64[0]), (self.buf.rng_key, self.h_i64[1]), (self.slot, self.h_i32[0]),
+                         (self.buf.top_k, self.h_i32[1]), (self.buf.rng_ctr, self.h_i32[2]),
+                         (self.buf.temperature, self.h_f32[0]), (self.buf.top_p, self.h_f32[1]),
+                         (self.active, self.h_u8)):
+            dst[:Mb].copy_(src[:Mb], non_blocking=True)
+        return Mb
+
+    def _body(self, hip, pool, Mb, seed, max_valid_id):
+        logits = hip.forward_pooled(self.tok[:Mb], self.slot[:Mb], self.last[:Mb], pool, decode=True)
+        sub = SamplerBuffers.__new__(SamplerBuffers)
+        b = self.buf
+        sub.temperature, sub.top_p, sub.top_k = b.temperature[:Mb], b.top_p[:Mb], b.top_k[:Mb]
+        sub.rng_key, sub.rng_ctr = b.rng_key[:Mb], b.rng_ctr[:Mb]
+        sub.bias_off = sub.bias_ids = sub.bias_val = None
+        sample_rows(logits, sub, rule=RULE_SINGLE, max_valid_id=max_valid_id, seed=seed, out_tok=self.out_tok[:Mb],
+                    out_logp=self.out_lp[:Mb], active=self.active[:Mb])
+
+    def run(self, hip, pool, Mb, seed, max_valid_id):
+        hip.packs()  # refresh the packed weights outside capture
+        key = (hip._packs_gen, RWKV7Model.gemm_workspace(hip.device).ws.data_ptr(), seed, max_valid_id, id(pool))
+        if key != self.key:
+            self.graphs.clear()
+            self.warm.clear()
+            self.key = key
+        g = self.graphs.get(Mb)
+        if g is None and Mb in self.warm:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=self.graph_pool):
+                self._body(hip, pool, Mb, seed, max_valid_id)
+            self.graphs[Mb] = g
+        if g is not None:
+            g.replay()
+        else:
+            self._body(hip, pool, Mb, seed, max_valid_id)
+            self.warm.add(Mb)
+
+
 class SchedulerCore:
     def __init__(self, model, tokenizer, max_batch_size: int = 64, max_batch_tokens: int = 8192,
                  prefill_chunk_size: int = 512, state_cache=None):
@@ -114,6 +199,9 @@ class SchedulerCore:
             TokenSampler._max_valid_token_id = mv
         # the slot pool: fixed size, whatever the queue length
         self.state_pool = StatePool(self._hip.config, max_batch_size, self.device)
+        # decode steps replay a captured graph per row bucket (False: eager launches)
+        self.use_graph = True
+        self._graphs = _DecodeGraphs(max_batch_size, self.device)
         self._seed = TokenSampler._seed * 7919 + TokenSampler._next_key()
         self._keys = 0
         self._step_counter = 0
@@ -227,6 +315,17 @@ class SchedulerCore:
     def _execute_decode(self, batch: List[SequenceState]) -> List[Tuple[Union[int, str], int]]:
         if not batch:
             return []
+        if self.use_graph and not any(s.logit_bias for s in batch):
+            # one graph replay; the step's one host synchronisation is the read of its tokens
+            gr = self._graphs
+            R = len(batch)
+            Mb = gr.load(batch)
+            gr.run(self._hip, self.state_pool, Mb, self._seed, TokenSampler._max_valid_token_id)
+            toks, lps = gr.out_tok[:R].tolist(), gr.out_lp[:R].tolist()
+            out = []
+            for seq, t, lp in zip(batch, toks, lps):
+                self._append(seq, t, lp, out)
+            return out
         R = len(batch)
         tokens = torch.tensor([s.last_token_id for s in batch], dtype=torch.int64).to(self.device)
         rows = torch.arange(R, dtype=torch.int32, device=self.device)

@@ -352,3 +352,28 @@ def test_batch_generator_bounded_memory_long_queue(tiny):
     ref = orl.scheduler_rollout(sd, [ps[i] for i in sub], 3, max_valid_id=V - 4)
     for i, r in zip(sub, ref):
         assert res["completion_ids"][i].cpu().tolist() == r, i
+
+
+def test_scheduler_graph_steps_equal_eager(tiny):
+    """SchedulerCore's decode step replays a captured graph per row bucket (40
+    slots: buckets of 32 and 40 rows as the pool fills and drains); its sampled
+    tokens equal the eager launches' token for token, with per-sequence
+    temperature / top_p / top_k, and both end every sequence at its cap."""
+    print("[case] SchedulerCore graph vs eager decode", flush=True)
+    m, _ = tiny
+    ps = prompts(70, 90, 1, 20)
+    runs = []
+    for use_graph in (True, False):
+        TokenSampler.manual_seed(77)
+        sch = SchedulerCore(m, TinyTok(), max_batch_size=40, max_batch_tokens=64, prefill_chunk_size=8)
+        sch.use_graph = use_graph
+        seqs = [SequenceState(seq_id=i, prompt_tokens=p, max_new_tokens=5 + i % 7, temperature=0.8 + 0.01 * (i % 5),
+                              top_p=0.9 if i % 2 else 1.0, top_k=30 if i % 3 == 0 else 0) for i, p in enumerate(ps)]
+        sch.add_sequences(seqs)
+        for _ in sch.run_to_completion_sync():
+            pass
+        if use_graph:
+            assert set(sch._graphs.graphs) >= {32, 40}, sorted(sch._graphs.graphs)
+        runs.append([s.generated_tokens for s in seqs])
+        assert all(len(s.generated_tokens) == s.max_new_tokens for s in seqs)
+    assert runs[0] == runs[1]
