@@ -25,8 +25,11 @@ pytestmark = pytest.mark.gpu
 V = 65536
 
 
-def draws(gpu_device, row, n, *, temperature, top_p, top_k, rule, max_valid_id=None, logit_bias=None, seed=1):
-    logits = row.to(gpu_device).float().expand(n, -1).contiguous()
+def draws(gpu_device, row, n, *, temperature, top_p, top_k, rule, max_valid_id=None, logit_bias=None, seed=1,
+          dtype=torch.float32):
+    """n draws of one row given as `dtype` logits (16-bit rows without bias take
+    the value-histogram kernel, the others the radix-select kernel)."""
+    logits = row.to(gpu_device).to(dtype).expand(n, -1).contiguous()
     buf = dsm.SamplerBuffers(n, gpu_device)
     buf.set_uniform(temperature, top_p, top_k)
     buf.set_bias(logit_bias, n)
@@ -86,14 +89,15 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("case", CASES)
-def test_sampled_distribution(gpu_device, case):
+def test_sampled_distribution(gpu_device, case, dtype):
     rule, temp, top_p, top_k = case
-    print(f"[case] sample rule={rule} T={temp} p={top_p} k={top_k}", flush=True)
-    row = peaked_row(100 + CASES.index(case))
+    print(f"[case] sample rule={rule} T={temp} p={top_p} k={top_k} {dtype}", flush=True)
+    row = peaked_row(100 + CASES.index(case)).to(dtype).float()  # the values the kernel sees
     n = 8192
     tok, lp = draws(gpu_device, row, n, temperature=temp, top_p=top_p, top_k=top_k, rule=rule,
-                    max_valid_id=65529)
+                    max_valid_id=65529, dtype=dtype)
     dist = osm.distribution(row, temperature=temp, top_p=top_p, top_k=top_k, max_valid_id=65529, rule=rule)
     kept = dist > 0
     assert bool(kept[tok].all()), "a draw fell outside the kept set"
@@ -115,28 +119,39 @@ def test_sampled_distribution(gpu_device, case):
     assert stat < chi2.ppf(0.999, max(dof, 1)), f"chi2 {stat:.1f} dof {dof}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("rule,top_p,top_k", [(osm.RULE_BATCH, 0.95, 0), (osm.RULE_SINGLE, 0.9, 0),
                                                (osm.RULE_BATCH, 0.9, 3000), (osm.RULE_SINGLE, 1.0, 20000)])
-def test_flat_rows_kept_set(gpu_device, rule, top_p, top_k):
+def test_flat_rows_kept_set(gpu_device, rule, top_p, top_k, dtype):
     """Rows like a random-init model's (logits ~N(0, 1)): tens of thousands of
     tokens share the probability, so every level of the threshold search sees
     crowded bins.  Every draw lies in the oracle's kept set, and the draws reach
-    across it (the largest drawn rank is near the kept set's size)."""
-    print(f"[case] flat row rule={rule} p={top_p} k={top_k}", flush=True)
+    across it (the largest drawn rank is near the kept set's size).  A bf16 row has
+    ties (tens of tokens per value): the kernel keeps or drops a tied value whole,
+    where the reference's sort keeps an arbitrary subset, so there every draw's
+    logit is at least the lowest logit the oracle keeps; the log-probabilities are
+    checked on the float32 rows."""
+    print(f"[case] flat row rule={rule} p={top_p} k={top_k} {dtype}", flush=True)
     g = torch.Generator().manual_seed(31)
-    row = torch.randn(V, generator=g)
+    row = torch.randn(V, generator=g).to(dtype).float()
     n = 8192
-    tok, lp = draws(gpu_device, row, n, temperature=1.0, top_p=top_p, top_k=top_k, rule=rule, max_valid_id=65529)
+    tok, lp = draws(gpu_device, row, n, temperature=1.0, top_p=top_p, top_k=top_k, rule=rule, max_valid_id=65529,
+                    dtype=dtype)
     dist = osm.distribution(row, temperature=1.0, top_p=top_p, top_k=top_k, max_valid_id=65529, rule=rule)
     kept = dist > 0
-    assert bool(kept[tok].all()), "a draw fell outside the kept set"
+    if dtype == torch.float32:
+        assert bool(kept[tok].all()), "a draw fell outside the kept set"
+    else:
+        assert bool((tok <= 65529).all())
+        assert bool((row[tok] >= row[kept].min()).all()), "a draw fell below the kept values"
     order = torch.argsort(row[:65530], descending=True)
     rank = torch.empty(65530, dtype=torch.long)
     rank[order] = torch.arange(65530)
     assert int(rank[tok].max()) > 0.9 * int(kept.sum())
-    for i in range(0, n, 509):
-        t = int(tok[i])
-        assert abs(float(lp[i]) - osm.logp(dist, t, rule)) < 1e-4
+    if dtype == torch.float32:
+        for i in range(0, n, 509):
+            t = int(tok[i])
+            assert abs(float(lp[i]) - osm.logp(dist, t, rule)) < 1e-4
 
 
 def test_bias_and_ban(gpu_device):
@@ -166,14 +181,15 @@ def test_bias_clamp(gpu_device):
         assert torch.allclose(lp, torch.full_like(lp, math.log(0.5)), atol=1e-4)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("bad", ["nan", "posinf", "allneginf"])
-def test_non_finite_row_is_uniform(gpu_device, bad):
+def test_non_finite_row_is_uniform(gpu_device, bad, dtype):
     """TokenSampler.sample (core.py:102-108): a softmax holding NaN or inf falls back
     to the uniform distribution over the vocabulary.  65,536 draws of one row,
     binned into 64 id ranges of 1024, pass a chi-square test against the uniform
     distribution (the draws are a fixed function of the seed), under top-p and
     without; logp = log(1/V + 1e-10)."""
-    print(f"[case] non-finite row {bad}", flush=True)
+    print(f"[case] non-finite row {bad} {dtype}", flush=True)
     row = peaked_row(11)
     if bad == "nan":
         row[12345] = float("nan")
@@ -183,12 +199,33 @@ def test_non_finite_row_is_uniform(gpu_device, bad):
         row[:] = float("-inf")
     n = 65536
     for top_p in (1.0, 0.9):
-        tok, lp = draws(gpu_device, row, n, temperature=1.0, top_p=top_p, top_k=0, rule=osm.RULE_SINGLE)
+        tok, lp = draws(gpu_device, row, n, temperature=1.0, top_p=top_p, top_k=0, rule=osm.RULE_SINGLE,
+                        dtype=dtype)
         assert bool(((tok >= 0) & (tok < V)).all())
         counts = torch.bincount(tok // 1024, minlength=64).double()
         stat = float(((counts - n / 64) ** 2 / (n / 64)).sum())
         assert stat < chi2.ppf(0.999, 63), stat
         assert torch.allclose(lp, torch.full_like(lp, math.log(1.0 / V + 1e-10)), atol=1e-4)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_all_equal_row_is_uniform(gpu_device, dtype):
+    """All 65,536 logits equal and no ban: every rule keeps every token (ties), so the
+    draw is uniform with q = 1 and W = V.  In the 16-bit kernel the row's one value
+    overflows its 16-bit counter, which it detects (the counts no longer add up) and
+    turns into this uniform draw.  65,536 draws binned into 64 id ranges pass a
+    chi-square test; logp = -log V (batch rule) or log(1/V + 1e-10)."""
+    print(f"[case] all-equal row {dtype}", flush=True)
+    row = torch.full((V,), 0.37)
+    n = 65536
+    for rule, top_p, top_k in ((osm.RULE_BATCH, 0.9, 0), (osm.RULE_SINGLE, 1.0, 100), (osm.RULE_MIXIN, 0.5, 0)):
+        tok, lp = draws(gpu_device, row, n, temperature=1.0, top_p=top_p, top_k=top_k, rule=rule, dtype=dtype)
+        assert bool(((tok >= 0) & (tok < V)).all())
+        counts = torch.bincount(tok // 1024, minlength=64).double()
+        stat = float(((counts - n / 64) ** 2 / (n / 64)).sum())
+        assert stat < chi2.ppf(0.999, 63), (rule, stat)
+        want = -math.log(V) if rule == osm.RULE_BATCH else math.log(1.0 / V + 1e-10)
+        assert torch.allclose(lp, torch.full_like(lp, want), atol=1e-4), rule
 
 
 def test_token_sampler_api(gpu_device):
