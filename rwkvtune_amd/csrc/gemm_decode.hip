@@ -486,18 +486,27 @@ hipError_t launch_tile(int M, int count, const void* const* A, const void* const
 // 256 x 32, 64 x 64, 128 x 64; 4 to 16 waves) and block targets (1 to 512)
 // over the five launches of a 1.5B and a 7.2B decode layer at M = 32 .. 256,
 // cold weights (MI355X; the plans compared in one process, interleaved):
-//   * up to 32 rows a 32 x 32 tile (4 K groups): every block only streams
-//     weights, and the narrow tile gives twice the column tiles and half the dead
-//     activation rows; up to 64 rows 64 x 64 (8 waves, two K groups); above,
-//     128 x 64 (8 waves, one K group), which reads each weight tile once up to
-//     128 rows and halves the activation re-reads of a column tile: 10% faster
-//     than 64 x 64 for a 7.2B layer at 80-128 rows (144 -> 128 us at 80), the same
-//     for 1.5B, and 10-25% faster above 128 rows;
-//   * results the kernel writes itself (epilogue applied) split K only up to 32
-//     rows, to about 256 blocks: above that the reduction launch costs more than
-//     the split gains (1.5B layer at 40-64 rows: 86 -> 74-81 us without it);
-//   * partial planes (summed by the next row kernel, no reduction launch)
-//     split to about 512 blocks up to 128 rows and 256 above.
+//   * up to 32 rows a 32 x 32 tile (4 K groups) with K split to about 256
+//     blocks (summed by the reduction launch): every block only streams
+//     weights, and the narrow tile gives twice the column tiles and half the
+//     dead activation rows;
+//   * above 32 rows, results the kernel writes itself (epilogue applied) are
+//     not split (the reduction launch costs more than the split gains: 1.5B
+//     layer at 40-64 rows 86 -> 74-81 us without it), and their tile minimises
+//     ceil(blocks / CUs) x (BM + BN): the rounds of blocks a CU runs times the
+//     rows and columns each block streams per K step (a CU's loads, not the
+//     matrix cores, bound these launches); ties go to the smaller tile, which
+//     puts more blocks on the CUs.  Measured per launch (graph replays over the
+//     layers): a 1.5B layer's r/k/v + LoRA-down and FFN key launches at 40-64
+//     rows 16.2-17.3 -> 14.4-16.3 us (32 x 32 instead of 64 x 64), at 80-128
+//     rows 18.8-20.2 -> 16.8-17.6 us (64 x 64 instead of 128 x 64, which left
+//     half the CUs idle), unchanged above; a 7.2B layer keeps 64 x 64 up to 64
+//     rows and 128 x 64 up to 128 (its wider matrices fill the GPU), and at
+//     160 rows takes 64 x 64 (55.6 / 62.5 against 61.0 / 65.7 us);
+//   * partial planes (summed by the next row kernel, no reduction launch):
+//     64 x 64 up to 64 rows, 128 x 64 above (one row tile up to 128 rows, so
+//     each weight tile is read once), split to about 512 blocks up to 128 rows
+//     and 256 above.
 using TileNarrow = Tile<1, 1, 1, 1, 4, 4>;
 using TileDecode = Tile<2, 2, 1, 1, 4, 2>;
 using TileWide = Tile<4, 2, 1, 1, 4, 1>;
@@ -505,7 +514,40 @@ constexpr int kMinK = 512;
 
 enum TileKind { kNarrow, kDecode, kWide };
 
-TileKind tile_for(int M) { return M <= 32 ? kNarrow : (M <= 64 ? kDecode : kWide); }
+// compute units of the current device (queried once per device)
+int cu_count() {
+    static std::mutex mu;
+    static int cached[kMaxDevices] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    std::lock_guard<std::mutex> lock(mu);
+    if (cached[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+        cached[dev] = n;
+    }
+    return cached[dev];
+}
+
+TileKind tile_for(int M, bool partial, int count, const int* N) {
+    if (M <= 32) return kNarrow;
+    if (partial) return M <= 64 ? kDecode : kWide;
+    const int cus = cu_count();
+    const int bm[3] = {TileNarrow::BM, TileDecode::BM, TileWide::BM};
+    const int bn[3] = {TileNarrow::BN, TileDecode::BN, TileWide::BN};
+    TileKind best = kNarrow;
+    int64_t best_cost = -1;
+    for (int t = 0; t < 3; ++t) {
+        int64_t blocks = 0;
+        for (int i = 0; i < count; ++i) blocks += (int64_t)((N[i] + bn[t] - 1) / bn[t]) * ((M + bm[t] - 1) / bm[t]);
+        const int64_t cost = (blocks + cus - 1) / cus * (bm[t] + bn[t]);
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best = (TileKind)t;
+        }
+    }
+    return best;
+}
 
 int target_for(int M, bool partial) {
     if (partial) return M <= 128 ? 512 : 256;
@@ -514,7 +556,7 @@ int target_for(int M, bool partial) {
 
 Plan plan_for(int M, int count, const int* N, const int* K, bool partial) {
     const int target = target_for(M, partial);
-    switch (tile_for(M)) {
+    switch (tile_for(M, partial, count, N)) {
         case kNarrow: return make_plan(TileNarrow::BM, TileNarrow::BN, M, count, N, K, target, kMinK, 0);
         case kDecode: return make_plan(TileDecode::BM, TileDecode::BN, M, count, N, K, target, kMinK, 0);
         default: return make_plan(TileWide::BM, TileWide::BN, M, count, N, K, target, kMinK, 0);
@@ -525,7 +567,7 @@ hipError_t launch_for(int M, int count, const void* const* A, const void* const*
                       const int64_t* lda, const int64_t* ldc, const int* N, const int* K, const int* epi, float* ws,
                       hipStream_t st, int partial) {
     const Plan pl = plan_for(M, count, N, K, partial != 0);
-    switch (tile_for(M)) {
+    switch (tile_for(M, partial != 0, count, N)) {
         case kNarrow: return launch_tile<TileNarrow>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl, partial);
         case kDecode: return launch_tile<TileDecode>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl, partial);
         default: return launch_tile<TileWide>(M, count, A, B, C, lda, ldc, N, K, epi, ws, st, pl, partial);

@@ -35,7 +35,7 @@ def close(c, r):
     return bool(((c.float() - r).abs() <= tol).all())
 
 
-@pytest.mark.parametrize("M", [1, 20, 32, 33, 64, 100, 200, 256])
+@pytest.mark.parametrize("M", [1, 20, 32, 33, 48, 64, 80, 100, 128, 160, 200, 256])
 def test_grouped_gemm(gpu_device, M):
     """Shapes of the decode step (r/k/v, LoRA downs with tanh / sigmoid, FFN
     key with relu^2, FFN value, head slice) plus K tails (K % 64 != 0) and an
