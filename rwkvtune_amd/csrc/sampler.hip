@@ -550,7 +550,6 @@ struct HistShared {
     uint32_t h[kHist / 2];  // counter of value key u: half u & 1 of word u >> 1
     unsigned long long seg_m[kSegs];  // per segment: fixed-point mass and count
     uint32_t seg_c[kSegs];
-    uint16_t occ[kSegs];    // occupied segments, descending
     unsigned long long wm[kWMax];
     uint32_t wc[kWMax];
     unsigned long long r64[2];
@@ -615,6 +614,21 @@ __device__ __forceinline__ T row_sum16(T x) {
     }
     return x;
 }
+// maximum over the 64 lanes (NaNs ignored, as fmaxf does), in every lane: row
+// maxima by the row_sum16 partner pattern, then the four rows' from lanes 0, 16,
+// 32, 48
+__device__ __forceinline__ float wave_max16(float x) {
+    x = fmaxf(x, __builtin_amdgcn_update_dpp(x, x, 0x140, 0xf, 0xf, false));
+    x = fmaxf(x, __builtin_amdgcn_update_dpp(x, x, 0x141, 0xf, 0xf, false));
+    x = fmaxf(x, __builtin_amdgcn_update_dpp(x, x, 0x4e, 0xf, 0xf, false));
+    x = fmaxf(x, __builtin_amdgcn_update_dpp(x, x, 0xb1, 0xf, 0xf, false));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
 // inclusive scan over the 64 lanes in lane order: row scans by row_shr 1, 2, 4, 8,
 // then the totals of the rows below (read from lanes 15, 31, 47)
 template <typename T>
@@ -673,11 +687,11 @@ __device__ __forceinline__ void block_scan2(uint32_t& c, unsigned long long& m, 
     m += om;
 }
 
-// exclusive scan of a count in thread order
+// exclusive scan of a count in thread order (the caller makes sure no thread still
+// reads wc: in sample16_kernel at least two barriers separate it from block_scan2)
 __device__ __forceinline__ uint32_t block_excl_scan_u32(uint32_t v, HistShared& sh) {
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint32_t x = wave_incl_scan(v);
-    __syncthreads();  // earlier readers of wc
     if (lane == 63) sh.wc[w] = x;
     __syncthreads();
     uint32_t off = 0;
@@ -749,7 +763,7 @@ __global__ __launch_bounds__(kT) void sample16_kernel(
     const int vmax = max_valid_id < V - 1 ? max_valid_id : V - 1;
     uint32_t w[kVPT / 2];
     load_row16<LT>(logits + (size_t)row * ld, V, vmax, w);
-    {   // clear the counters (ordered before the atomics by the barriers of the maximum)
+    {   // clear the counters (ordered before the atomics by the barrier of the maximum)
         uint4* hz = reinterpret_cast<uint4*>(sh.h);
 #pragma unroll
         for (int i = 0; i < kHist / 2 / 4 / kT; ++i) hz[i * kT + tid] = make_uint4(0u, 0u, 0u, 0u);
@@ -761,7 +775,14 @@ __global__ __launch_bounds__(kT) void sample16_kernel(
         unpack2<LT>(w[i], a, b);
         mm = fmaxf(mm, fmaxf(a, b));
     }
-    const float mx = block_max_f(mm, &red);  // NaNs do not count here; their keys are found below
+    // row maximum (NaNs do not count here; their keys are found below); the
+    // barrier also orders the clearing of the counters before the atomics
+    mm = wave_max16(mm);
+    if (lane == 0) red.f[wv] = mm;
+    __syncthreads();
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) mx = fmaxf(mx, red.f[i]);
 #pragma unroll
     for (int i = 0; i < kVPT / 2; ++i) {
         const uint32_t ua = okey16(w[i] & 0xffffu), ub = okey16(w[i] >> 16);
@@ -770,70 +791,45 @@ __global__ __launch_bounds__(kT) void sample16_kernel(
     }
     __syncthreads();
 
-    // occupied segments, listed in descending key order (thread t checks segment
-    // kSegs - 1 - t); empty segments get zero totals here
-    const int my_seg = kSegs - 1 - tid;
-    {
-        const uint4* hw = reinterpret_cast<const uint4*>(sh.h) + my_seg * 8;  // its 32 words
-        uint32_t any = 0u;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint4 q4 = hw[i];
-            any |= q4.x | q4.y | q4.z | q4.w;
-        }
-        const bool occupied = any != 0u;
-        const unsigned long long bal = __ballot(occupied);
-        if (lane == 0) sh.wc[wv] = (uint32_t)__popcll(bal);
-        if (!occupied) {
-            sh.seg_c[my_seg] = 0u;
-            sh.seg_m[my_seg] = 0ull;
-        }
-        __syncthreads();
-        int off = 0;
-        for (int i = 0; i < wv; ++i) off += (int)sh.wc[i];
-        if (occupied)
-            sh.occ[off + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
-                                                        __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u))] =
-                (uint16_t)my_seg;
-    }
-    int n_occ = 0;
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) n_occ += (int)sh.wc[i];
-    __syncthreads();
-
-    // per-segment totals: a row of 16 lanes per occupied segment (four per wave in
-    // turn), four keys per lane.  q = exp((l - max) / T) = exp2((l - max) * log2(e) / T),
-    // with the reciprocal temperature (within an ulp of the division); the maximum
-    // gets exactly 1
+    // per-segment totals: segment 4 (16 i + wave) + row is summed by a row of 16
+    // lanes of the wave (four segments per wave and step, 16 steps), four keys per
+    // lane; a step whose four segments are empty writes zeros and skips the rest.
+    // q = exp((l - max) / T) = exp2((l - max) * log2(e) / T), with the reciprocal
+    // temperature (within an ulp of the division); the maximum gets exactly 1
     const float c1 = (temp != 1.0f ? 1.0f / temp : 1.0f) * 1.4426950408889634f;
     const uint32_t kpinf = key_pinf<LT>(), kninf = key_ninf<LT>();
+    const int my_seg = kSegs - 1 - tid;
     bool nan = false;
-    for (int base = 4 * wv; base < n_occ; base += 4 * kWaves) {  // wave-uniform
-        const int e = base + (lane >> 4);
+    {
         const int r = lane & 15;
-        uint32_t c = 0u, seg = 0u;
-        unsigned long long m = 0ull;
-        if (e < n_occ) {
-            seg = sh.occ[e];
+#pragma unroll 1
+        for (int i = 0; i < kSegs / (4 * kWaves); ++i) {
+            const uint32_t seg = (uint32_t)(4 * (kWaves * i + wv) + (lane >> 4));
+            // this lane's keys 64 seg + 4 r .. + 3: words 32 seg + 2 r, + 1
+            const uint2 wd = *reinterpret_cast<const uint2*>(&sh.h[32 * seg + 2 * r]);
+            uint32_t c = 0u;
+            unsigned long long m = 0ull;
+            if (__ballot((wd.x | wd.y) != 0u) != 0ull) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const uint32_t u = 64u * seg + 63u - (uint32_t)(4 * r + i);
-                const uint32_t n = hist_count(sh, u);
-                if (n != 0u) {
-                    if (u > kpinf || u < kninf) {
-                        nan = true;
-                    } else {
-                        c += n;
-                        m += (unsigned long long)n * fx_of_q(q_of_key<LT>(u, mx, c1));
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t n = ((e < 2 ? wd.x : wd.y) >> ((e & 1) * 16)) & 0xffffu;
+                    if (n != 0u) {
+                        const uint32_t u = 64u * seg + 4u * (uint32_t)r + (uint32_t)e;
+                        if (u > kpinf || u < kninf) {
+                            nan = true;
+                        } else {
+                            c += n;
+                            m += (unsigned long long)n * fx_of_q(q_of_key<LT>(u, mx, c1));
+                        }
                     }
                 }
+                c = row_sum16(c);
+                m = row_sum16(m);
             }
-        }
-        c = row_sum16(c);
-        m = row_sum16(m);
-        if (e < n_occ && r == 0) {
-            sh.seg_c[seg] = c;
-            sh.seg_m[seg] = m;
+            if (r == 0) {
+                sh.seg_c[seg] = c;
+                sh.seg_m[seg] = m;
+            }
         }
     }
     const bool any_nan = __syncthreads_or(nan);
@@ -877,8 +873,9 @@ __global__ __launch_bounds__(kT) void sample16_kernel(
             sh.r64[0] = exc_m;
         }
         walk_segment<LT, true>(sh, kk, mx, c1);
+        // (a walk's inputs and results are disjoint slots, and the next walk writes
+        // its results only after its first barrier: no barrier needed after this read)
         Wfx = sh.r64[1] + (unsigned long long)(uint32_t)sh.r32[3] * (uint32_t)sh.r32[4];
-        __syncthreads();
     }
     if (nucleus) {
         // the value whose inclusion crosses p of the kept mass: the running mass
@@ -895,7 +892,6 @@ __global__ __launch_bounds__(kT) void sample16_kernel(
         const unsigned long long above = sh.r64[1];
         const bool keep = rule != RULE_BATCH || above == 0ull;
         Wfx = keep ? above + (unsigned long long)(uint32_t)sh.r32[3] * (uint32_t)sh.r32[4] : above;
-        __syncthreads();
     }
 
     // the draw: a value by the integer inverse CDF over the kept prefix (target <
