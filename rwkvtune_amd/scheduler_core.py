@@ -14,7 +14,9 @@ One ``step_sync`` is one step of the reference's loop (``:250-299, 445-600,
 2. decode one token for every running sequence - one pooled single-token forward
    over their slots (rows addressed through the slot table, no gather / scatter
    of states) and one device sampler launch with each sequence's own
-   temperature / top_p / top_k / logit_bias (``TokenSampler.sample`` rules);
+   temperature / top_p / top_k / logit_bias (``TokenSampler.sample`` rules),
+   replayed as one captured graph per row bucket (rows with a logit_bias run
+   eagerly);
 3. prefill the next chunk (at most ``prefill_chunk_size`` tokens) of prefilling
    sequences under the ``max_batch_tokens`` budget, all chunks in one ragged
    forward (no grouping by length); a sequence whose prompt is complete draws its
