@@ -18,9 +18,11 @@ full-size rollouts with property checks.
   bit for bit: the decode GEMM's K-split plan depends on the row count, so the
   float32 summation order - and, at temperature 1 on random weights, the drawn
   tokens - can differ in the last bits.
-* Two 7.2B layers also decode 32, 64 and 96 rows: the three other plans of the
-  decode GEMM at C = 4096 (32 x 32 tile with split K and the reduction launch;
-  64 x 64; 128 x 64 over a partial row tile).
+* Two 7.2B layers also decode 32, 64, 96 and 160 rows, and two 1.5B layers 48
+  and 96: the other plans of the decode GEMM (32 x 32 tile with split K and the
+  reduction launch; 64 x 64; 128 x 64 over a partial row tile; at C = 4096 and
+  129-192 rows 64 x 64 over three row tiles; at C = 2048, 33-64 rows, 32 x 32
+  without split and, 65-128 rows, 64 x 64 for the launches with epilogues).
 * cfg5's model (RWKV-7 7.2B, all 32 layers) on a reduced rollout (8 prompts x
   2048 tokens, chunk 256): the same properties with 8 (twice) and 3 slots; and at
   its real slot count on the bench's own 128 x 2048-token prompts with the stop
@@ -65,7 +67,8 @@ def to_f64(states):
 
 @pytest.mark.parametrize("preset,rows,steps", [("rwkv7-1.5b", 256, 2), ("rwkv7-7.2b", 128, 1),
                                                ("rwkv7-7.2b", 32, 1), ("rwkv7-7.2b", 64, 1),
-                                               ("rwkv7-7.2b", 96, 1)])
+                                               ("rwkv7-7.2b", 96, 1), ("rwkv7-7.2b", 160, 1),
+                                               ("rwkv7-1.5b", 48, 1), ("rwkv7-1.5b", 96, 1)])
 def test_decode_layers_at_benchmark_shape(gpu_device, preset, rows, steps):
     print(f"[case] bf16 decode, two layers of {preset}, {rows} rows, {steps} steps", flush=True)
     cfg = config_from_preset(preset, n_layer=2, vocab_size=1000)
