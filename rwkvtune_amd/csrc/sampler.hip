@@ -42,12 +42,11 @@
 
 namespace {
 
-// sample_kernel and greedy_kernel: 1024 threads x 64 values
+// sample16_kernel, sample_kernel and greedy_kernel: 1024 threads x 64 values
 constexpr int kT = 1024;
 constexpr int kVPT = 64;  // values per thread
 constexpr int kTG = 1024, kVPTG = 64;
 constexpr int kWMax = 16;  // waves of the larger block
-constexpr int kBins = 1024;  // radix bins per level (one per thread)
 
 enum { RULE_BATCH = 0, RULE_SINGLE = 1, RULE_MIXIN = 2 };
 
