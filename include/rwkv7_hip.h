@@ -286,6 +286,33 @@ int rwkv7_gemm_decode_partials(int64_t M, const void *A, const void *B, int64_t 
 int64_t rwkv7_gemm_packed_elems(int N, int K);
 int rwkv7_gemm_pack(const void *B, int64_t ldb, int N, int K, void *out, void *stream);
 
+/*
+ * LM head for decode rows: logits[M, V] (bf16, row stride ldc) = A[M, K] . W^T
+ * with A bf16 row-major (row stride lda) and W the head weight [V][K] in the
+ * packed layout of rwkv7_head_pack, float32 accumulation rounded to bf16 once.
+ * V % 256 == 0, K % 64 == 0 and 256 <= K <= 65536; lda >= K and ldc >= V, both
+ * multiples of 8; A, the packed weight and the logits 16-byte aligned.  One
+ * block per 256 columns streams its rows of W once per row tile; rows are tiled
+ * by 64 (M <= 64) or 128, so any M works, but above 128 rows W is streamed
+ * once per 128 rows (a library GEMM with 256-row tiles is faster there).
+ * Replaces the head of the decode step, model.py:494-495 (self.head on the
+ * normalised last hidden state).
+ */
+int rwkv7_head_logits(int64_t M, int V, int K, const void *A, int64_t lda, const void *W_packed,
+                      void *logits, int64_t ldc, void *stream);
+
+/*
+ * Weight packing for rwkv7_head_logits: W [V][K] bf16 (row stride ldw, a
+ * multiple of 8, K % 64 == 0) into rwkv7_head_packed_elems(V, K) bf16
+ * elements: 64-row x 32-column pieces of 4 KB, piece (g, kt) at element
+ * (g * K/32 + kt) * 2048 holding rows 64 g .. 64 g + 63, columns 32 kt ..
+ * 32 kt + 31 row-major; rows past V zero.  Run once per weight (no counterpart
+ * in the reference: its head weight is read in place).
+ * rwkv7_head_packed_elems returns -1 on invalid sizes.
+ */
+int64_t rwkv7_head_packed_elems(int V, int K);
+int rwkv7_head_pack(const void *W, int64_t ldw, int V, int K, void *out, void *stream);
+
 /* ------------------------------------------------------------------------
  * Sampling
  * ------------------------------------------------------------------------ */

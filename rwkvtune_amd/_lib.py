@@ -57,6 +57,9 @@ SIGNATURES = {
     "rwkv7_gemm_decode_partials": (_I32, [_I64, _P, _P, _I64, _I32, _I32, _P, _I64, _P, _P]),
     "rwkv7_gemm_packed_elems": (_I64, [_I32, _I32]),
     "rwkv7_gemm_pack": (_I32, [_P, _I64, _I32, _I32, _P, _P]),
+    "rwkv7_head_logits": (_I32, [_I64, _I32, _I32, _P, _I64, _P, _P, _I64, _P]),
+    "rwkv7_head_packed_elems": (_I64, [_I32, _I32]),
+    "rwkv7_head_pack": (_I32, [_P, _I64, _I32, _I32, _P, _P]),
     "rwkv7_selective_log_softmax": (_I32, [_I32, _I64, _I64, _P, _I64, _P, _P, _P]),
 }
 

@@ -766,6 +766,55 @@ extern "C" int rwkv7_gemm_pack(const void* B, int64_t ldb, int N, int K, void* o
 }
 
 // ---------------------------------------------------------------------------
+// LM head for decode rows (head_gemm.hip)
+// ---------------------------------------------------------------------------
+
+int head_min_k();
+int head_row_tile(int M);
+int64_t head_packed_elems(int V, int K);
+hipError_t launch_head_logits(int M, int V, int K, const void* A, int64_t lda, const void* Bp, void* C, int64_t ldc,
+                              hipStream_t st);
+hipError_t launch_head_pack(const void* W, int64_t ldw, int V, int K, void* out, hipStream_t st);
+
+extern "C" int64_t rwkv7_head_packed_elems(int V, int K) {
+    if (V <= 0 || K <= 0 || (K % 64) != 0 || V > (1 << 24) || K > (1 << 16)) {
+        fail(RWKV7_ERR_INVALID, "rwkv7_head_packed_elems: 0 < V <= 2^24, 0 < K <= 65536, K %% 64 == 0 required "
+             "(V=%d K=%d)", V, K);
+        return -1;
+    }
+    ok();
+    return head_packed_elems(V, K);
+}
+
+extern "C" int rwkv7_head_pack(const void* W, int64_t ldw, int V, int K, void* out, void* stream) {
+    if (rwkv7_head_packed_elems(V, K) < 0) return RWKV7_ERR_INVALID;
+    if (!W || !out) return fail(RWKV7_ERR_INVALID, "rwkv7_head_pack: null pointer");
+    if (ldw < K || (ldw % 8) != 0 || ((((uintptr_t)W) | ((uintptr_t)out)) & 15))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_head_pack: ldw >= K, ldw %% 8 == 0 and 16-byte aligned buffers required");
+    return launch_status(launch_head_pack(W, ldw, V, K, out, (hipStream_t)stream), "head_pack_kernel");
+}
+
+extern "C" int rwkv7_head_logits(int64_t M, int V, int K, const void* A, int64_t lda, const void* W_packed,
+                                 void* logits, int64_t ldc, void* stream) {
+    if (M < 0 || M > kMaxInt)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_head_logits: 0 <= M <= 2^31 - 1 required (M=%lld)", (long long)M);
+    if (V <= 0 || (V % 256) != 0 || V > (1 << 24) || (K % 64) != 0 || K < head_min_k() || K > (1 << 16))
+        return fail(RWKV7_ERR_INVALID, "rwkv7_head_logits: V %% 256 == 0, K %% 64 == 0 and %d <= K <= 65536 required "
+                    "(V=%d K=%d)", head_min_k(), V, K);
+    if (M == 0) return ok();
+    if (!A || !W_packed || !logits) return fail(RWKV7_ERR_INVALID, "rwkv7_head_logits: null pointer");
+    if (lda < K || (lda % 8) != 0 || ldc < V || (ldc % 8) != 0)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_head_logits: lda >= K, ldc >= V, both multiples of 8 required");
+    if ((((uintptr_t)A) | ((uintptr_t)W_packed) | ((uintptr_t)logits)) & 15)
+        return fail(RWKV7_ERR_INVALID, "rwkv7_head_logits: A, the packed weight and the logits must be 16-byte "
+                    "aligned");
+    const int bm = head_row_tile((int)M);
+    if ((M + bm - 1) / bm > 65535) return fail(RWKV7_ERR_INVALID, "rwkv7_head_logits: too many rows");
+    return launch_status(launch_head_logits((int)M, V, K, A, lda, W_packed, logits, ldc, (hipStream_t)stream),
+                         "head_logits_kernel");
+}
+
+// ---------------------------------------------------------------------------
 // Selective log-softmax (logprob.hip)
 // ---------------------------------------------------------------------------
 

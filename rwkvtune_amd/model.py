@@ -289,6 +289,52 @@ class PackedWeight:
                   _lib.stream_of(self.t))
 
 
+class HeadPack:
+    """The head weight [V][K] (bf16) in the layout of ``rwkv7_head_pack``
+    (64-row x 32-column pieces of 4 KB), for ``rwkv7_head_logits``: the logits
+    of up to ``MAX_ROWS`` rows (decode steps, prefill's last tokens) in one
+    launch that streams the weight once.  Above that a library GEMM with
+    256-row tiles is faster (LM head 65,536 x 2,048, cold weights: 48-55 us
+    against 67-72 us for the library at 32-128 rows; 75 us for both at 192
+    rows; the library ahead at 256)."""
+
+    MAX_ROWS = 128
+
+    @staticmethod
+    def supported(weight: torch.Tensor) -> bool:
+        V, K = weight.shape
+        return (weight.dtype == torch.bfloat16 and weight.ndim == 2 and weight.is_cuda and V % 256 == 0
+                and K % 64 == 0 and 256 <= K <= 65536)
+
+    def __init__(self, weight: torch.Tensor):
+        if not self.supported(weight):
+            raise ValueError("HeadPack needs a bf16 [V][K] weight on the GPU with V % 256 == 0, K % 64 == 0, "
+                             "256 <= K <= 65536")
+        self.V, self.K = int(weight.shape[0]), int(weight.shape[1])
+        n = _lib.load().rwkv7_head_packed_elems(self.V, self.K)
+        if n < 0:
+            raise ValueError("rwkv7_head_packed_elems: " + _lib.load().rwkv7_last_error().decode())
+        self.t = torch.empty(n, dtype=torch.bfloat16, device=weight.device)
+        self.pack(weight)
+
+    def pack(self, weight: torch.Tensor):
+        """(Re)write the packed copy from ``weight`` (same shape) into the same buffer."""
+        if tuple(weight.shape) != (self.V, self.K):
+            raise ValueError(f"repack of a {self.V} x {self.K} head from {tuple(weight.shape)}")
+        w = weight if weight.stride(1) == 1 and weight.stride(0) % 8 == 0 and weight.data_ptr() % 16 == 0 \
+            else weight.contiguous()
+        _lib.call("rwkv7_head_pack", _lib.ptr(w), w.stride(0), self.V, self.K, _lib.ptr(self.t),
+                  _lib.stream_of(self.t))
+
+    def logits(self, x: torch.Tensor) -> torch.Tensor:
+        """x [M, K] bf16 (unit column stride) -> logits [M, V] bf16."""
+        M = x.shape[0]
+        out = torch.empty((M, self.V), dtype=torch.bfloat16, device=x.device)
+        _lib.call("rwkv7_head_logits", M, self.V, self.K, _lib.ptr(x), x.stride(0), _lib.ptr(self.t),
+                  _lib.ptr(out), out.stride(0), _lib.stream_of(x))
+        return out
+
+
 class _LayerPack:
     """float32 copies of one layer's per-channel parameters, laid out for the
     kernels, and (bf16 models) the packed decode-GEMM weights.  ``refresh``
@@ -393,6 +439,7 @@ class RWKV7Model(nn.Module):
         self.ln_out = nn.LayerNorm(config.n_embd)
         self.head = nn.Linear(config.n_embd, config.vocab_size, bias=False)
         self._packs = None
+        self._head_pack = None
         self._packs_key = None
         self._packs_struct = None
         # bumped whenever the packs are rebuilt (new buffers) or a parameter's
@@ -405,8 +452,12 @@ class RWKV7Model(nn.Module):
         # grouped MFMA GEMM over packed weights: r, k, v and the LoRA downs (tanh /
         # sigmoid fused) in one launch, the LoRA ups in one, the FFN key (relu^2
         # fused) and value, the output projection (split-K planes summed by the
-        # next row kernel); the head stays a library GEMM (faster there, measured)
+        # next row kernel)
         self.use_grouped_gemm = True
+        # logits of up to HeadPack.MAX_ROWS rows of a bf16 model on the library's
+        # head GEMM over a packed copy of the head weight (larger row counts and
+        # other dtypes: a library GEMM)
+        self.use_head_kernel = True
         # decode: output projection on the grouped GEMM's split-K planes (summed by
         # the next row kernel) instead of the library GEMM
         self.use_grouped_output = True
@@ -483,10 +534,15 @@ class RWKV7Model(nn.Module):
                     pk.refresh(b)
                 self._ln_out[0].copy_(self.ln_out.weight.detach().float())
                 self._ln_out[1].copy_(self.ln_out.bias.detach().float())
+                if self._head_pack is not None:
+                    self._head_pack.pack(self.head.weight.detach())
             else:
                 self._packs = [_LayerPack(b, C) for b in self.blocks]
                 self._ln_out = (self.ln_out.weight.detach().float().contiguous(),
                                 self.ln_out.bias.detach().float().contiguous())
+                self._head_pack = None
+                if HeadPack.supported(self.head.weight):
+                    self._head_pack = HeadPack(self.head.weight.detach())
                 self._packs_struct = self._struct_key()
                 self._packs_gen += 1
         if old is not None and [k[0] for k in key] != [k[0] for k in old]:
@@ -724,6 +780,15 @@ class RWKV7Model(nn.Module):
                   P(self._ln_out[0]), P(self._ln_out[1]), P(xo), st)
         if return_hidden:
             return xo
+        return self._head_logits(xo)
+
+    def _head_logits(self, xo: torch.Tensor) -> torch.Tensor:
+        """logits = head(xo) (model.py:494-495): the library's head GEMM over the
+        packed head for up to HeadPack.MAX_ROWS bf16 rows, a library GEMM otherwise."""
+        hp = self._head_pack
+        if (hp is not None and self.use_head_kernel and xo.shape[0] <= HeadPack.MAX_ROWS
+                and xo.dtype == torch.bfloat16 and xo.stride(1) == 1):
+            return hp.logits(xo)
         return self._lin(xo, self.head.weight)
 
     # -- reference-compatible entry points ------------------------------------
