@@ -2,7 +2,7 @@
 """Benchmark of rwkvtune's batched-generation hot path on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
-                    [--workload rollout|cfg5|scheduler|decode|prefill|tmix|gemm|logprob|train]
+                    [--workload rollout|cfg5|scheduler|decode|prefill|tmix|gemm|logprob|train|sampler]
 
 Prints ONE JSON line.  One GPU only: ``--gpus N`` with N > 1 exits with a message.
 
@@ -668,6 +668,68 @@ def cpu_baseline_decode(reps: int = 3):
                       f"mean of {reps}; {dt * 1e3:.1f} ms/step"}
 
 
+def head_sampler_leg(dev, M=256, reps=200, C=2048):
+    """One sampling step of the cfg4 rollout at M rows: the LM head as the model
+    computes it (the library's head GEMM over the packed head up to
+    HeadPack.MAX_ROWS rows, hipBLASLt above; [M, C] x [65536, C]^T bf16, two head
+    copies alternating so the 268 MB weight is not cache-resident, as in the
+    rollout where the layers' weights stream in between) and the sampler (greedy
+    launch + 16-bit sampling kernel, RULE_BATCH, temperature 1, top_p 0.95, ids
+    above 65529 banned), as graph replays; HIP events on the launch stream.  The
+    library GEMM's head time at the same M is reported beside it."""
+    import torch.nn.functional as F
+    from rwkvtune_amd import sampler as dsm
+    from rwkvtune_amd.model import HeadPack
+    V = 65536
+    g = torch.Generator(device=dev).manual_seed(11)
+    heads = [(torch.randn(V, C, generator=g, device=dev) * 0.02).to(torch.bfloat16) for _ in range(2)]
+    packs = [HeadPack(w) for w in heads]
+    xo = torch.randn(M, C, generator=g, device=dev).to(torch.bfloat16)
+    logits = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+    buf = dsm.SamplerBuffers(M, dev)
+    buf.set_uniform(1.0, 0.95, 0)
+    buf.rng_key.copy_(torch.arange(M, device=dev))
+    tok = torch.empty(M, dtype=torch.int64, device=dev)
+    lp = torch.empty(M, dtype=torch.float32, device=dev)
+
+    def head_lib(i):
+        torch.matmul(xo, heads[i % 2].t(), out=logits)
+
+    def head(i):
+        if M <= HeadPack.MAX_ROWS:
+            packs[i % 2].logits(xo, out=logits)
+        else:
+            head_lib(i)
+
+    def sample(i):
+        buf.rng_ctr.fill_(i)
+        dsm.sample_rows(logits, buf, rule=dsm.RULE_BATCH, max_valid_id=MAX_VALID_ID, seed=1, out_tok=tok,
+                        out_logp=lp)
+
+    res = {}
+    s = torch.cuda.Stream(dev)
+    for name, fns in (("head", (head,)), ("head_lib", (head_lib,)), ("sampler", (sample,)),
+                      ("step", (head, sample))):
+        with torch.cuda.stream(s):
+            for i in range(2):
+                for f in fns:
+                    f(i)
+            torch.cuda.synchronize(dev)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=s):
+                for i in range(20):
+                    for f in fns:
+                        f(i)
+            graph.replay()  # the first replay uploads the graph
+            torch.cuda.synchronize(dev)
+            res[name] = time_launches(lambda i: graph.replay(), reps // 20, s) / 20
+    wbytes = V * C * 2
+    return {"M": M, "head_us": res["head"], "head_lib_us": res["head_lib"], "sampler_us": res["sampler"],
+            "step_us": res["step"], "head_GBs": wbytes / (res["head"] * 1e-6) / 1e9, "logits_bytes": M * V * 2,
+            "tokens_per_s": M / (res["step"] * 1e-6), "head_kernel": M <= HeadPack.MAX_ROWS,
+            "valid": bool(((tok >= 0) & (tok <= MAX_VALID_ID)).all())}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -675,8 +737,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--workload", default="rollout",
                     choices=["rollout", "cfg5", "scheduler", "decode", "prefill", "tmix", "gemm", "logprob",
-                             "train"])
-    ap.add_argument("--rows", type=int, default=256, help="rows of the gemm workload")
+                             "train", "sampler"])
+    ap.add_argument("--rows", type=int, default=256, help="rows of the gemm and sampler workloads")
+    ap.add_argument("--embd", type=int, default=2048, help="head input width of the sampler workload (4096: 7.2B)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-cfg5", action="store_true", help="skip the 7.2B rollout leg of the default workload")
     a = ap.parse_args()
@@ -863,6 +926,25 @@ def main():
                          "kernel": gm["kernel"], "M": a.rows, "us_per_launch": gm["us_per_layer"] / 5,
                          "algorithmic_bytes": gm["weight_bytes_per_layer"] / 5},
             "cpu_baseline": None,
+        }
+    elif a.workload == "sampler":
+        # one sampling step at --rows rows: LM head + sampler (for kernel-trace runs)
+        reps = 200 if a.steps is None else a.steps
+        hs = head_sampler_leg(dev, M=a.rows, reps=reps, C=a.embd)
+        out = {
+            "metric": METRIC, "value": hs["tokens_per_s"], "unit": "sampled tokens/s", "n_gpus": 1, "steps": reps,
+            "warmup": 2, "ms_per_step": hs["step_us"] / 1e3, "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "bf16 head and logits, fp32 sampling", "data": "synthetic",
+            "config": {"workload": f"sampling step at {a.rows} rows: LM head [{a.rows}, {a.embd}] x "
+                                   f"[65536, {a.embd}]^T ({'head_logits_kernel' if hs['head_kernel'] else 'hipBLASLt'})"
+                                   " + sampler (RULE_BATCH, temperature 1, top_p 0.95)"},
+            "roofline": {"bound": "hbm", "achieved": hs["head_GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": hs["head_GBs"] / PEAK_HBM_GBS, "traffic": None,
+                         "kernel": "head_logits_kernel" if hs["head_kernel"] else "LM head GEMM (hipBLASLt)",
+                         "us_per_launch": hs["head_us"], "algorithmic_bytes": 65536 * a.embd * 2},
+            "head_us": hs["head_us"], "head_lib_us": hs["head_lib_us"], "sampler_us": hs["sampler_us"],
+            "step_us": hs["step_us"],
+            "draws_valid": hs["valid"], "cpu_baseline": None,
         }
     elif a.workload == "tmix":
         # the roofline kernel alone (for kernel-trace / PMC runs), then a plain copy of

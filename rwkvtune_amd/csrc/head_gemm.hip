@@ -18,8 +18,9 @@
 //     issues stage s + R into the slot stage s leaves, reads stage s + 1's
 //     operands into the second register set while stage s's products run; the
 //     last R stages are unrolled at compile time with their own wait counts;
-//   * the epilogue stages the bf16 tile in the (then idle) LDS ring and writes
-//     whole 16-byte row chunks.
+//   * the epilogue pairs neighbouring columns across lanes (one DPP swap) and
+//     stores 4 bytes per lane (16-byte chunks staged through LDS measured the
+//     same or slower).
 // MFMA operand layout (gfx950): lane l supplies row l%32 of A and of B, k =
 // 8*(l/32) .. +7; accumulator q of lane l is C[8*(q/4) + 4*(l/32) + q%4][l%32].
 #include <type_traits>
@@ -46,13 +47,11 @@ struct HeadTile {
     static constexpr int STAGE = LINES * 128;
     // direct loads (8 lines each) per wave per stage: LA of A, then LB of W
     static constexpr int LA = BM / 2 / 8 / NWAVE, LB = BN / 2 / 8 / NWAVE, PER = LA + LB;
-    static constexpr int LDT = BN + 8;  // bf16 per row of the epilogue's LDS tile (16-byte pad)
     static_assert(BN == 256, "one block per 256 columns");
     static_assert(LA * 16 * NWAVE == BM && LB * 16 * NWAVE == BN, "loads split evenly over the waves");
     static_assert(R % 2 == 0 && R >= 2 && R <= 6, "stage pairs in the main loop, tail unrolled up to 6");
     static_assert((R - 1) * PER < 64, "vmcnt holds at most 63 outstanding loads");
     static_assert(R * STAGE <= 160 * 1024, "LDS");
-    static_assert(BM * LDT * 2 <= R * STAGE, "the epilogue tile fits in the ring");
 };
 
 using TileM64 = HeadTile<1, 4, 2, 2, 6>;   // 64 x 256, 4 waves, 6 stages (120 KB)
@@ -219,30 +218,25 @@ __global__ __launch_bounds__(T::THREADS) void head_logits_kernel(int M, int K, c
         tail(std::integral_constant<int, 5>(), a1, b1, a0, b0);
     }
 
-    // epilogue: every wave is past its last LDS read (and every load has landed)
-    // once all reach the barrier; the ring then holds the block's bf16 tile
-    // [BM][LDT], written out as whole 16-byte chunks of the rows below M
-    __syncthreads();
-    bf16_t* tile = reinterpret_cast<bf16_t*>(ring);
+    // epilogue: lanes 2j and 2j + 1 hold columns 2j and 2j + 1 of the same rows;
+    // one swap of a register with the neighbour lane (DPP quad_perm 1,0,3,2)
+    // gives the even lane columns 2j..2j+1 of row r and the odd lane those of row
+    // r + 1, so each lane stores 4 bytes
+    const bool odd = lr & 1;
 #pragma unroll
     for (int a = 0; a < T::MS; ++a)
 #pragma unroll
         for (int b = 0; b < T::NS; ++b) {
-            const int col = wn + 32 * b + lr;
+            const int col = n0 + wn + 32 * b + (lr & ~1);
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const int row = wm + 32 * a + 8 * (q >> 2) + 4 * hi + (q & 3);
-                tile[row * T::LDT + col] = f32_to_bf16(acc[a][b][q]);
+            for (int q = 0; q < 16; q += 2) {
+                const uint32_t v0 = f32_to_bf16(acc[a][b][q]), v1 = f32_to_bf16(acc[a][b][q + 1]);
+                const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)(odd ? v0 : v1), 0xB1, 0xF, 0xF, false);
+                const uint32_t packed = odd ? (recv | (v1 << 16)) : (v0 | (recv << 16));
+                const int row = m0 + wm + 32 * a + 8 * (q >> 2) + 4 * hi + (q & 3) + (odd ? 1 : 0);
+                if (row < M) *reinterpret_cast<uint32_t*>(C + (int64_t)row * ldc + col) = packed;
             }
         }
-    __syncthreads();
-    constexpr int CPR = T::BN / 8;  // 16-byte chunks per row
-    const int rows = min(T::BM, M - m0);
-    for (int idx = threadIdx.x; idx < rows * CPR; idx += T::THREADS) {
-        const int r = idx / CPR, c = idx % CPR;
-        const uint4 v = *reinterpret_cast<const uint4*>(tile + r * T::LDT + 8 * c);
-        *reinterpret_cast<uint4*>(C + (int64_t)(m0 + r) * ldc + n0 + 8 * c) = v;
-    }
 }
 
 // W [V][K] (row stride ldw) -> [ceil(V/64)][K/32][64][32]; rows past V zero.

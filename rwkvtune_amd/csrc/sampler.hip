@@ -545,6 +545,51 @@ constexpr int kHist = 65536;
 
 constexpr int kSegs = kHist / 64;  // segments of 64 consecutive value keys
 
+// Greedy rows (temperature < 1e-6, core.py:80-83, 184-188): argmax of the banned
+// logits with the lowest index on ties, logp = log_softmax(banned logits)[token].
+// Thread t of the 1024-thread block takes elements j * 1024 + t.  Run by
+// sample16_kernel for its greedy rows and by greedy_kernel ahead of
+// sample_kernel (whose register footprint doubles when it shares a kernel with
+// this path).  Not inlined: the sampling path's registers stay its own.
+template <typename LT>
+__device__ __attribute__((noinline)) void greedy_row(int row, int V, const LT* __restrict__ lg, int max_valid_id,
+                                           int64_t* __restrict__ out_tok, float* __restrict__ out_logp, Red* red,
+                                           unsigned long long* red64) {
+    typedef io_traits<LT> tr;
+    const int tid = threadIdx.x;
+    const int vmax = max_valid_id < V - 1 ? max_valid_id : V - 1;
+    float x[kVPTG];
+#pragma unroll
+    for (int j = 0; j < kVPTG; ++j) {
+        const int i = j * kTG + tid;
+        const float v = tr::to_f32(lg[i < V ? i : V - 1]);  // unconditional load (see load_row)
+        x[j] = i <= vmax ? v : -INFINITY;
+    }
+    // padding is -inf at the highest indices, so it never wins a tie
+    unsigned long long best = 0;
+#pragma unroll
+    for (int j = 0; j < kVPTG; ++j) {
+        const unsigned i = (unsigned)(j * kTG + tid);
+        const unsigned long long c = ((unsigned long long)okey(x[j]) << 32) | (unsigned long long)(0xffffffffu - i);
+        best = c > best ? c : best;
+    }
+    best = block_max_u64(best, red64);
+    const int tok = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
+    float mm = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < kVPTG; ++j) mm = fmaxf(mm, x[j]);
+    const float mx = block_max_f(mm, red);
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < kVPTG; ++j) s += (x[j] == -INFINITY) ? 0.f : expf(x[j] - mx);
+    const float Z = block_sum_f(s, red);
+    if (tid == 0) {
+        out_tok[row] = tok;
+        // the argmax value is mx unless every logit is -inf / NaN
+        out_logp[row] = (mx == -INFINITY) ? -INFINITY : -logf(Z);
+    }
+}
+
 struct HistShared {
     uint32_t h[kHist / 2];  // counter of value key u: half u & 1 of word u >> 1
     unsigned long long seg_m[kSegs];  // per segment: fixed-point mass and count
@@ -758,7 +803,10 @@ __global__ __launch_bounds__(kT) void sample16_kernel(
     if (active != nullptr && active[row] == 0) return;  // whole block
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const float temp = temperature[row];
-    if (!(temp >= 1e-6f)) return;  // greedy rows belong to greedy_kernel
+    if (!(temp >= 1e-6f)) {  // greedy row (the counters' words serve as its reduction space)
+        greedy_row<LT>(row, V, logits + (size_t)row * ld, max_valid_id, out_tok, out_logp, &red, sh.wm);
+        return;
+    }
     const int vmax = max_valid_id < V - 1 ? max_valid_id : V - 1;
     uint32_t w[kVPT / 2];
     load_row16<LT>(logits + (size_t)row * ld, V, vmax, w);
@@ -1037,55 +1085,18 @@ __global__ __launch_bounds__(kT) void sample_kernel(
               fsum, &pick, sh, out_tok + row, out_logp + row);
 }
 
-// Greedy rows (temperature < 1e-6, core.py:80-83, 184-188): argmax of the banned
-// logits with the lowest index on ties, logp = log_softmax(banned logits)[token].
-// A kernel of its own: sharing one kernel with the sampling path doubles its
-// register footprint.
 template <typename LT>
 __global__ __launch_bounds__(kTG) void greedy_kernel(
     int M, int V, const LT* __restrict__ logits, int64_t ld, int max_valid_id,
     const float* __restrict__ temperature, const uint8_t* __restrict__ active,
     int64_t* __restrict__ out_tok, float* __restrict__ out_logp)
 {
-    typedef io_traits<LT> tr;
     __shared__ Red red;
     __shared__ unsigned long long red64[kWMax];
     const int row = blockIdx.x;
     if (active != nullptr && active[row] == 0) return;
     if (temperature[row] >= 1e-6f) return;  // sampled rows belong to sample_kernel
-    const int tid = threadIdx.x;
-    const LT* lg = logits + (size_t)row * ld;
-    const int vmax = max_valid_id < V - 1 ? max_valid_id : V - 1;
-    float x[kVPTG];
-#pragma unroll
-    for (int j = 0; j < kVPTG; ++j) {
-        const int i = j * kTG + tid;
-        const float v = tr::to_f32(lg[i < V ? i : V - 1]);  // unconditional load (see load_row)
-        x[j] = i <= vmax ? v : -INFINITY;
-    }
-    // padding is -inf at the highest indices, so it never wins a tie
-    unsigned long long best = 0;
-#pragma unroll
-    for (int j = 0; j < kVPTG; ++j) {
-        const unsigned i = (unsigned)(j * kTG + tid);
-        const unsigned long long c = ((unsigned long long)okey(x[j]) << 32) | (unsigned long long)(0xffffffffu - i);
-        best = c > best ? c : best;
-    }
-    best = block_max_u64(best, red64);
-    const int tok = (int)(0xffffffffu - (unsigned)(best & 0xffffffffull));
-    float mm = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < kVPTG; ++j) mm = fmaxf(mm, x[j]);
-    const float mx = block_max_f(mm, &red);
-    float s = 0.f;
-#pragma unroll
-    for (int j = 0; j < kVPTG; ++j) s += (x[j] == -INFINITY) ? 0.f : expf(x[j] - mx);
-    const float Z = block_sum_f(s, &red);
-    if (tid == 0) {
-        out_tok[row] = tok;
-        // the argmax value is mx unless every logit is -inf / NaN
-        out_logp[row] = (mx == -INFINITY) ? -INFINITY : -logf(Z);
-    }
+    greedy_row<LT>(row, V, logits + (size_t)row * ld, max_valid_id, out_tok, out_logp, &red, red64);
 }
 
 // Repetition penalty, in place, once per occurrence of each id in the row's
@@ -1134,18 +1145,18 @@ hipError_t launch_sample(int M, int V, const void* logits, int64_t ld, int rule,
                          const uint8_t* active, uint64_t seed, const int64_t* rng_key,
                          const int32_t* rng_ctr, int64_t* out_tok, float* out_logp, hipStream_t st)
 {
-    hipLaunchKernelGGL(greedy_kernel<LT>, dim3(M), dim3(kTG), 0, st, M, V, (const LT*)logits, ld, max_valid_id,
-                       temperature, active, out_tok, out_logp);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
     if constexpr (sizeof(LT) == 2) {
-        if (bias_off == nullptr) {
+        if (bias_off == nullptr) {  // one launch: sample16_kernel takes the greedy rows too
             hipLaunchKernelGGL(sample16_kernel<LT>, dim3(M), dim3(kT), 0, st, M, V, (const LT*)logits, ld, rule,
                                max_valid_id, temperature, top_p, top_k, active, seed, rng_key, rng_ctr, out_tok,
                                out_logp);
             return hipGetLastError();
         }
     }
+    hipLaunchKernelGGL(greedy_kernel<LT>, dim3(M), dim3(kTG), 0, st, M, V, (const LT*)logits, ld, max_valid_id,
+                       temperature, active, out_tok, out_logp);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
     hipLaunchKernelGGL(sample_kernel<LT>, dim3(M), dim3(kT), 0, st, M, V, (const LT*)logits, ld, rule,
                        max_valid_id, temperature, top_p, top_k, bias_off, bias_ids, bias_val, active, seed,
                        rng_key, rng_ctr, out_tok, out_logp);

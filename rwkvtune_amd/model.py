@@ -326,10 +326,12 @@ class HeadPack:
         _lib.call("rwkv7_head_pack", _lib.ptr(w), w.stride(0), self.V, self.K, _lib.ptr(self.t),
                   _lib.stream_of(self.t))
 
-    def logits(self, x: torch.Tensor) -> torch.Tensor:
-        """x [M, K] bf16 (unit column stride) -> logits [M, V] bf16."""
+    def logits(self, x: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """x [M, K] bf16 (unit column stride) -> logits [M, V] bf16 (into ``out``
+        if given: [M, >= V] bf16 with unit column stride)."""
         M = x.shape[0]
-        out = torch.empty((M, self.V), dtype=torch.bfloat16, device=x.device)
+        if out is None:
+            out = torch.empty((M, self.V), dtype=torch.bfloat16, device=x.device)
         _lib.call("rwkv7_head_logits", M, self.V, self.K, _lib.ptr(x), x.stride(0), _lib.ptr(self.t),
                   _lib.ptr(out), out.stride(0), _lib.stream_of(x))
         return out
