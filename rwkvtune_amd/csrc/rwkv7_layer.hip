@@ -249,9 +249,11 @@ __global__ __launch_bounds__(TH) void shift_mix_kernel(
     // Every operand is loaded up front - the row, the previous row (or the
     // slot's x_prev), the LayerNorm parameters and the mix coefficients - into
     // plain register arrays, so their latencies overlap.
-    // (with two chunks per thread in 1024-thread blocks - at most 128 registers -
-    // the mix coefficients are read at use instead: their registers would spill)
-    constexpr bool kPreMix = NV == 1 || TH < 1024;
+    // (1024-thread blocks read the mix coefficients at use instead: preloaded, 7
+    // mixes take 82 VGPRs, one block per CU; read at use, 62, two blocks per CU:
+    // C = 4096 at 16,384 prefill rows 474 -> 408 us, at 128 decode rows 8.8 ->
+    // 8.3 us; with two chunks per thread their registers would spill)
+    constexpr bool kPreMix = TH < 1024;
     constexpr int NVM = kPreMix ? NV : 1;
     const float* pp = prev_pool + (size_t)(slot < 0 ? 0 : slot) * C;
     f32x4 cur[NV], prv[NV], lw[NV], lb[NV], mu[NMIX][NVM];
