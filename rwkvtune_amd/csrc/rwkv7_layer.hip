@@ -246,17 +246,17 @@ __global__ __launch_bounds__(TH) void shift_mix_kernel(
         return a;
     };
 
-    // Every operand is loaded up front - the row, the previous row (or the
-    // slot's x_prev), the LayerNorm parameters and the mix coefficients - into
-    // plain register arrays, so their latencies overlap.
-    // (1024-thread blocks read the mix coefficients at use instead: preloaded, 7
-    // mixes take 82 VGPRs, one block per CU; read at use, 62, two blocks per CU:
-    // C = 4096 at 16,384 prefill rows 474 -> 408 us, at 128 decode rows 8.8 ->
-    // 8.3 us; with two chunks per thread their registers would spill)
-    constexpr bool kPreMix = TH < 1024;
-    constexpr int NVM = kPreMix ? NV : 1;
+    // The row, the previous row (or the slot's x_prev) and the LayerNorm
+    // parameters are loaded up front into plain register arrays, so their
+    // latencies overlap; the mix coefficients (L2-resident) are read at use.
+    // Preloading them too cost registers and blocks per CU: 7 mixes at 512
+    // threads 78 instead of 60 VGPRs (three blocks per CU instead of four; 7-mix
+    // launch at 256 decode rows 7.0 vs 6.8 us, at 69,568 prefill rows 785 vs 778
+    // us), at 1024 threads 82 instead of 62 (one block per CU instead of two;
+    // C = 4096 at 16,384 prefill rows 474 vs 408 us, at 128 decode rows 8.8 vs
+    // 8.3 us).
     const float* pp = prev_pool + (size_t)(slot < 0 ? 0 : slot) * C;
-    f32x4 cur[NV], prv[NV], lw[NV], lb[NV], mu[NMIX][NVM];
+    f32x4 cur[NV], prv[NV], lw[NV], lb[NV];
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         const int c = t + j * TH;
@@ -267,11 +267,6 @@ __global__ __launch_bounds__(TH) void shift_mix_kernel(
             prv[j] = resid(m - 1, e_prv, c);
         lw[j] = c < C4 ? *reinterpret_cast<const f32x4*>(ln_w + 4 * c) : z;
         lb[j] = c < C4 ? *reinterpret_cast<const f32x4*>(ln_b + 4 * c) : z;
-        if constexpr (kPreMix) {
-#pragma unroll
-            for (int q = 0; q < NMIX; ++q)
-                mu[q][j] = c < C4 ? *reinterpret_cast<const f32x4*>(mix + (size_t)q * C + 4 * c) : z;
-        }
     }
     // ln0 on the residual (layer 0); the previous row needs it too
     if (src.ln0_w != nullptr) ln_regs<NV, TH>(cur, prv, !first, C4, src.ln0_w, src.ln0_b, red);
@@ -292,9 +287,7 @@ __global__ __launch_bounds__(TH) void shift_mix_kernel(
             const f32x4 xx = prv[j] - x;
 #pragma unroll
             for (int q = 0; q < NMIX; ++q) {
-                f32x4 mq;
-                if constexpr (kPreMix) mq = mu[q][j];
-                else mq = *reinterpret_cast<const f32x4*>(mix + (size_t)q * C + 4 * c);
+                const f32x4 mq = *reinterpret_cast<const f32x4*>(mix + (size_t)q * C + 4 * c);
                 vec4io<IO>::store(out + ((size_t)q * M + m) * C + 4 * c, x + xx * mq);
             }
         }
