@@ -36,7 +36,8 @@ Every sequence's tokens depend only on its prompt state, the logits of its
 rows and its own (sequence, position) random stream, so results do not depend
 on slot assignment or polling cadence.  Float32 models give the same tokens for
 any slot count.  For 16-bit models the decode projections' plan (tile and K
-split of the packed-weight GEMM, and the library GEMM of the head) is chosen by
+split of the packed-weight GEMM; the head's own kernel and its row tile up to
+128 rows, a library GEMM above) is chosen by
 the step's row bucket, so float32 summation order, and with it a sampled token
 now and then, can differ between runs with different slot counts; runs of one
 configuration are bit-identical.
