@@ -346,3 +346,36 @@ def test_every_draw_is_written(gpu_device, rule):
             dsm.sample_rows(logits, buf, rule=rule, max_valid_id=65529, seed=5, out_tok=tok, out_logp=lp)
             bad += ((tok < 0) | (tok > 65529) | ~torch.isfinite(lp)).sum()
     assert int(bad) == 0, f"{int(bad)} draws unwritten or invalid"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_mixed_greedy_and_sampled_rows(gpu_device, dtype):
+    """One 16-bit launch with greedy rows (temperature 0) between sampled ones
+    (temperature 1, top_p 0.9): the greedy rows run the greedy path inside the
+    sampling kernel and equal the oracle's argmax (logp within 1e-4); every
+    sampled row's draw lies in the oracle's kept set; every row is written."""
+    print(f"[case] mixed greedy / sampled rows {dtype}", flush=True)
+    g = torch.Generator().manual_seed(33)
+    n = 64
+    logits = (torch.randn(n, V, generator=g) * 2).to(dtype)
+    d = logits.to(gpu_device)
+    buf = dsm.SamplerBuffers(n, gpu_device)
+    buf.set_uniform(1.0, 0.9, 0)
+    greedy = torch.arange(n) % 3 == 0
+    buf.temperature.copy_(torch.where(greedy, 0.0, 1.0).to(gpu_device))
+    buf.rng_key.copy_(torch.arange(n, dtype=torch.int64, device=gpu_device))
+    tok = torch.full((n,), -1, dtype=torch.int64, device=gpu_device)
+    lp = torch.full((n,), float("nan"), dtype=torch.float32, device=gpu_device)
+    dsm.sample_rows(d, buf, rule=osm.RULE_BATCH, max_valid_id=65529, seed=4, out_tok=tok, out_logp=lp)
+    torch.cuda.synchronize()
+    tok, lp = tok.cpu(), lp.cpu()
+    assert bool((tok >= 0).all()) and bool(torch.isfinite(lp).all())
+    for i in range(n):
+        row = logits[i].float()
+        if greedy[i]:
+            t, l = osm.greedy(row, max_valid_id=65529)
+            assert int(tok[i]) == t and abs(float(lp[i]) - l) < 1e-4, i
+        else:
+            dist = osm.distribution(row, temperature=1.0, top_p=0.9, top_k=0, max_valid_id=65529,
+                                    rule=osm.RULE_BATCH)
+            assert float(dist[int(tok[i])]) > 0, i
