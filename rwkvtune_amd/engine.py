@@ -19,10 +19,12 @@ Used by the drop-in front ends (``GRPOBatchGenerator``, ``SchedulerCore``,
    length), admits waiting ones into the freed slots by copying their prompt's
    state from the store (fork-on-admit: G generations of one prompt share one
    prefill) and packs the live slots into the leading rows.  A step runs the
-   smallest row bucket (multiples of 32 up to 256, then of 64 and 128) that
-   covers the live rows, so the projections, row kernels and head shrink as
-   the rollout drains; the host bounds the live rows by the sequences not yet
-   known to be finished.
+   smallest row bucket (8, 16, multiples of 32 up to 256, then of 64 and 128)
+   that covers the live rows, so the projections, row kernels and head shrink
+   as the rollout drains; the host bounds the live rows by the sequences not
+   yet known to be finished.  Below 32 rows every kernel runs the plan of 32
+   rows (in the projections the tile's rows past the bucket read a zero page),
+   so the 8- and 16-row steps give the 32-row step's results for their rows.
    Each bucket's step is captured once in a HIP graph and replayed; the graphs
    and every buffer they reference live in a decode context that is reused by
    later runs of the same configuration.  The host polls the
@@ -56,7 +58,7 @@ from .sampler import RULE_BATCH, RULE_SINGLE, SamplerBuffers, repetition_penalty
 
 C_NEXT, C_DONE, C_STEP, C_NADMIT, C_LIVE = 0, 1, 2, 3, 4
 
-ROW_BUCKETS = (32, 64, 96, 128, 160, 192, 224, 256, 320, 384, 448, 512, 640, 768, 896, 1024)
+ROW_BUCKETS = (8, 16, 32, 64, 96, 128, 160, 192, 224, 256, 320, 384, 448, 512, 640, 768, 896, 1024)
 
 
 def row_buckets(S: int):

@@ -244,3 +244,39 @@ def test_bf16_error_within_reference_bf16_path(gpu_device, shape, grouped):
     finally:
         m.use_grouped_gemm = False
     print(f"  worst ratio to the reference bf16 error: from fp64 {worst[0]:.2f}, from it {worst[1]:.2f}", flush=True)
+
+
+def test_small_row_buckets_match_32_rows(gpu_device):
+    """Decode steps of 8 and 16 rows (the rollout's smallest row buckets) give
+    bit-identical logits and states to the same rows of a 32-row step: below 32
+    rows the projections, the head and the row kernels run the 32-row plan (the
+    tile's rows past the step read a zero page).  bf16 model at the 1.5B width
+    (two layers, 65,536-token head), states from a random start; the slots past
+    the step keep their states."""
+    print("[case] 8 / 16-row decode steps against the 32-row step", flush=True)
+    cfg = config_from_preset("rwkv7-1.5b", n_layer=2)
+    m = build_model(cfg, dtype=torch.bfloat16, device="cuda", seed=31)
+    g = torch.Generator(device=gpu_device).manual_seed(32)
+    start = StatePool(cfg, 32, gpu_device)
+    start.kv.normal_(0.0, 0.1, generator=g)
+    start.att_x.normal_(generator=g)
+    start.ffn_x.normal_(generator=g)
+    tok = torch.randint(0, cfg.vocab_size, (32,), generator=g, device=gpu_device)
+    rows = torch.arange(32, dtype=torch.int32, device=gpu_device)
+
+    def step(M):
+        pool = StatePool(cfg, 32, gpu_device)
+        for name in ("kv", "att_x", "ffn_x"):
+            getattr(pool, name).copy_(getattr(start, name))
+        logits = m.forward_pooled(tok[:M], rows[:M], rows[:M], pool, decode=True)
+        torch.cuda.synchronize()
+        return logits, pool
+
+    l32, p32 = step(32)
+    for M in (16, 8):
+        lm, pm = step(M)
+        assert torch.equal(lm, l32[:M]), M
+        for name in ("kv", "att_x", "ffn_x"):
+            a, b, s0 = getattr(pm, name), getattr(p32, name), getattr(start, name)
+            assert torch.equal(a[:, :M], b[:, :M]), (M, name)
+            assert torch.equal(a[:, M:], s0[:, M:]), (M, name)
