@@ -61,7 +61,10 @@ The default line also carries:
 * ``roofline_rollout`` - the whole rollout decode step: algorithmic bytes (every
   decode weight once per step + each live row's state read and written) over the
   measured decode time;
-* ``wkv7_decode_cfg2`` / ``wkv7_prefill_cfg3`` - the stand-alone WKV kernels;
+* ``wkv7_decode_cfg2`` / ``wkv7_prefill_cfg3`` - the stand-alone WKV kernels; for the
+  prefill both the chunk algebra's contraction flops (``algorithmic_TFLOPs``,
+  ``algorithmic_frac``) and the bf16 part products the MFMAs execute
+  (``mfma_bf16_TFLOPs``, ``mfma_frac``: hi / lo operand splits, ~2.7x);
 * ``cfg5_rollout`` - one timed 7.2B rollout (the ``cfg5`` workload) after one warm-up
   (``--no-cfg5`` skips it).
 
@@ -814,8 +817,10 @@ def main():
             "roofline_rollout": rr,
             "cfg5_rollout": c5,
             "wkv7_decode_cfg2": {"GBs": wk["GBs"], "frac": wk["frac"], "us_per_step": wk["us_per_step"]},
-            "wkv7_prefill_cfg3": {k: pf[k] for k in ("us_per_launch", "tokens_per_s", "mfma_bf16_TFLOPs",
-                                                     "mfma_frac", "GBs", "hbm_frac", "speedup_vs_token_serial")},
+            "wkv7_prefill_cfg3": dict({k: pf[k] for k in ("us_per_launch", "tokens_per_s", "algorithmic_TFLOPs",
+                                                          "mfma_bf16_TFLOPs", "mfma_frac", "GBs", "hbm_frac",
+                                                          "speedup_vs_token_serial")},
+                                      algorithmic_frac=pf["algorithmic_TFLOPs"] / PEAK_BF16_TFLOPS),
             "cpu_baseline": cpu,
         }
     elif a.workload == "scheduler":
