@@ -246,15 +246,16 @@ def test_bf16_error_within_reference_bf16_path(gpu_device, shape, grouped):
     print(f"  worst ratio to the reference bf16 error: from fp64 {worst[0]:.2f}, from it {worst[1]:.2f}", flush=True)
 
 
-def test_small_row_buckets_match_32_rows(gpu_device):
+@pytest.mark.parametrize("preset,layers", [("rwkv7-1.5b", 2), ("rwkv7-7.2b", 1)])
+def test_small_row_buckets_match_32_rows(gpu_device, preset, layers):
     """Decode steps of 8 and 16 rows (the rollout's smallest row buckets) give
     bit-identical logits and states to the same rows of a 32-row step: below 32
     rows the projections, the head and the row kernels run the 32-row plan (the
-    tile's rows past the step read a zero page).  bf16 model at the 1.5B width
-    (two layers, 65,536-token head), states from a random start; the slots past
+    tile's rows past the step read a zero page).  bf16 models at the 1.5B and
+    7.2B widths (65,536-token head), states from a random start; the slots past
     the step keep their states."""
-    print("[case] 8 / 16-row decode steps against the 32-row step", flush=True)
-    cfg = config_from_preset("rwkv7-1.5b", n_layer=2)
+    print(f"[case] 8 / 16-row decode steps against the 32-row step, {preset}", flush=True)
+    cfg = config_from_preset(preset, n_layer=layers)
     m = build_model(cfg, dtype=torch.bfloat16, device="cuda", seed=31)
     g = torch.Generator(device=gpu_device).manual_seed(32)
     start = StatePool(cfg, 32, gpu_device)
