@@ -164,6 +164,22 @@ def gemm_pmc_traffic(path=os.path.join(ROOT, "profiles", "gemm_decode_m256_pmc.m
     return (float(m.group(1)) + float(m.group(2))) * 1e6 / 5
 
 
+def head_pmc_traffic(path=os.path.join(ROOT, "profiles", "head_logits_m128_pmc.md")):
+    """HBM bytes per head_logits_kernel launch at 128 rows (C = 2048) from the
+    committed rocprofv3 --pmc summary: its line 'Per launch: fabric reads R MB,
+    writes W MB' (FETCH_SIZE and WRITE_SIZE, each scaled by the counter's reading
+    for a plain copy of known size); or None."""
+    import re
+    try:
+        text = open(path).read()
+    except OSError:
+        return None
+    m = re.search(r"Per launch: fabric reads ([0-9.]+) MB, writes ([0-9.]+) MB", text)
+    if m is None:
+        return None
+    return (float(m.group(1)) + float(m.group(2))) * 1e6
+
+
 def copy_reference(dev, n_bytes=256 * 32 * 64 * 64 * 4, reps=8):
     """Plain device copy of a known size (the PMC counters' scale reference)."""
     n = n_bytes // 4
@@ -676,10 +692,10 @@ def head_sampler_leg(dev, M=256, reps=200, C=2048):
     computes it (the library's head GEMM over the packed head up to
     HeadPack.MAX_ROWS rows, hipBLASLt above; [M, C] x [65536, C]^T bf16, two head
     copies alternating so the 268 MB weight is not cache-resident, as in the
-    rollout where the layers' weights stream in between) and the sampler (greedy
-    launch + 16-bit sampling kernel, RULE_BATCH, temperature 1, top_p 0.95, ids
-    above 65529 banned), as graph replays; HIP events on the launch stream.  The
-    library GEMM's head time at the same M is reported beside it."""
+    rollout where the layers' weights stream in between) and the sampler (one
+    16-bit sampling launch, RULE_BATCH, temperature 1, top_p 0.95, ids above 65529
+    banned), as graph replays; HIP events on the launch stream.  The library
+    GEMM's head time at the same M is reported beside it."""
     import torch.nn.functional as F
     from rwkvtune_amd import sampler as dsm
     from rwkvtune_amd.model import HeadPack
@@ -935,6 +951,8 @@ def main():
         # one sampling step at --rows rows: LM head + sampler (for kernel-trace runs)
         reps = 200 if a.steps is None else a.steps
         hs = head_sampler_leg(dev, M=a.rows, reps=reps, C=a.embd)
+        copy_reference(dev)  # scales the PMC byte counters of the head profile
+        own_head = hs["head_kernel"] and a.rows == 128 and a.embd == 2048
         out = {
             "metric": METRIC, "value": hs["tokens_per_s"], "unit": "sampled tokens/s", "n_gpus": 1, "steps": reps,
             "warmup": 2, "ms_per_step": hs["step_us"] / 1e3, "higher_is_better": True, "scaling": "weak",
@@ -943,7 +961,8 @@ def main():
                                    f"[65536, {a.embd}]^T ({'head_logits_kernel' if hs['head_kernel'] else 'hipBLASLt'})"
                                    " + sampler (RULE_BATCH, temperature 1, top_p 0.95)"},
             "roofline": {"bound": "hbm", "achieved": hs["head_GBs"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                         "frac": hs["head_GBs"] / PEAK_HBM_GBS, "traffic": None,
+                         "frac": hs["head_GBs"] / PEAK_HBM_GBS,
+                         "traffic": head_pmc_traffic() if own_head else None,
                          "kernel": "head_logits_kernel" if hs["head_kernel"] else "LM head GEMM (hipBLASLt)",
                          "us_per_launch": hs["head_us"], "algorithmic_bytes": 65536 * a.embd * 2},
             "head_us": hs["head_us"], "head_lib_us": hs["head_lib_us"], "sampler_us": hs["sampler_us"],
